@@ -1,0 +1,247 @@
+"""Benchmark of the MatMulNBits hot path on one MI355X.
+
+Headline (``value``): achieved HBM GB/s of the int4 dequant-GEMV of the
+Llama-3-8B FFN up-projection decode (MatMulNBits fp16, M=1, K=4096, N=14336,
+block_size=32, no zero points). A step is one operator call on one batch of
+synthetic input that is already resident in HBM. Weight replicas rotate so the
+working set (>= 10 x 33 MB) exceeds the 256 MB Infinity Cache and every step
+reads its weights from HBM.
+
+The same JSON line also carries the prefill GEMM (M=2048, K=4096, N=14336,
+block_size=128, packed zero points, bias) in TFLOP/s, the fused Qkv and Mlp
+decode workloads in GB/s, the roofline of the dominant kernel and the CPU
+baseline (the NumPy oracle on this host's cores, a bounded sample).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
+FP16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, published
+
+
+def _gen_weights(torch, g, n, kb, blob, dev):
+    return torch.randint(0, 256, (n, kb, blob), dtype=torch.uint8, device=dev, generator=g)
+
+
+def _scales(torch, g, shape, dev):
+    return (torch.rand(shape, device=dev, generator=g) * 0.019 + 0.001).half()
+
+
+def make_replicas(torch, name, R, dev, seed):
+    """R independent weight sets of a workload, generated on the device."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    reps = []
+    if name == "decode_up_m1":
+        K, N, bs = 4096, 14336, 32
+        A = torch.randn((1, K), device=dev, generator=g).half()
+        for _ in range(R):
+            reps.append(dict(B=_gen_weights(torch, g, N, K // bs, bs // 2, dev), S=_scales(torch, g, (N, K // bs), dev)))
+        return dict(A=A, reps=reps, K=K, N=N, bs=bs)
+    if name == "prefill_m2048":
+        M, K, N, bs = 2048, 4096, 14336, 128
+        kb = K // bs
+        A = torch.randn((M, K), device=dev, generator=g).half()
+        for _ in range(R):
+            reps.append(dict(B=_gen_weights(torch, g, N, kb, bs // 2, dev), S=_scales(torch, g, (N, kb), dev),
+                             Z=torch.randint(0, 256, (N, (kb + 1) // 2), dtype=torch.uint8, device=dev, generator=g),
+                             bias=(torch.randn(N, device=dev, generator=g) * 0.01).half()))
+        return dict(A=A, reps=reps, K=K, N=N, bs=bs, M=M)
+    if name == "qkv_gqa_m4":
+        K, Nq, Nkv, bs = 4096, 4096, 1024, 64
+        kb = K // bs
+        A = torch.randn((4, K), device=dev, generator=g).half()
+        gamma = torch.ones(K, device=dev).half()
+        for _ in range(R):
+            r = {}
+            for p, n in (("q", Nq), ("k", Nkv), ("v", Nkv)):
+                r[p + "B"] = _gen_weights(torch, g, n, kb, bs // 2, dev)
+                r[p + "S"] = _scales(torch, g, (n, kb), dev)
+                r[p + "Z"] = torch.randint(0, 256, (n, (kb + 1) // 2), dtype=torch.uint8, device=dev, generator=g)
+            reps.append(r)
+        return dict(A=A, gamma=gamma, reps=reps, K=K, Nq=Nq, Nkv=Nkv, bs=bs)
+    if name == "mlp_swiglu_m16":
+        K, N, bs = 4096, 14336, 32
+        A = torch.randn((16, K), device=dev, generator=g).half()
+        for _ in range(R):
+            reps.append(dict(gB=_gen_weights(torch, g, N, K // bs, bs // 2, dev), gS=_scales(torch, g, (N, K // bs), dev),
+                             uB=_gen_weights(torch, g, N, K // bs, bs // 2, dev), uS=_scales(torch, g, (N, K // bs), dev)))
+        return dict(A=A, reps=reps, K=K, N=N, bs=bs)
+    raise KeyError(name)
+
+
+def step_fn(ops, name, w):
+    """A callable running step i on replica i % R (outputs preallocated)."""
+    torch = sys.modules["torch"]
+    reps, A = w["reps"], w["A"]
+    if name == "decode_up_m1":
+        Y = torch.empty((1, w["N"]), dtype=torch.float16, device=A.device)
+        return lambda i: ops.matmul_nbits(A, reps[i % len(reps)]["B"], reps[i % len(reps)]["S"], block_size=w["bs"], out=Y)
+    if name == "prefill_m2048":
+        Y = torch.empty((w["M"], w["N"]), dtype=torch.float16, device=A.device)
+
+        def f(i):
+            r = reps[i % len(reps)]
+            return ops.matmul_nbits(A, r["B"], r["S"], r["Z"], r["bias"], block_size=w["bs"], out=Y)
+        return f
+    if name == "qkv_gqa_m4":
+        def f(i):
+            r = reps[i % len(reps)]
+            return ops.matmul_nbits_qkv(A, r["qB"], r["qS"], r["kB"], r["kS"], r["vB"], r["vS"], norm_scale=w["gamma"],
+                                        block_size=w["bs"], q_zero_points=r["qZ"], k_zero_points=r["kZ"],
+                                        v_zero_points=r["vZ"], want_residual=False)
+        return f
+    if name == "mlp_swiglu_m16":
+        def f(i):
+            r = reps[i % len(reps)]
+            return ops.matmul_nbits_mlp(A, r["gB"], r["gS"], r["uB"], r["uS"], block_size=w["bs"])
+        return f
+    raise KeyError(name)
+
+
+def time_steps(torch, fn, steps, warmup):
+    """Average device time per step with HIP events on the launch stream."""
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(steps):
+        fn(warmup + i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / steps, wall / steps * 1e3
+
+
+def per_launch_percentiles(torch, fn, n, warmup):
+    """Per-launch event timing (p10/p50/p90 ms); each launch bracketed alone."""
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        fn(i)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i, (a, b) in enumerate(ev):
+        a.record(stream)
+        fn(i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    t = sorted(a.elapsed_time(b) for a, b in ev)
+    return t[len(t) // 10], t[len(t) // 2], t[(9 * len(t)) // 10]
+
+
+def cpu_baseline(budget_s: float = 20.0):
+    """The NumPy oracle on this host for the decode GEMV workload (bounded)."""
+    import numpy as np
+    from oracle import oracle as O
+    from xrgpu_amd import workloads
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:
+        threads = 1
+    w = workloads.make("decode_up_m1")
+    i, at = w["inputs"], w["attrs"]
+    O.matmul_nbits(i["aT"][:, :], i["bT"][:64], i["scalesT"][:64], K=at["K"], N=64, block_size=32)  # warm
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        O.matmul_nbits(i["aT"], i["bT"], i["scalesT"], K=at["K"], N=at["N"], block_size=32)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    gbs = workloads.algorithmic_bytes(w) / t / 1e9
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": int(threads), "kind": "port",
+            "sample": f"NumPy oracle (unpack + fp32 dequant + fp64 matvec), full decode GEMV "
+                      f"M=1 K=4096 N=14336, median of {len(times)} runs, {t * 1e3:.1f} ms/call; "
+                      f"BLAS threads={threads}, host cores={len(os.sched_getaffinity(0))}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--replicas", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build's hot path (MatMulNBits family) runs on a single device; "
+              "multi-GPU sharding is a design note only.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from xrgpu_amd import ops, workloads
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    results = {}
+    names = ["decode_up_m1", "prefill_m2048", "qkv_gqa_m4", "mlp_swiglu_m16"]
+    if args.only:
+        names = [n for n in names if n in args.only.split(",")]
+    for name in names:
+        R = args.replicas if name != "prefill_m2048" else 2
+        w = make_replicas(torch, name, R, dev, seed=hash(name) & 0xFFFF)
+        fn = step_fn(ops, name, w)
+        steps = args.steps if name != "prefill_m2048" else max(10, args.steps // 10)
+        ms, wall_ms = time_steps(torch, fn, steps, args.warmup)
+        p10, p50, p90 = per_launch_percentiles(torch, fn, min(100, steps), 5)
+        wl = workloads.make(name, scale_down=1) if name == "decode_up_m1" else None
+        results[name] = dict(ms=ms, wall_ms=wall_ms, p10=p10, p50=p50, p90=p90, steps=steps, replicas=R)
+        del w, fn, wl
+        torch.cuda.empty_cache()
+
+    out = {}
+    if "decode_up_m1" in results:
+        r = results["decode_up_m1"]
+        nbytes = 33_067_008
+        gbs = nbytes / (r["ms"] * 1e-3) / 1e9
+        out = {
+            "metric": "int4 GEMV µs + HBM GB/s (M=1,K=4096,N=14336); prefill TFLOP/s (M=2048)",
+            "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
+            "ms_per_step": round(r["ms"], 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f16 (int4 weights, fp32 accumulate)", "data": "synthetic",
+            "config": {"workload": "decode_up_m1: MatMulNBits M=1 K=4096 N=14336 bits=4 block_size=32 no zp, "
+                                   "Llama-3-8B FFN up-projection", "replicas": r["replicas"],
+                       "parallelism": "single GPU"},
+            "gemv_us": round(r["ms"] * 1e3, 3),
+            "gemv_us_per_launch_p10_p50_p90": [round(x * 1e3, 3) for x in (r["p10"], r["p50"], r["p90"])],
+            "host_wall_us_per_call": round(r["wall_ms"] * 1e3, 3),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "k_gemv_q4 (ZP none, 1 block per chunk, MatMul)", "bytes_per_launch": nbytes},
+        }
+    if "prefill_m2048" in results:
+        r = results["prefill_m2048"]
+        fl = 2 * 2048 * 4096 * 14336
+        tf = fl / (r["ms"] * 1e-3) / 1e12
+        out["prefill"] = {"workload": "prefill_m2048: MatMulNBits M=2048 K=4096 N=14336 bs=128 packed zp bias",
+                          "us": round(r["ms"] * 1e3, 2), "tflops": round(tf, 2),
+                          "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": FP16_PEAK_TFLOPS,
+                                       "unit": "TFLOP/s", "frac": round(tf / FP16_PEAK_TFLOPS, 4),
+                                       "flops_per_launch": fl}}
+    for name, nbytes in (("qkv_gqa_m4", 13_656_064), ("mlp_swiglu_m16", 66_650_112)):
+        if name in results:
+            r = results[name]
+            gbs = nbytes / (r["ms"] * 1e-3) / 1e9
+            out[name] = {"us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                         "bytes_per_launch": nbytes}
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,133 @@
+/* xrmm: MI355X (gfx950) MatMulNBits / MatMulNBitsQkv / MatMulNBitsMlp.
+ *
+ * C ABI of libxrmm.so. Plain pointers and sizes only. Every entry point
+ * returns XRMM_OK or an error class and leaves a thread-local message for
+ * xrmm_last_error().
+ *
+ * Error classes mirror the reference's two exception types
+ * (kernels/_shared/extended/planner.cpp, vulkan.cpp:105,115):
+ *   XRMM_EINVAL  <- std::invalid_argument (contract, shape, attribute problems)
+ *   XRMM_EDEVICE <- std::runtime_error    (device, timeout, GPU-side failures)
+ *
+ * dtype codes follow the order of xrgpu::operators::DType
+ * (runtime/include/xrgpu/operators.h:9).
+ */
+#ifndef XRMM_H
+#define XRMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  XRMM_OK = 0,
+  XRMM_EINVAL = 1,
+  XRMM_EDEVICE = 2,
+};
+
+/* runtime/include/xrgpu/operators.h:9 enum class DType */
+enum {
+  XRMM_F32 = 0,
+  XRMM_F16 = 1,
+  XRMM_I32 = 2,
+  XRMM_U32 = 3,
+  XRMM_I16 = 4,
+  XRMM_I8 = 5,
+  XRMM_U8 = 6,
+  XRMM_I64 = 7,
+  XRMM_BOOL = 8,
+  XRMM_UNSPECIFIED = 9,
+};
+
+/* Fused activation kinds of MatMulNBitsMlp; the codes are those of
+ * activation_lower (kernels/_shared/extended/complex_plan.cpp:55). */
+enum {
+  XRMM_ACT_NONE = 0,
+  XRMM_ACT_RELU = 1,
+  XRMM_ACT_SILU = 2,
+  XRMM_ACT_GELU = 3,
+  XRMM_ACT_TANH = 4,
+  XRMM_ACT_SIGMOID = 5,
+  XRMM_ACT_SWIGLU = 6, /* passes the gate value through, as the shader does */
+};
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* xrmm_last_error(void);
+
+/* Library version string. */
+const char* xrmm_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Zero-copy entry points: every tensor pointer is a DEVICE pointer of the
+ * current HIP device, contiguous row-major; `stream` is a hipStream_t (NULL =
+ * the null stream). They enqueue work and return without synchronising.
+ *
+ * Zero points (`zp_dtype`):
+ *   XRMM_UNSPECIFIED  absent: z = 2^(bits-1)
+ *   XRMM_F32/XRMM_F16 float zero points [N, ceil(K/block_size)] (reference T3)
+ *   XRMM_U8           packed uint8 [N, ceil(ceil(K/block_size)*bits/8)],
+ *                     low-first (ONNX Runtime layout; an extension)
+ * `dtype` is T1 (XRMM_F32 or XRMM_F16): the type of A, scales, bias, outputs.
+ * ------------------------------------------------------------------------- */
+
+/* com.microsoft.MatMulNBits, opcode 1025.
+ * Replaces the serial packedMatmul path of
+ * kernels/_shared/extended/shaders/complex_kernel.glsl:80,83 as planned by
+ * kernels/_shared/extended/complex_plan.cpp:117-120 (inputs
+ * aT,bT,scalesT,zeroPointsT?,biasT?; output yT = aT.shape[:-1]+[N]).
+ * A [M,K], B [N,kb,blob] u8, scales [N,kb], bias [N] or NULL, Y [M,N]. */
+int xrmm_matmul_nbits(const void* A, const void* B, const void* scales, const void* zero_points,
+                      int32_t zp_dtype, const void* bias, void* Y, int64_t M, int64_t K,
+                      int64_t N, int32_t bits, int32_t block_size, int32_t dtype, void* stream);
+
+/* com.microsoft.MatMulNBitsQkv, opcode 1028 (complex_kernel.glsl:81,83;
+ * complex_plan.cpp:37,119). x = RMSNorm(A + skip) * norm_scale (eps), then
+ * Q = x Wq^T [M,Nq], K = x Wk^T [M,Nkv], V = x Wv^T [M,Nkv]; residual
+ * (A + skip, [M,K]) is written when non-NULL. skip may be NULL. The three
+ * zero-point pointers are an extension (NULL = implicit midpoint) and share
+ * `zp_dtype`. */
+int xrmm_matmul_nbits_qkv(const void* A, const void* skip, const void* norm_scale,
+                          const void* q_B, const void* q_scales, const void* q_zero_points,
+                          const void* k_B, const void* k_scales, const void* k_zero_points,
+                          const void* v_B, const void* v_scales, const void* v_zero_points,
+                          int32_t zp_dtype, void* Q, void* Kout, void* V, void* residual,
+                          int64_t M, int64_t K, int64_t Nq, int64_t Nkv, int32_t bits,
+                          int32_t block_size, float epsilon, int32_t dtype, void* stream);
+
+/* com.microsoft.MatMulNBitsMlp, opcode 1027 (complex_kernel.glsl:39-47,81,83;
+ * complex_plan.cpp:36,55,118). x = A + skip, RMS-normalised by norm_scale when
+ * that is non-NULL; Y = act(x Wg^T + gate_bias) * (x Wu^T + up_bias) [M,N];
+ * residual (A + skip) is written when non-NULL. Zero points are an extension
+ * (NULL = implicit midpoint). */
+int xrmm_matmul_nbits_mlp(const void* A, const void* skip, const void* norm_scale,
+                          const void* gate_B, const void* gate_scales, const void* gate_zero_points,
+                          const void* gate_bias, const void* up_B, const void* up_scales,
+                          const void* up_zero_points, const void* up_bias, int32_t zp_dtype,
+                          void* Y, void* residual, int64_t M, int64_t K, int64_t N, int32_t bits,
+                          int32_t block_size, float epsilon, int32_t activation, int32_t dtype,
+                          void* stream);
+
+/* Dequantized weights W [N,K] (nbitWeight, complex_kernel.glsl:80) in
+ * `out_dtype`: XRMM_F32 gives the reference value (float(code) - z) * scale;
+ * XRMM_F16 gives that value rounded once to binary16, produced by the same
+ * device dequantisation routine the fp16 GEMV/GEMM kernels use. `scale_dtype`
+ * is the dtype of `scales`. The reference has no standalone dequantisation
+ * entry; this one exposes the kernels' weight staging for bit-exact checks. */
+int xrmm_dequantize(const void* B, const void* scales, const void* zero_points, int32_t zp_dtype,
+                    void* W, int64_t N, int64_t K, int32_t bits, int32_t block_size,
+                    int32_t scale_dtype, int32_t out_dtype, void* stream);
+
+/* Name of the kernel the dispatcher picks for a MatMulNBits call of this
+ * geometry ("gemv_q4_mfma", "gemm_q4_mfma", "generic", ...), without touching
+ * the device. Returns a static string; NULL with XRMM_EINVAL set on a bad
+ * geometry. */
+const char* xrmm_select_kernel(int32_t op, int64_t M, int64_t K, int64_t N, int32_t bits,
+                               int32_t block_size, int32_t dtype, int32_t zp_dtype);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XRMM_H */

@@ -1,0 +1,63 @@
+"""C-ABI checks that run without a GPU: the library loads, exports every symbol
+include/xrmm.h declares, and rejects invalid geometry before touching a device."""
+import ctypes
+
+import pytest
+
+from xrgpu_amd import _native as nat
+
+
+def test_library_exports_every_declared_symbol():
+    lib = nat.lib()
+    declared = nat.declared_symbols()
+    assert len(declared) >= 7
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_version():
+    assert b"gfx950" in nat.lib().xrmm_version()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(bits=3), "bits"),
+    (dict(block_size=0), "block_size"),
+    (dict(K=0), "K must be positive"),
+    (dict(N=0), "N required"),
+    (dict(dtype=nat.I32), "T1"),
+    (dict(zp_dtype=nat.I32), "zero points"),
+])
+def test_invalid_geometry_is_einval(kw, msg):
+    args = dict(M=0, K=64, N=8, bits=4, block_size=32, dtype=nat.F16, zp_dtype=nat.UNSPECIFIED)
+    args.update(kw)
+    rc = nat.lib().xrmm_matmul_nbits(None, None, None, None, args["zp_dtype"], None, None, args["M"], args["K"],
+                                     args["N"], args["bits"], args["block_size"], args["dtype"], None)
+    assert rc == nat.XRMM_EINVAL
+    assert msg in nat.last_error()
+
+
+def test_empty_m_is_a_no_op_without_device():
+    # M = 0 (fixture empty_zero_dim): nothing to launch, returns OK
+    rc = nat.lib().xrmm_matmul_nbits(None, None, None, None, nat.UNSPECIFIED, None, None, 0, 32, 4, 4, 32,
+                                     nat.F32, None)
+    assert rc == nat.XRMM_OK and nat.last_error() == ""
+
+
+def test_qkv_requires_norm_scale():
+    rc = nat.lib().xrmm_matmul_nbits_qkv(*([None] * 12), nat.UNSPECIFIED, None, None, None, None, 0, 64, 8, 8, 4, 32,
+                                         ctypes.c_float(1e-6), nat.F16, None)
+    assert rc == nat.XRMM_EINVAL and "normScaleT" in nat.last_error()
+
+
+@pytest.mark.parametrize("op,M,K,N,bs,dtype,zp,expect", [
+    (0, 1, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),
+    (0, 2048, 4096, 14336, 128, nat.F16, nat.U8, "gemm_q4_mfma"),
+    (1, 4, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_mfma"),
+    (2, 16, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),
+    (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "generic"),
+    (0, 1, 33, 8, 32, nat.F16, nat.UNSPECIFIED, "generic"),
+    (0, 4, 64, 8, 8, nat.F16, nat.UNSPECIFIED, "generic"),
+])
+def test_kernel_selection(op, M, K, N, bs, dtype, zp, expect):
+    r = nat.lib().xrmm_select_kernel(op, M, K, N, 4, bs, dtype, zp)
+    assert r.decode() == expect

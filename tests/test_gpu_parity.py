@@ -1,0 +1,365 @@
+"""GPU parity: HIP kernels of libxrmm against the oracle on the same seeded inputs.
+
+Bars: dequantized weights and nibble unpacking bit-exact; outputs within
+max|d| <= 1e-2*max|Y_ref| for fp16 and 1e-5*max|Y_ref| for fp32
+(``oracle.tolerance_ok``); golden fixtures also meet their own atol/rtol.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests import fixture_util as F
+from xrgpu_amd import workloads
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev(x):
+    return None if x is None else torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def host(t):
+    return None if t is None else t.detach().cpu().numpy()
+
+
+def ops():
+    from xrgpu_amd import ops as _ops
+    return _ops
+
+
+def rand_case(rng, M, K, N, bits, bs, dtype, zp, bias=False, scale_lo=0.001, scale_hi=0.02):
+    kb = O.k_blocks(K, bs)
+    A = rng.standard_normal((M, K)).astype(dtype)
+    B = rng.integers(0, 256, size=(N, kb, O.blob_bytes(bs, bits)), dtype=np.uint8)
+    S = rng.uniform(scale_lo, scale_hi, (N, kb)).astype(dtype)
+    Z = None
+    if zp == "packed":
+        Z = rng.integers(0, 256, size=(N, O.packed_zp_bytes(kb, bits)), dtype=np.uint8)
+    elif zp == "float_int":
+        Z = rng.integers(0, 1 << bits, size=(N, kb)).astype(dtype)
+    elif zp == "float":
+        Z = rng.uniform(0, (1 << bits) - 1, (N, kb)).astype(dtype)
+    b = (rng.standard_normal(N) * 0.1).astype(dtype) if bias else None
+    return A, B, S, Z, b
+
+
+def assert_parity(actual, expected, dtype, what=""):
+    ok, err, lim = O.tolerance_ok(actual, expected, dtype)
+    assert ok, f"{what}: max|d|={err} > {lim}"
+
+
+# --------------------------------------------------------------------------- dequantisation
+
+@pytest.mark.parametrize("bs", [16, 32, 48, 64, 128])
+@pytest.mark.parametrize("zp", [None, "packed", "float_int", "float"])
+def test_dequantize_f16_bit_exact(gpu, bs, zp):
+    rng = np.random.default_rng(bs * 7 + len(zp or ""))
+    K, N = 4 * bs, 37
+    _, B, S, Z, _ = rand_case(rng, 1, K, N, 4, bs, np.float16, zp, scale_lo=1e-7, scale_hi=4.0)
+    W = host(ops().dequantize(dev(B), dev(S), dev(Z), K=K, block_size=bs, out_dtype=torch.float16))
+    ref = O.dequantize(B, S, Z, K, 4, bs, stage="f16")
+    assert np.array_equal(W.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("bits,bs,K", [(4, 32, 128), (2, 16, 80), (8, 32, 70), (4, 8, 24)])
+@pytest.mark.parametrize("zp", [None, "packed", "float"])
+def test_dequantize_f32_bit_exact(gpu, bits, bs, K, zp):
+    rng = np.random.default_rng(bits * 31 + bs + K)
+    _, B, S, Z, _ = rand_case(rng, 1, K, 19, bits, bs, np.float32, zp)
+    W = host(ops().dequantize(dev(B), dev(S), dev(Z), K=K, bits=bits, block_size=bs, out_dtype=torch.float32))
+    ref = O.dequantize(B, S, Z, K, bits, bs, stage="f32")
+    assert np.array_equal(W.view(np.uint32), ref.view(np.uint32))
+
+
+# --------------------------------------------------------------------------- MatMulNBits
+
+FAST_CASES = [
+    # M, K, N, bs, zp, bias
+    (1, 256, 64, 32, None, False),
+    (1, 512, 50, 32, "packed", True),
+    (2, 256, 33, 16, "packed", False),
+    (4, 1024, 96, 64, "packed", True),
+    (7, 384, 48, 128, None, True),
+    (16, 512, 80, 32, "float_int", False),
+    (16, 288, 17, 32, None, True),       # K tail inside the last block (K % bs != 0)
+    (3, 256, 40, 48, "packed", False),   # 16-code half blocks
+]
+
+
+@pytest.mark.parametrize("M,K,N,bs,zp,bias", FAST_CASES)
+def test_gemv_fp16_parity(gpu, M, K, N, bs, zp, bias):
+    rng = np.random.default_rng(M * 1000 + K + N + bs)
+    A, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, np.float16, zp, bias)
+    assert ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16,
+                               None if zp is None else ("packed" if zp == "packed" else "float")) == "gemv_q4_mfma"
+    Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
+    ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs)
+    assert_parity(Y, ref, np.float16)
+
+
+GEMM_CASES = [
+    (17, 256, 64, 32, None, False),
+    (64, 512, 130, 32, "packed", True),
+    (200, 1024, 256, 128, "packed", True),
+    (129, 320, 100, 64, None, False),
+    (96, 288, 40, 32, "packed", True),   # K tail
+]
+
+
+@pytest.mark.parametrize("M,K,N,bs,zp,bias", GEMM_CASES)
+def test_gemm_fp16_parity(gpu, M, K, N, bs, zp, bias):
+    rng = np.random.default_rng(M * 7 + K + N + bs)
+    A, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, np.float16, zp, bias)
+    assert ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16,
+                               None if zp is None else "packed") == "gemm_q4_mfma"
+    Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
+    ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs)
+    assert_parity(Y, ref, np.float16)
+
+
+GENERIC_CASES = [
+    # M, K, N, bits, bs, dtype, zp, bias
+    (1, 2048, 64, 4, 32, np.float32, "packed", False),
+    (3, 70, 9, 4, 32, np.float32, "float", True),
+    (2, 33, 5, 2, 16, np.float32, None, True),
+    (5, 40, 7, 8, 16, np.float16, "packed", False),
+    (4, 24, 6, 4, 8, np.float16, None, True),
+    (20, 100, 11, 8, 32, np.float32, "float", True),
+    (2, 17, 2, 4, 16, np.float16, "float", True),
+]
+
+
+@pytest.mark.parametrize("M,K,N,bits,bs,dtype,zp,bias", GENERIC_CASES)
+def test_generic_parity(gpu, M, K, N, bits, bs, dtype, zp, bias):
+    rng = np.random.default_rng(M + K + N + bits + bs)
+    A, B, S, Z, b = rand_case(rng, M, K, N, bits, bs, dtype, zp, bias)
+    Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, bits=bits, block_size=bs))
+    ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, bits=bits, block_size=bs)
+    assert_parity(Y, ref, dtype)
+
+
+def test_rank3_activation_folds_leading_axes(gpu):
+    rng = np.random.default_rng(5)
+    A, B, S, Z, b = rand_case(rng, 6, 256, 32, 4, 32, np.float16, "packed", True)
+    A3 = A.reshape(2, 3, 256)
+    Y = host(ops().matmul_nbits(dev(A3), dev(B), dev(S), dev(Z), dev(b), block_size=32))
+    assert Y.shape == (2, 3, 32)
+    assert_parity(Y, O.matmul_nbits(A3, B, S, Z, b, K=256, N=32, block_size=32), np.float16)
+
+
+# --------------------------------------------------------------------------- golden fixtures
+
+MNB = "com.microsoft.MatMulNBits"
+
+
+def run_mnb_fixture(case, ins):
+    at = case["attrs"]
+    return host(ops().matmul_nbits(dev(ins["aT"]), dev(ins["bT"]), dev(ins["scalesT"]), dev(ins.get("zeroPointsT")),
+                                   dev(ins.get("biasT")), K=at["K"], N=at["N"], bits=at.get("bits", 4),
+                                   block_size=at["block_size"]))
+
+
+@pytest.mark.parametrize("name", ["q4_block512_schema_legal_cpu_provider_gap_exact", "empty_zero_dim",
+                                  "empty_zero_dim_f16"])
+def test_fixture_explicit_outputs(gpu, name):
+    case = F.find(MNB, name)
+    y = run_mnb_fixture(case, F.case_inputs(case))
+    exp = F.materialize(case["outputs"]["yT"])
+    assert y.shape == exp.shape and y.dtype == exp.dtype
+    assert F.reference_compare(y, exp, *F.case_tolerance(case, "yT"))
+
+
+@pytest.mark.parametrize("name", ["ort_f16_large_k_accumulator_cancellation_m1_k8192_n8",
+                                  "ort_f16_large_k_accumulator_cancellation_m8_k8192_n8",
+                                  "f16_full_k_accumulator_cancellation_prefill_m64_k4096_n64"])
+def test_fixture_accumulator_cancellation_exact_zero(gpu, name):
+    case = F.find(MNB, name)
+    y = run_mnb_fixture(case, F.case_inputs(case))
+    assert y.dtype == np.float16 and np.all(y == 0), np.abs(y).max()
+
+
+def test_fixture_shapes_with_oracle(gpu):
+    """Every MatMulNBits fixture case of the reference, with its own shapes,
+    attributes and data where materialisable (seeded substitutes for the
+    upstream-only fillFloat32 generator), against the oracle."""
+    ran = 0
+    for case in F.load_cases():
+        if case["operation"] != MNB:
+            continue
+        at = case["attrs"]
+        ins = F.case_inputs(case, substitute=True)
+        if any(v.size > 8_000_000 for v in ins.values()):
+            continue
+        y = run_mnb_fixture(case, ins)
+        ref = O.matmul_nbits(ins["aT"], ins["bT"], ins["scalesT"], ins.get("zeroPointsT"), ins.get("biasT"),
+                             K=at["K"], N=at["N"], bits=at.get("bits", 4), block_size=at["block_size"])
+        assert_parity(y, ref, ref.dtype, case["name"])
+        ran += 1
+    assert ran >= 60
+
+
+# --------------------------------------------------------------------------- Qkv / Mlp
+
+QKV_CASES = [
+    # M, K, Nq, Nkv, bs, dtype, zp, skip
+    (1, 256, 64, 32, 32, np.float16, None, False),
+    (4, 512, 128, 48, 64, np.float16, "packed", True),
+    (16, 256, 40, 24, 32, np.float16, None, True),
+    (3, 96, 20, 12, 32, np.float32, "packed", True),
+]
+
+
+@pytest.mark.parametrize("M,K,Nq,Nkv,bs,dtype,zp,skip", QKV_CASES)
+def test_qkv_parity(gpu, M, K, Nq, Nkv, bs, dtype, zp, skip):
+    rng = np.random.default_rng(M + K + Nq + Nkv)
+    A = rng.standard_normal((M, K)).astype(dtype)
+    sk = rng.standard_normal((M, K)).astype(dtype) if skip else None
+    g = rng.uniform(0.5, 1.5, K).astype(dtype)
+    parts = [rand_case(rng, 1, K, n, 4, bs, dtype, zp)[1:4] for n in (Nq, Nkv, Nkv)]
+    o = ops()
+    Q, Kk, V, R = o.matmul_nbits_qkv(dev(A), *[dev(x) for p in parts for x in p[:2]], norm_scale=dev(g), skip=dev(sk),
+                                     block_size=bs, q_zero_points=dev(parts[0][2]), k_zero_points=dev(parts[1][2]),
+                                     v_zero_points=dev(parts[2][2]))
+    ref = O.matmul_nbits_qkv(A, parts[0][0], parts[0][1], parts[1][0], parts[1][1], parts[2][0], parts[2][1], K=K,
+                             Nq=Nq, Nkv=Nkv, norm_scale=g, skip=sk, block_size=bs, q_zero_points=parts[0][2],
+                             k_zero_points=parts[1][2], v_zero_points=parts[2][2])
+    for got, exp, nm in zip((Q, Kk, V), ref[:3], "qkv"):
+        assert_parity(host(got), exp, dtype, nm)
+    assert np.array_equal(host(R), ref[3])  # residual A + skip: bit-exact
+
+
+MLP_CASES = [
+    # M, K, N, bs, dtype, skip, norm, biases, act
+    (1, 256, 64, 32, np.float16, False, False, False, "silu"),
+    (16, 512, 72, 32, np.float16, False, False, False, "silu"),
+    (4, 256, 40, 64, np.float16, True, True, True, "silu"),
+    (8, 128, 24, 32, np.float16, True, False, True, "gelu"),
+    (2, 64, 10, 16, np.float32, True, True, True, "silu"),
+    (5, 256, 33, 32, np.float16, False, True, False, "relu"),
+]
+
+
+@pytest.mark.parametrize("M,K,N,bs,dtype,skip,norm,biases,act", MLP_CASES)
+def test_mlp_parity(gpu, M, K, N, bs, dtype, skip, norm, biases, act):
+    rng = np.random.default_rng(M + K + N + bs)
+    A = rng.standard_normal((M, K)).astype(dtype)
+    sk = rng.standard_normal((M, K)).astype(dtype) if skip else None
+    g = rng.uniform(0.5, 1.5, K).astype(dtype) if norm else None
+    _, gB, gS, _, gb = rand_case(rng, 1, K, N, 4, bs, dtype, None, biases)
+    _, uB, uS, _, ub = rand_case(rng, 1, K, N, 4, bs, dtype, None, biases)
+    Y, R = ops().matmul_nbits_mlp(dev(A), dev(gB), dev(gS), dev(uB), dev(uS), skip=dev(sk), norm_scale=dev(g),
+                                  gate_bias=dev(gb), up_bias=dev(ub), block_size=bs, activation=act,
+                                  want_residual=True)
+    ref, r = O.matmul_nbits_mlp(A, gB, gS, uB, uS, K=K, N=N, skip=sk, norm_scale=g, gate_bias=gb, up_bias=ub,
+                                block_size=bs, activation=act)
+    assert_parity(host(Y), ref, dtype)
+    assert np.array_equal(host(R), r)
+
+
+@pytest.mark.parametrize("name", ["pinned_plain_gb_ub", "pinned_norm_nogb_noub", "pinned_skipsum_gb_ub"])
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_fixture_mlp_pinned(gpu, name, dtype):
+    case = F.find("com.microsoft.MatMulNBitsMlp", name)
+    ins = F.case_inputs(case)
+    conv = {k: (v.astype(dtype) if v.dtype != np.uint8 else v) for k, v in ins.items()}
+    at = case["attrs"]
+    Y, R = ops().matmul_nbits_mlp(dev(conv["aT"]), dev(conv["gateBT"]), dev(conv["gateScalesT"]), dev(conv["upBT"]),
+                                  dev(conv["upScalesT"]), skip=dev(conv.get("skipT")),
+                                  norm_scale=dev(conv.get("normScaleT")), gate_bias=dev(conv.get("gateBiasT")),
+                                  up_bias=dev(conv.get("upBiasT")), block_size=at["block_size"],
+                                  activation=at["activation"], want_residual=True)
+    exp = F.materialize(case["outputs"]["yT"])
+    if dtype == np.float32:
+        assert F.reference_compare(host(Y), exp, *F.case_tolerance(case, "yT"))
+        if "residualT" in case["outputs"]:
+            assert F.reference_compare(host(R), F.materialize(case["outputs"]["residualT"]),
+                                       *F.case_tolerance(case, "residualT"))
+    else:
+        ref, _ = O.matmul_nbits_mlp(conv["aT"], conv["gateBT"], conv["gateScalesT"], conv["upBT"], conv["upScalesT"],
+                                    K=at["K"], N=at["N"], skip=conv.get("skipT"), norm_scale=conv.get("normScaleT"),
+                                    gate_bias=conv.get("gateBiasT"), up_bias=conv.get("upBiasT"),
+                                    block_size=at["block_size"])
+        assert_parity(host(Y), ref, np.float16)
+
+
+def test_fixture_qkv_kat(gpu):
+    case = F.find("com.microsoft.MatMulNBitsQkv", "independent_nonzero_reference_qkv_kat")
+    ins = F.case_inputs(case)
+    Q, Kk, V, R = ops().matmul_nbits_qkv(dev(ins["aT"]), dev(ins["qBT"]), dev(ins["qScalesT"]), dev(ins["kBT"]),
+                                         dev(ins["kScalesT"]), dev(ins["vBT"]), dev(ins["vScalesT"]),
+                                         norm_scale=dev(ins["normScaleT"]), skip=dev(ins["skipT"]), block_size=16)
+    base = 0.8320502943
+    for t, c in ((Q, 1), (Kk, 2), (V, 3)):
+        assert np.allclose(host(t), base * c, atol=2e-4, rtol=2e-4)
+    assert np.array_equal(host(R), np.array([[1.5, 1.5, -0.75, 1.5]], np.float32))
+
+
+# --------------------------------------------------------------------------- full-size workloads
+
+def _run_workload(w):
+    i, at, o = w["inputs"], w["attrs"], ops()
+    d = {k: dev(v) for k, v in i.items()}
+    if w["op"] == "com.microsoft.MatMulNBits":
+        return [o.matmul_nbits(d["aT"], d["bT"], d["scalesT"], d.get("zeroPointsT"), d.get("biasT"),
+                               block_size=at["block_size"])]
+    if w["op"] == "com.microsoft.MatMulNBitsQkv":
+        return list(o.matmul_nbits_qkv(d["aT"], d["qBT"], d["qScalesT"], d["kBT"], d["kScalesT"], d["vBT"],
+                                       d["vScalesT"], norm_scale=d["normScaleT"], block_size=at["block_size"],
+                                       epsilon=at["epsilon"], q_zero_points=d["qZeroPointsT"],
+                                       k_zero_points=d["kZeroPointsT"], v_zero_points=d["vZeroPointsT"])[:3])
+    return [o.matmul_nbits_mlp(d["aT"], d["gateBT"], d["gateScalesT"], d["upBT"], d["upScalesT"],
+                               block_size=at["block_size"], activation=at["activation"])[0]]
+
+
+def test_workload_cpu_f32_k2048(gpu):
+    w = workloads.make("cpu_f32_k2048")
+    i, at = w["inputs"], w["attrs"]
+    y = host(_run_workload(w)[0])
+    ref = O.matmul_nbits(i["aT"], i["bT"], i["scalesT"], i["zeroPointsT"], K=at["K"], N=at["N"], block_size=32)
+    assert_parity(y, ref, np.float32)
+
+
+def test_workload_decode_up_m1(gpu):
+    w = workloads.make("decode_up_m1")
+    i, at = w["inputs"], w["attrs"]
+    assert ops().select_kernel("MatMulNBits", 1, at["K"], at["N"], 4, 32) == "gemv_q4_mfma"
+    y = host(_run_workload(w)[0])
+    ref = O.matmul_nbits(i["aT"], i["bT"], i["scalesT"], K=at["K"], N=at["N"], block_size=32)
+    assert_parity(y, ref, np.float16)
+
+
+def test_workload_qkv_gqa_m4(gpu):
+    w = workloads.make("qkv_gqa_m4")
+    i, at = w["inputs"], w["attrs"]
+    outs = [host(t) for t in _run_workload(w)]
+    ref = O.matmul_nbits_qkv(i["aT"], i["qBT"], i["qScalesT"], i["kBT"], i["kScalesT"], i["vBT"], i["vScalesT"],
+                             K=at["K"], Nq=at["Nq"], Nkv=at["Nkv"], norm_scale=i["normScaleT"],
+                             block_size=at["block_size"], epsilon=at["epsilon"], q_zero_points=i["qZeroPointsT"],
+                             k_zero_points=i["kZeroPointsT"], v_zero_points=i["vZeroPointsT"])
+    for got, exp in zip(outs, ref[:3]):
+        assert_parity(got, exp, np.float16)
+
+
+def test_workload_mlp_swiglu_m16(gpu):
+    w = workloads.make("mlp_swiglu_m16")
+    i, at = w["inputs"], w["attrs"]
+    y = host(_run_workload(w)[0])
+    ref, _ = O.matmul_nbits_mlp(i["aT"], i["gateBT"], i["gateScalesT"], i["upBT"], i["upScalesT"], K=at["K"],
+                                N=at["N"], block_size=at["block_size"])
+    assert_parity(y, ref, np.float16)
+
+
+def test_workload_prefill_m2048_row_sample(gpu):
+    """Full-size prefill on the GPU; rows are independent, so a seeded sample of
+    96 rows (plus the first and last) is checked against the oracle."""
+    w = workloads.make("prefill_m2048")
+    i, at = w["inputs"], w["attrs"]
+    assert ops().select_kernel("MatMulNBits", 2048, at["K"], at["N"], 4, 128, zp="packed") == "gemm_q4_mfma"
+    y = host(_run_workload(w)[0])
+    rows = np.unique(np.concatenate([[0, 2047], np.random.default_rng(9).choice(2048, 96, replace=False)]))
+    ref = O.matmul_nbits(i["aT"][rows], i["bT"], i["scalesT"], i["zeroPointsT"], i["biasT"], K=at["K"], N=at["N"],
+                         block_size=at["block_size"])
+    assert_parity(y[rows], ref, np.float16)
+    assert np.all(np.isfinite(y))

@@ -1,0 +1,181 @@
+// C ABI of libxrmm: argument validation and dispatch of the zero-copy entry
+// points. The error classes mirror the reference's std::invalid_argument
+// (contract / geometry) and std::runtime_error (device) split.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/xrmm.h"
+#include "xrmm_internal.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+int ok() {
+  g_error.clear();
+  return XRMM_OK;
+}
+
+int dev_fail(hipError_t e, const char* where) {
+  return fail(XRMM_EDEVICE, std::string(where) + ": " + hipGetErrorString(e));
+}
+
+bool t1_ok(int32_t d) { return d == XRMM_F32 || d == XRMM_F16; }
+
+// zero-point dtype -> kind; -1 if invalid
+int zp_kind_of(int32_t zp_dtype) {
+  if (zp_dtype == XRMM_UNSPECIFIED) return xrmm::ZP_NONE;
+  if (zp_dtype == XRMM_F32 || zp_dtype == XRMM_F16) return xrmm::ZP_FLOAT;
+  if (zp_dtype == XRMM_U8) return xrmm::ZP_PACKED;
+  return -1;
+}
+
+// Shared geometry checks; fills the common part of the launch description.
+int geometry(xrmm::Launch& L, int op, int64_t M, int64_t K, int32_t bits, int32_t block_size,
+             int32_t dtype, int32_t zp_dtype) {
+  if (!t1_ok(dtype)) return fail(XRMM_EINVAL, "T1 must be float32 or float16");
+  if (bits != 2 && bits != 4 && bits != 8) return fail(XRMM_EINVAL, "bits must be 2, 4 or 8");
+  if (block_size <= 0) return fail(XRMM_EINVAL, "Invalid packed matmul geometry: block_size must be positive");
+  if (K <= 0) return fail(XRMM_EINVAL, "Invalid packed matmul geometry: K must be positive");
+  if (M < 0) return fail(XRMM_EINVAL, "M must be non-negative");
+  const int zk = zp_kind_of(zp_dtype);
+  if (zk < 0) return fail(XRMM_EINVAL, "zero points must be float32, float16 or packed uint8");
+  std::memset(&L, 0, sizeof(L));
+  L.op = op;
+  L.dtype = dtype == XRMM_F32 ? xrmm::DT_F32 : xrmm::DT_F16;
+  L.zp_kind = zk;
+  L.zp_dtype = zp_dtype == XRMM_F32 ? xrmm::DT_F32 : xrmm::DT_F16;
+  L.bits = bits;
+  L.block_size = block_size;
+  L.M = M;
+  L.K = K;
+  L.kb = (K + block_size - 1) / block_size;
+  L.blob = (static_cast<int64_t>(block_size) * bits + 7) / 8;
+  L.zrow = (L.kb * bits + 7) / 8;
+  return XRMM_OK;
+}
+
+int run(const xrmm::Launch& L, void* stream) {
+  hipError_t e = xrmm::launch(L, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return dev_fail(e, "kernel launch");
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* xrmm_last_error(void) { return g_error.c_str(); }
+
+const char* xrmm_version(void) { return "xrmm 0.1.0 gfx950"; }
+
+int xrmm_matmul_nbits(const void* A, const void* B, const void* scales, const void* zero_points,
+                      int32_t zp_dtype, const void* bias, void* Y, int64_t M, int64_t K, int64_t N,
+                      int32_t bits, int32_t block_size, int32_t dtype, void* stream) {
+  xrmm::Launch L;
+  if (int rc = geometry(L, xrmm::OP_MATMUL, M, K, bits, block_size, dtype, zp_dtype)) return rc;
+  if (N <= 0) return fail(XRMM_EINVAL, "Packed matmul N required");
+  if (zp_dtype != XRMM_UNSPECIFIED && !zero_points) return fail(XRMM_EINVAL, "zero-point dtype given without zero points");
+  if (M > 0 && (!A || !B || !scales || !Y)) return fail(XRMM_EINVAL, "null tensor pointer");
+  L.nproj = 1;
+  L.A = A;
+  L.p[0] = xrmm::Proj{static_cast<const uint8_t*>(B), scales, zero_points, bias, Y, N};
+  return run(L, stream);
+}
+
+int xrmm_matmul_nbits_qkv(const void* A, const void* skip, const void* norm_scale, const void* q_B,
+                          const void* q_scales, const void* q_zero_points, const void* k_B,
+                          const void* k_scales, const void* k_zero_points, const void* v_B,
+                          const void* v_scales, const void* v_zero_points, int32_t zp_dtype, void* Q,
+                          void* Kout, void* V, void* residual, int64_t M, int64_t K, int64_t Nq,
+                          int64_t Nkv, int32_t bits, int32_t block_size, float epsilon, int32_t dtype,
+                          void* stream) {
+  xrmm::Launch L;
+  if (int rc = geometry(L, xrmm::OP_QKV, M, K, bits, block_size, dtype, zp_dtype)) return rc;
+  if (Nq <= 0 || Nkv <= 0) return fail(XRMM_EINVAL, "Nq and Nkv must be positive");
+  if (!norm_scale) return fail(XRMM_EINVAL, "Missing complex input: normScaleT");
+  if (M > 0 && (!A || !q_B || !k_B || !v_B || !q_scales || !k_scales || !v_scales || !Q || !Kout || !V))
+    return fail(XRMM_EINVAL, "null tensor pointer");
+  if (zp_dtype == XRMM_UNSPECIFIED && (q_zero_points || k_zero_points || v_zero_points))
+    return fail(XRMM_EINVAL, "zero points given without a zero-point dtype");
+  L.nproj = 3;
+  L.A = A;
+  L.skip = skip;
+  L.gamma = norm_scale;
+  L.residual = residual;
+  L.eps = epsilon;
+  L.p[0] = xrmm::Proj{static_cast<const uint8_t*>(q_B), q_scales, q_zero_points, nullptr, Q, Nq};
+  L.p[1] = xrmm::Proj{static_cast<const uint8_t*>(k_B), k_scales, k_zero_points, nullptr, Kout, Nkv};
+  L.p[2] = xrmm::Proj{static_cast<const uint8_t*>(v_B), v_scales, v_zero_points, nullptr, V, Nkv};
+  return run(L, stream);
+}
+
+int xrmm_matmul_nbits_mlp(const void* A, const void* skip, const void* norm_scale, const void* gate_B,
+                          const void* gate_scales, const void* gate_zero_points, const void* gate_bias,
+                          const void* up_B, const void* up_scales, const void* up_zero_points,
+                          const void* up_bias, int32_t zp_dtype, void* Y, void* residual, int64_t M,
+                          int64_t K, int64_t N, int32_t bits, int32_t block_size, float epsilon,
+                          int32_t activation, int32_t dtype, void* stream) {
+  xrmm::Launch L;
+  if (int rc = geometry(L, xrmm::OP_MLP, M, K, bits, block_size, dtype, zp_dtype)) return rc;
+  if (N <= 0) return fail(XRMM_EINVAL, "Packed matmul N required");
+  if (activation < XRMM_ACT_NONE || activation > XRMM_ACT_SWIGLU) return fail(XRMM_EINVAL, "Unknown fused activation");
+  if (M > 0 && (!A || !gate_B || !gate_scales || !up_B || !up_scales || !Y))
+    return fail(XRMM_EINVAL, "null tensor pointer");
+  if (zp_dtype == XRMM_UNSPECIFIED && (gate_zero_points || up_zero_points))
+    return fail(XRMM_EINVAL, "zero points given without a zero-point dtype");
+  L.nproj = 2;
+  L.A = A;
+  L.skip = skip;
+  L.gamma = norm_scale;
+  L.residual = residual;
+  L.eps = epsilon;
+  L.act = activation;
+  L.p[0] = xrmm::Proj{static_cast<const uint8_t*>(gate_B), gate_scales, gate_zero_points, gate_bias, Y, N};
+  L.p[1] = xrmm::Proj{static_cast<const uint8_t*>(up_B), up_scales, up_zero_points, up_bias, nullptr, N};
+  return run(L, stream);
+}
+
+int xrmm_dequantize(const void* B, const void* scales, const void* zero_points, int32_t zp_dtype, void* W,
+                    int64_t N, int64_t K, int32_t bits, int32_t block_size, int32_t scale_dtype,
+                    int32_t out_dtype, void* stream) {
+  xrmm::Launch L;
+  if (int rc = geometry(L, xrmm::OP_MATMUL, 0, K, bits, block_size, scale_dtype, zp_dtype)) return rc;
+  if (N <= 0) return fail(XRMM_EINVAL, "N must be positive");
+  if (!t1_ok(out_dtype)) return fail(XRMM_EINVAL, "output dtype must be float32 or float16");
+  if (!B || !scales || !W) return fail(XRMM_EINVAL, "null tensor pointer");
+  if (zp_dtype != XRMM_UNSPECIFIED && !zero_points) return fail(XRMM_EINVAL, "zero-point dtype given without zero points");
+  L.nproj = 1;
+  L.p[0] = xrmm::Proj{static_cast<const uint8_t*>(B), scales, zero_points, nullptr, nullptr, N};
+  hipError_t e = xrmm::launch_dequantize(L, W, out_dtype == XRMM_F32 ? xrmm::DT_F32 : xrmm::DT_F16,
+                                         static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return dev_fail(e, "dequantize launch");
+  return ok();
+}
+
+const char* xrmm_select_kernel(int32_t op, int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size,
+                               int32_t dtype, int32_t zp_dtype) {
+  xrmm::Launch L;
+  if (op < xrmm::OP_MATMUL || op > xrmm::OP_MLP) {
+    fail(XRMM_EINVAL, "unknown operator code");
+    return nullptr;
+  }
+  if (geometry(L, op, M, K, bits, block_size, dtype, zp_dtype)) return nullptr;
+  // aligned placeholders: the selection only looks at pointer alignment
+  static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
+  L.nproj = op == xrmm::OP_QKV ? 3 : op == xrmm::OP_MLP ? 2 : 1;
+  L.A = dummy;
+  for (int i = 0; i < L.nproj; ++i) L.p[i] = xrmm::Proj{dummy, dummy, zp_dtype == XRMM_UNSPECIFIED ? nullptr : dummy, nullptr, nullptr, N};
+  ok();
+  return xrmm::kernel_name(xrmm::select_kernel(L));
+}
+
+}  // extern "C"

@@ -1,0 +1,57 @@
+// Internal interfaces shared by the kernel file and the host ABI of libxrmm.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace xrmm {
+
+enum Op { OP_MATMUL = 0, OP_QKV = 1, OP_MLP = 2 };
+enum ZpKind { ZP_NONE = 0, ZP_FLOAT = 1, ZP_PACKED = 2 };
+enum DT { DT_F32 = 0, DT_F16 = 1 };
+
+// One packed projection: weights, scales, optional zero points and bias, and
+// where its output goes.
+struct Proj {
+  const uint8_t* B;    // [N, kb, blob]
+  const void* scales;  // [N, kb] of dtype
+  const void* zp;      // nullptr | float [N, kb] | packed u8 [N, zrow]
+  const void* bias;    // nullptr | [N] of dtype
+  void* Y;             // [M, N] of dtype (unused for the Mlp up projection)
+  int64_t N;
+};
+
+// Everything a launch needs; passed to kernels by value.
+struct Launch {
+  int op;
+  int dtype;     // T1: DT_F32 / DT_F16
+  int zp_kind;   // ZpKind
+  int zp_dtype;  // DT_F32 / DT_F16 for ZP_FLOAT
+  int bits;
+  int block_size;
+  int act;       // Mlp activation kind
+  int nproj;     // 1 (MatMul), 3 (Qkv), 2 (Mlp: gate, up)
+  int64_t M, K, kb, blob, zrow;
+  const void* A;
+  const void* skip;      // nullable
+  const void* gamma;     // nullable
+  void* residual;        // nullable
+  float eps;
+  Proj p[3];
+};
+
+// Kernel families the dispatcher chooses between.
+enum Kernel { K_GENERIC = 0, K_GEMV_Q4 = 1, K_GEMM_Q4 = 2 };
+
+// Choose a kernel family for the geometry (host only, no device calls).
+Kernel select_kernel(const Launch& L);
+const char* kernel_name(Kernel k);
+
+// Enqueue the operator on `stream`. Returns hipSuccess or the launch error.
+hipError_t launch(const Launch& L, hipStream_t stream);
+
+// W [N, K] in out_dtype (see xrmm_dequantize).
+hipError_t launch_dequantize(const Launch& L, void* W, int out_dtype, hipStream_t stream);
+
+}  // namespace xrmm

@@ -1,0 +1,175 @@
+"""PyTorch-ROCm front end of the zero-copy entry points.
+
+Tensors stay on the GPU; the library receives their device pointers and the
+current HIP stream. PyTorch only provides memory and streams here: every
+operator runs a HIP kernel of libxrmm.so, and a missing library raises.
+
+Shapes follow the operator contracts (kernels/com.microsoft.MatMulNBits*/
+contract.json): A ``[..., K]`` (leading axes fold into rows), B
+``[N, ceil(K/bs), ceil(bs*bits/8)]`` uint8, scales ``[N, ceil(K/bs)]``,
+float zero points ``[N, ceil(K/bs)]`` or packed uint8 zero points
+``[N, ceil(ceil(K/bs)*bits/8)]``.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+_T1 = {torch.float32: nat.F32, torch.float16: nat.F16}
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream=None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _check_dev(*ts):
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise nat.XrmmInvalid("tensors must be on the GPU")
+        if not t.is_contiguous():
+            raise nat.XrmmInvalid("tensors must be contiguous")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise nat.XrmmInvalid("tensors must share one device")
+    return dev
+
+
+def _zp_dtype(zp):
+    if zp is None:
+        return nat.UNSPECIFIED
+    if zp.dtype == torch.uint8:
+        return nat.U8
+    if zp.dtype in _T1:
+        return _T1[zp.dtype]
+    raise nat.XrmmInvalid("zero points must be float32, float16 or uint8")
+
+
+def _t1(A):
+    if A.dtype not in _T1:
+        raise nat.XrmmInvalid("A must be float32 or float16")
+    return _T1[A.dtype]
+
+
+def _geometry(K, bits, block_size):
+    kb = (K + block_size - 1) // block_size
+    blob = (block_size * bits + 7) // 8
+    return kb, blob, (kb * bits + 7) // 8
+
+
+def _check_weights(B, S, Z, N, K, bits, bs, dtype, name=""):
+    kb, blob, zrow = _geometry(K, bits, bs)
+    if B.dtype != torch.uint8 or tuple(B.shape) != (N, kb, blob):
+        raise nat.XrmmInvalid(f"{name}B must be uint8 [{N}, {kb}, {blob}], got {B.dtype} {tuple(B.shape)}")
+    if S.dtype != dtype or tuple(S.shape) != (N, kb):
+        raise nat.XrmmInvalid(f"{name}scales must be {dtype} [{N}, {kb}], got {S.dtype} {tuple(S.shape)}")
+    if Z is not None:
+        want = (N, zrow) if Z.dtype == torch.uint8 else (N, kb)
+        if tuple(Z.shape) != want:
+            raise nat.XrmmInvalid(f"{name}zero points must have shape {list(want)}, got {tuple(Z.shape)}")
+
+
+def matmul_nbits(A, B, scales, zero_points=None, bias=None, *, K=None, N=None, bits=4,
+                 block_size=32, out=None, stream=None):
+    """com.microsoft.MatMulNBits on the GPU. Returns Y ``A.shape[:-1] + [N]``."""
+    K = int(K if K is not None else A.shape[-1])
+    N = int(N if N is not None else B.shape[0])
+    if A.shape[-1] != K:
+        raise nat.XrmmInvalid("A's last dimension must equal K")
+    _check_dev(A, B, scales, zero_points, bias, out)
+    _check_weights(B, scales, zero_points, N, K, bits, block_size, A.dtype)
+    if bias is not None and (bias.dtype != A.dtype or tuple(bias.shape) != (N,)):
+        raise nat.XrmmInvalid("bias must be [N] of A's dtype")
+    M = A.numel() // K
+    if out is None:
+        out = torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
+    nat.check(nat.lib().xrmm_matmul_nbits(_ptr(A), _ptr(B), _ptr(scales), _ptr(zero_points),
+                                          _zp_dtype(zero_points), _ptr(bias), _ptr(out), M, K, N,
+                                          bits, block_size, _t1(A), _stream(stream)))
+    return out
+
+
+def matmul_nbits_qkv(A, q_B, q_scales, k_B, k_scales, v_B, v_scales, *, norm_scale, skip=None,
+                     K=None, Nq=None, Nkv=None, bits=4, block_size=32, epsilon=1e-6,
+                     q_zero_points=None, k_zero_points=None, v_zero_points=None,
+                     want_residual=True, stream=None):
+    """com.microsoft.MatMulNBitsQkv. Returns ``(Q, K, V, residual-or-None)``."""
+    K = int(K if K is not None else A.shape[-1])
+    Nq = int(Nq if Nq is not None else q_B.shape[0])
+    Nkv = int(Nkv if Nkv is not None else k_B.shape[0])
+    zps = (q_zero_points, k_zero_points, v_zero_points)
+    _check_dev(A, skip, norm_scale, q_B, q_scales, k_B, k_scales, v_B, v_scales, *zps)
+    for (Bm, S, Z, n, nm) in ((q_B, q_scales, zps[0], Nq, "q_"), (k_B, k_scales, zps[1], Nkv, "k_"),
+                              (v_B, v_scales, zps[2], Nkv, "v_")):
+        _check_weights(Bm, S, Z, n, K, bits, block_size, A.dtype, nm)
+    present = [z for z in zps if z is not None]
+    zdt = _zp_dtype(present[0]) if present else nat.UNSPECIFIED
+    if any(_zp_dtype(z) != zdt for z in present):
+        raise nat.XrmmInvalid("zero points of the three projections must share a dtype")
+    M = A.numel() // K
+    lead = tuple(A.shape[:-1])
+    Q = torch.empty(lead + (Nq,), dtype=A.dtype, device=A.device)
+    Ko = torch.empty(lead + (Nkv,), dtype=A.dtype, device=A.device)
+    V = torch.empty(lead + (Nkv,), dtype=A.dtype, device=A.device)
+    R = torch.empty_like(A) if want_residual else None
+    nat.check(nat.lib().xrmm_matmul_nbits_qkv(
+        _ptr(A), _ptr(skip), _ptr(norm_scale), _ptr(q_B), _ptr(q_scales), _ptr(zps[0]), _ptr(k_B),
+        _ptr(k_scales), _ptr(zps[1]), _ptr(v_B), _ptr(v_scales), _ptr(zps[2]), zdt, _ptr(Q), _ptr(Ko),
+        _ptr(V), _ptr(R), M, K, Nq, Nkv, bits, block_size, float(epsilon), _t1(A), _stream(stream)))
+    return Q, Ko, V, R
+
+
+def matmul_nbits_mlp(A, gate_B, gate_scales, up_B, up_scales, *, skip=None, norm_scale=None,
+                     gate_bias=None, up_bias=None, K=None, N=None, bits=4, block_size=32,
+                     epsilon=1e-5, activation="silu", gate_zero_points=None, up_zero_points=None,
+                     want_residual=False, stream=None):
+    """com.microsoft.MatMulNBitsMlp. Returns ``(Y, residual-or-None)``."""
+    K = int(K if K is not None else A.shape[-1])
+    N = int(N if N is not None else gate_B.shape[0])
+    if activation not in nat.ACT:
+        raise nat.XrmmInvalid("Unknown fused activation: " + str(activation))
+    _check_dev(A, skip, norm_scale, gate_B, gate_scales, up_B, up_scales, gate_bias, up_bias,
+               gate_zero_points, up_zero_points)
+    _check_weights(gate_B, gate_scales, gate_zero_points, N, K, bits, block_size, A.dtype, "gate_")
+    _check_weights(up_B, up_scales, up_zero_points, N, K, bits, block_size, A.dtype, "up_")
+    present = [z for z in (gate_zero_points, up_zero_points) if z is not None]
+    zdt = _zp_dtype(present[0]) if present else nat.UNSPECIFIED
+    M = A.numel() // K
+    Y = torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
+    R = torch.empty_like(A) if want_residual else None
+    nat.check(nat.lib().xrmm_matmul_nbits_mlp(
+        _ptr(A), _ptr(skip), _ptr(norm_scale), _ptr(gate_B), _ptr(gate_scales), _ptr(gate_zero_points),
+        _ptr(gate_bias), _ptr(up_B), _ptr(up_scales), _ptr(up_zero_points), _ptr(up_bias), zdt, _ptr(Y),
+        _ptr(R), M, K, N, bits, block_size, float(epsilon), nat.ACT[activation], _t1(A), _stream(stream)))
+    return Y, R
+
+
+def dequantize(B, scales, zero_points=None, *, K, bits=4, block_size=32, out_dtype=torch.float32,
+               stream=None):
+    """Dequantized ``W[N, K]``: float32 reference value or its one-rounding fp16."""
+    N = int(B.shape[0])
+    _check_dev(B, scales, zero_points)
+    _check_weights(B, scales, zero_points, N, K, bits, block_size, scales.dtype)
+    W = torch.empty((N, K), dtype=out_dtype, device=B.device)
+    nat.check(nat.lib().xrmm_dequantize(_ptr(B), _ptr(scales), _ptr(zero_points), _zp_dtype(zero_points),
+                                        _ptr(W), N, K, bits, block_size, _T1[scales.dtype], _T1[out_dtype],
+                                        _stream(stream)))
+    return W
+
+
+def select_kernel(op: str, M, K, N, bits=4, block_size=32, dtype=torch.float16, zp=None) -> str:
+    code = {"MatMulNBits": 0, "MatMulNBitsQkv": 1, "MatMulNBitsMlp": 2}[op]
+    zdt = nat.UNSPECIFIED if zp is None else {"packed": nat.U8, "float": nat.F16}[zp]
+    r = nat.lib().xrmm_select_kernel(code, M, K, N, bits, block_size, _T1[dtype], zdt)
+    if r is None:
+        raise nat.XrmmInvalid(nat.last_error())
+    return r.decode()
