@@ -84,7 +84,8 @@ FAST_CASES = [
     (7, 384, 48, 128, None, True),
     (16, 512, 80, 32, "float_int", False),
     (16, 288, 17, 32, None, True),       # K tail inside the last block (K % bs != 0)
-    (3, 256, 40, 48, "packed", False),   # 16-code half blocks
+    (3, 256, 40, 16, "packed", True),    # two blocks per 16-byte chunk
+    (9, 512, 70, 32, "packed", True),    # four column tiles per workgroup
 ]
 
 
@@ -128,6 +129,7 @@ GENERIC_CASES = [
     (4, 24, 6, 4, 8, np.float16, None, True),
     (20, 100, 11, 8, 32, np.float32, "float", True),
     (2, 17, 2, 4, 16, np.float16, "float", True),
+    (3, 256, 40, 4, 48, np.float16, "packed", False),  # non-power-of-two block
 ]
 
 

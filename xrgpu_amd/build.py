@@ -1,7 +1,9 @@
 """Build libxrmm.so for gfx950 in-tree with hipcc.
 
 ``python -m xrgpu_amd.build`` compiles ``xrgpu_amd/csrc`` into
-``xrgpu_amd/lib/libxrmm.so``. It cross-compiles without a GPU.
+``xrgpu_amd/lib/libxrmm.so``. Translation units compile in parallel (the GEMV
+family once per zero-point kind) into ``xrgpu_amd/_build`` and are linked into
+one shared library. It cross-compiles without a GPU.
 """
 from __future__ import annotations
 
@@ -9,18 +11,28 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
+OBJ_DIR = os.path.join(HERE, "_build")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libxrmm.so")
 ARCH = os.environ.get("XRMM_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["xrmm_kernels.hip", "xrmm_api.cpp", "xrmm_operator.cpp"]
+# (source, extra defines, object name)
+UNITS = [
+    ("xrmm_kernels.hip", [], "kernels.o"),
+    ("xrmm_gemv_zp.hip", ["-DXRMM_ZPK=0"], "gemv_zp0.o"),
+    ("xrmm_gemv_zp.hip", ["-DXRMM_ZPK=1"], "gemv_zp1.o"),
+    ("xrmm_gemv_zp.hip", ["-DXRMM_ZPK=2"], "gemv_zp2.o"),
+    ("xrmm_api.cpp", [], "api.o"),
+    ("xrmm_operator.cpp", [], "operator.o"),
+]
 
 FLAGS = [
-    "-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # keep packed-fp32 VALU forms out of the device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unused-command-line-argument",
@@ -34,21 +46,31 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(LIB_DIR, exist_ok=True)
-    srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *FLAGS, "-I", os.path.join(ROOT, "include"), *srcs, "-o", tmp]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed building libxrmm.so")
-    # warnings that are not the host pass's notice about the gfx feature flag
+        raise RuntimeError("hipcc failed: " + " ".join(cmd[-3:]))
     noise = [ln for ln in res.stderr.splitlines() if ln.strip() and "packed-fp32-ops" not in ln]
     if verbose and noise:
         sys.stderr.write("\n".join(noise) + "\n")
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    os.makedirs(LIB_DIR, exist_ok=True)
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    cc = hipcc()
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
+    units = [(os.path.join(CSRC, src), defs, os.path.join(OBJ_DIR, obj)) for src, defs, obj in UNITS
+             if os.path.exists(os.path.join(CSRC, src))]
+    cmds = [[cc, *FLAGS, *inc, *defs, "-c", src, "-o", obj] for src, defs, obj in units]
+    jobs = jobs or min(len(cmds), max(1, (os.cpu_count() or 4)))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(lambda c: _run(c, verbose), cmds))
+    tmp = LIB + ".tmp"
+    _run([cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *[obj for _, _, obj in units], "-o", tmp], verbose)
     os.replace(tmp, LIB)
     return LIB
 

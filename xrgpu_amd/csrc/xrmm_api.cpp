@@ -60,6 +60,9 @@ int geometry(xrmm::Launch& L, int op, int64_t M, int64_t K, int32_t bits, int32_
   L.kb = (K + block_size - 1) / block_size;
   L.blob = (static_cast<int64_t>(block_size) * bits + 7) / 8;
   L.zrow = (L.kb * bits + 7) / 8;
+  L.bs_log2 = -1;
+  for (int i = 0; i < 31; ++i)
+    if (block_size == (1 << i)) L.bs_log2 = i;
   return XRMM_OK;
 }
 

@@ -32,6 +32,7 @@ struct Launch {
   int block_size;
   int act;       // Mlp activation kind
   int nproj;     // 1 (MatMul), 3 (Qkv), 2 (Mlp: gate, up)
+  int bs_log2;   // log2(block_size) when it is a power of two, else -1
   int64_t M, K, kb, blob, zrow;
   const void* A;
   const void* skip;      // nullable

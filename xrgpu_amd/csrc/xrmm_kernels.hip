@@ -23,173 +23,9 @@
 // reference's float32 weight rounded once to binary16. Codes are widened with
 // the exponent-bias trick: OR-ing a nibble into the mantissa of 1024.0h gives
 // 1024 + code exactly (and 1024 + 16*code for the high nibble of a byte).
-#include "xrmm_internal.h"
+#include "xrmm_gemv.h"
 
 namespace xrmm {
-
-typedef _Float16 f16;
-typedef f16 f16x2 __attribute__((ext_vector_type(2)));
-typedef f16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// ---------------------------------------------------------------------------
-// scalar helpers
-
-__device__ __forceinline__ float ld_t(const void* p, int64_t i, int dt) {
-  return dt == DT_F32 ? static_cast<const float*>(p)[i]
-                      : static_cast<float>(static_cast<const f16*>(p)[i]);
-}
-
-__device__ __forceinline__ void st_t(void* p, int64_t i, float v, int dt) {
-  if (dt == DT_F32)
-    static_cast<float*>(p)[i] = v;
-  else
-    static_cast<f16*>(p)[i] = static_cast<f16>(v);  // v_cvt_f16_f32: RNE
-}
-
-// z(n, b) (complex_kernel.glsl:80): midpoint when absent, the float element, or
-// the ONNX Runtime packed low-first field.
-__device__ __forceinline__ float zp_value(const Launch& L, const Proj& P, int64_t n, int64_t b) {
-  if (!P.zp) return static_cast<float>(1u << (L.bits - 1));
-  if (L.zp_kind == ZP_FLOAT) return ld_t(P.zp, n * L.kb + b, L.zp_dtype);
-  const int64_t bit = b * L.bits;
-  const uint32_t byte = static_cast<const uint8_t*>(P.zp)[n * L.zrow + (bit >> 3)];
-  return static_cast<float>((byte >> (bit & 7)) & ((1u << L.bits) - 1u));
-}
-
-// nbitWeight (complex_kernel.glsl:80): (float(code) - z) * scale in float32.
-__device__ __forceinline__ float weight_f32(const Launch& L, const Proj& P, int64_t n, int64_t k) {
-  const int64_t b = k / L.block_size;
-  const int64_t bit = (k - b * L.block_size) * L.bits;
-  const uint32_t byte = P.B[(n * L.kb + b) * L.blob + (bit >> 3)];
-  const uint32_t q = (byte >> (bit & 7)) & ((1u << L.bits) - 1u);
-  const float z = zp_value(L, P, n, b);
-  const float s = ld_t(P.scales, n * L.kb + b, L.dtype);
-  return __fmul_rn(__fsub_rn(static_cast<float>(q), z), s);
-}
-
-// logistic / fused (complex_kernel.glsl:39-47), erf form of gelu for 1027.
-__device__ __forceinline__ float logistic(float x) {
-  return x >= 0.f ? 1.f / (1.f + expf(-x)) : expf(x) / (1.f + expf(x));
-}
-
-__device__ __forceinline__ float activate(float x, int kind) {
-  switch (kind) {
-    case 1: return x > 0.f ? x : 0.f;
-    case 2: return x * logistic(x);
-    case 3: return .5f * x * (1.f + erff(x * .7071067811865475f));
-    case 4: return tanhf(x);
-    case 5: return logistic(x);
-    default: return x;
-  }
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
-// ---------------------------------------------------------------------------
-// 4-bit dequantisation to binary16 (shared by GEMV, GEMM and xrmm_dequantize)
-
-__device__ __forceinline__ f16x2 as_h2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
-
-// Per-block constants: -(1024 + z), -(64 + z) and the scale, each as a pair.
-struct Dq {
-  f16x2 nz1024, nz64, s;
-};
-
-__device__ __forceinline__ Dq dq_consts(float z, f16 s) {
-  Dq c;
-  const f16 a = static_cast<f16>(-(1024.f + z)), b = static_cast<f16>(-(64.f + z));
-  c.nz1024 = f16x2{a, a};
-  c.nz64 = f16x2{b, b};
-  c.s = f16x2{s, s};
-  return c;
-}
-
-// Eight low-first codes of one dword -> (code - z) * scale, in the order
-// [c0, c4, c1, c5, c2, c6, c3, c7]. The activations are staged in the same
-// order, so the dot product is unchanged.
-__device__ __forceinline__ f16x8 dq8(uint32_t x, const Dq& c) {
-  const uint32_t lo = 0x000F000Fu, hi = 0x00F000F0u, magic = 0x64006400u;
-  const uint32_t x8 = x >> 8;
-  const f16x2 inv16 = {static_cast<f16>(0.0625f), static_cast<f16>(0.0625f)};
-  // 1024 + c - (1024 + z) and (1024 + 16c)/16 - (64 + z): both exact
-  f16x2 d0 = as_h2((x & lo) | magic) + c.nz1024;
-  f16x2 d1 = __builtin_elementwise_fma(as_h2((x & hi) | magic), inv16, c.nz64);
-  f16x2 d2 = as_h2((x8 & lo) | magic) + c.nz1024;
-  f16x2 d3 = __builtin_elementwise_fma(as_h2((x8 & hi) | magic), inv16, c.nz64);
-  d0 = d0 * c.s;
-  d1 = d1 * c.s;
-  d2 = d2 * c.s;
-  d3 = d3 * c.s;
-  return f16x8{d0.x, d0.y, d1.x, d1.y, d2.x, d2.y, d3.x, d3.y};
-}
-
-// Float zero point of arbitrary value: the reference float32 weight, rounded
-// once to binary16 (same pair order as dq8).
-__device__ __forceinline__ f16x8 dq8_f32z(uint32_t x, float z, float s) {
-  f16x8 r;
-  const int order[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float q = static_cast<float>((x >> (4 * order[i])) & 15u);
-    r[i] = static_cast<f16>(__fmul_rn(__fsub_rn(q, z), s));
-  }
-  return r;
-}
-
-// Pair order of eight consecutive activations, matching dq8.
-__device__ __forceinline__ f16x8 pair_order(f16x8 v) {
-  return __builtin_shufflevector(v, v, 0, 4, 1, 5, 2, 6, 3, 7);
-}
-
-template <int ZPK>
-__device__ __forceinline__ float zp_fast(const Launch& L, const Proj& P, int64_t n, int64_t b) {
-  if constexpr (ZPK == ZP_NONE) {
-    return 8.f;
-  } else if constexpr (ZPK == ZP_PACKED) {
-    const uint32_t byte = static_cast<const uint8_t*>(P.zp)[n * L.zrow + (b >> 1)];
-    return static_cast<float>((byte >> ((b & 1) * 4)) & 15u);
-  } else {
-    return ld_t(P.zp, n * L.kb + b, L.zp_dtype);
-  }
-}
-
-// Dequantise one 16-byte chunk (32 codes) of column n starting at code 32*ch.
-// SPC = 1 when the chunk lies in one block (block_size % 32 == 0), 2 when
-// each 16-code half lies in one block (block_size % 16 == 0).
-template <int ZPK, int SPC>
-__device__ __forceinline__ void dq_chunk(const Launch& L, const Proj& P, int64_t n, int64_t ch,
-                                         bool valid, u32x4 w, f16x8 out[4]) {
-#pragma unroll
-  for (int half = 0; half < SPC; ++half) {
-    const int64_t b = (ch * 32 + half * 16) / L.block_size;
-    f16 s = static_cast<f16>(0.f);
-    float z = 8.f;
-    if (valid) {
-      s = static_cast<const f16*>(P.scales)[n * L.kb + b];
-      z = zp_fast<ZPK>(L, P, n, b);
-    }
-    if constexpr (ZPK == ZP_FLOAT) {
-      const float sf = static_cast<float>(s);
-#pragma unroll
-      for (int d = half * (4 / SPC); d < (half + 1) * (4 / SPC); ++d) out[d] = dq8_f32z(w[d], z, sf);
-    } else {
-      const Dq c = dq_consts(z, s);
-#pragma unroll
-      for (int d = half * (4 / SPC); d < (half + 1) * (4 / SPC); ++d) out[d] = dq8(w[d], c);
-    }
-  }
-}
-
-__device__ __forceinline__ u32x4 ld16(const void* p) {
-  return *static_cast<const u32x4*>(p);
-}
 
 // ---------------------------------------------------------------------------
 // generic kernel: one wave per (column, block of MB rows)
@@ -280,198 +116,6 @@ __global__ __launch_bounds__(64) void k_generic(Launch L) {
         y = activate(y + gb, L.act) * (acc2[i] + ub);
       }
       st_t(P.Y, m * P.N + col, y, L.dtype);
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// GEMV for M <= 16: fp16 activations, 4-bit weights, MFMA 16x16x32
-
-constexpr int GEMV_WAVES = 4;
-
-template <int ZPK, int SPC, int OP>
-__global__ __launch_bounds__(GEMV_WAVES * 64) void k_gemv_q4(Launch L) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ float s_inv[16];
-  constexpr int NT = GEMV_WAVES * 64;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int M = static_cast<int>(L.M);
-  const int64_t K = L.K;
-  const int64_t Kp = L.kb * L.block_size;  // padded K, a multiple of 32
-  const int64_t ldA = Kp + 8;               // halfs per staged row
-  f16* As = reinterpret_cast<f16*>(smem);
-  float* red = reinterpret_cast<float*>(smem);
-
-  // tile -> projection
-  int64_t tile = blockIdx.x;
-  int pi = 0;
-  if constexpr (OP == OP_QKV) {
-    const int64_t t0 = (L.p[0].N + 15) / 16, t1 = (L.p[1].N + 15) / 16;
-    if (tile >= t0) {
-      tile -= t0;
-      pi = 1;
-      if (tile >= t1) {
-        tile -= t1;
-        pi = 2;
-      }
-    }
-  }
-  const Proj& P = L.p[pi];
-  const int64_t n0 = tile * 16;
-  const int64_t groups = Kp / 8;
-
-  // RMS statistic of r = A + skip per row (packedInput, complex_kernel.glsl:81)
-  if constexpr (OP != OP_MATMUL) {
-    if (L.gamma) {
-      for (int m = wave; m < M; m += GEMV_WAVES) {
-        float s = 0.f;
-        for (int64_t j = lane; j < K / 8; j += 64) {
-          const f16x8 a = __builtin_bit_cast(f16x8, ld16(static_cast<const f16*>(L.A) + m * K + j * 8));
-          f16x8 sk = {};
-          if (L.skip) sk = __builtin_bit_cast(f16x8, ld16(static_cast<const f16*>(L.skip) + m * K + j * 8));
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float r = __fadd_rn(static_cast<float>(a[i]), static_cast<float>(sk[i]));
-            s += r * r;
-          }
-        }
-        s = wave_sum(s);
-        if (lane == 0) s_inv[m] = 1.f / sqrtf(s / static_cast<float>(K) + L.eps);
-      }
-      __syncthreads();
-    }
-  }
-
-  // stage the activations (normalised for Qkv/Mlp) in pair order
-  for (int64_t idx = tid; idx < static_cast<int64_t>(M) * groups; idx += NT) {
-    const int m = static_cast<int>(idx / groups);
-    const int64_t k = (idx - static_cast<int64_t>(m) * groups) * 8;
-    f16x8 v = {};
-    if (k < K) {
-      v = __builtin_bit_cast(f16x8, ld16(static_cast<const f16*>(L.A) + m * K + k));
-      if constexpr (OP != OP_MATMUL) {
-        f16x8 sk = {};
-        if (L.skip) sk = __builtin_bit_cast(f16x8, ld16(static_cast<const f16*>(L.skip) + m * K + k));
-        float r[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) r[i] = __fadd_rn(static_cast<float>(v[i]), static_cast<float>(sk[i]));
-        if (L.residual && blockIdx.x == 0) {
-          f16x8 rr;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) rr[i] = static_cast<f16>(r[i]);
-          *reinterpret_cast<f16x8*>(static_cast<f16*>(L.residual) + m * K + k) = rr;
-        }
-        if (L.gamma) {
-          const f16x8 g = __builtin_bit_cast(f16x8, ld16(static_cast<const f16*>(L.gamma) + k));
-          const float inv = s_inv[m];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) v[i] = static_cast<f16>(r[i] * (inv * static_cast<float>(g[i])));
-        } else {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) v[i] = static_cast<f16>(r[i]);
-        }
-      }
-    }
-    *reinterpret_cast<f16x8*>(As + m * ldA + k) = pair_order(v);
-  }
-  __syncthreads();
-
-  // main loop: lane (c, g) streams column n0 + c, chunk 8s + 4h + g
-  const int c = lane & 15, g = lane >> 4;
-  const int64_t n = n0 + c;
-  const bool nval = n < P.N;
-  const int64_t row_bytes = L.kb * L.blob;
-  const int64_t nchunk = row_bytes >> 4;
-  const uint8_t* Brow = P.B + (nval ? n : 0) * row_bytes;
-  const uint8_t* Urow = nullptr;
-  if constexpr (OP == OP_MLP) Urow = L.p[1].B + (nval ? n : 0) * row_bytes;
-  const bool aval = c < M;
-  const f16* Arow = As + c * ldA;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
-  const int64_t steps = (nchunk + 7) / 8;
-
-  u32x4 wb[2], wu[2];
-  auto load_step = [&](int64_t s) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int64_t ch = s * 8 + h * 4 + g;
-      const bool ok = nval && ch < nchunk;
-      wb[h] = ok ? ld16(Brow + ch * 16) : u32x4{0u, 0u, 0u, 0u};
-      if constexpr (OP == OP_MLP) wu[h] = ok ? ld16(Urow + ch * 16) : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-
-  int64_t s = wave;
-  if (s < steps) load_step(s);
-  for (; s < steps; s += GEMV_WAVES) {
-    u32x4 cb[2] = {wb[0], wb[1]}, cu[2];
-    if constexpr (OP == OP_MLP) {
-      cu[0] = wu[0];
-      cu[1] = wu[1];
-    }
-    if (s + GEMV_WAVES < steps) load_step(s + GEMV_WAVES);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int64_t ch = s * 8 + h * 4 + g;
-      const bool cval = ch < nchunk;
-      f16x8 b[4];
-      dq_chunk<ZPK, SPC>(L, P, n, ch, nval && cval, cb[h], b);
-      f16x8 a[4];
-#pragma unroll
-      for (int d = 0; d < 4; ++d)
-        a[d] = (aval && cval) ? *reinterpret_cast<const f16x8*>(Arow + ch * 32 + d * 8) : f16x8{};
-#pragma unroll
-      for (int d = 0; d < 4; ++d) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[d], b[d], acc, 0, 0, 0);
-      if constexpr (OP == OP_MLP) {
-        f16x8 u[4];
-        dq_chunk<ZPK, SPC>(L, L.p[1], n, ch, nval && cval, cu[h], u);
-#pragma unroll
-        for (int d = 0; d < 4; ++d) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[d], u[d], acc2, 0, 0, 0);
-      }
-    }
-  }
-
-  // reduce the waves' partial sums through LDS
-  __syncthreads();
-  constexpr int NACC = OP == OP_MLP ? 8 : 4;
-  if (wave > 0) {
-    float* dst = red + ((wave - 1) * 64 + lane) * NACC;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) dst[r] = acc[r];
-    if constexpr (OP == OP_MLP) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dst[4 + r] = acc2[r];
-    }
-  }
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int w = 1; w < GEMV_WAVES; ++w) {
-    const float* src = red + ((w - 1) * 64 + lane) * NACC;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] += src[r];
-    if constexpr (OP == OP_MLP) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc2[r] += src[4 + r];
-    }
-  }
-  if (!nval) return;
-  // lane (c, g) holds rows 4g..4g+3 of column n
-  float bias = 0.f, ubias = 0.f;
-  if constexpr (OP == OP_MATMUL) {
-    if (P.bias) bias = static_cast<float>(static_cast<const f16*>(P.bias)[n]);
-  }
-  if constexpr (OP == OP_MLP) {
-    if (P.bias) bias = static_cast<float>(static_cast<const f16*>(P.bias)[n]);
-    if (L.p[1].bias) ubias = static_cast<float>(static_cast<const f16*>(L.p[1].bias)[n]);
-  }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = 4 * g + r;
-    if (m < M) {
-      float y = acc[r] + bias;
-      if constexpr (OP == OP_MLP) y = activate(y, L.act) * (acc2[r] + ubias);
-      static_cast<f16*>(P.Y)[static_cast<int64_t>(m) * P.N + n] = static_cast<f16>(y);
     }
   }
 }
@@ -609,34 +253,25 @@ __global__ __launch_bounds__(256) void k_dequant_f32(Launch L, void* W, int out_
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-static int spc_of(int block_size) { return block_size % 32 == 0 ? 1 : 2; }
 
 // fp16, 4-bit, blocks of whole 16-code halves, rows of whole 16-byte chunks,
 // K a multiple of 8 and 16-byte aligned tensors.
 static bool q4_fast_ok(const Launch& L) {
   if (L.dtype != DT_F16 || L.bits != 4) return false;
-  if (L.block_size % 16 != 0) return false;
+  if (L.bs_log2 < 4) return false;  // power-of-two block_size >= 16
   const int64_t Kp = L.kb * L.block_size;
   if (Kp % 32 != 0 || L.K % 8 != 0) return false;
   if (!aligned16(L.A) || !aligned16(L.skip) || !aligned16(L.gamma) || !aligned16(L.residual)) return false;
   for (int i = 0; i < L.nproj; ++i) {
-    if (!aligned16(L.p[i].B)) return false;
+    if (!aligned16(L.p[i].B) || !aligned16(L.p[i].scales) || !aligned16(L.p[i].zp)) return false;
     if (L.zp_kind == ZP_FLOAT && L.p[i].zp == nullptr) return false;
   }
   return true;
 }
 
-static int64_t gemv_lds_bytes(const Launch& L) {
-  const int64_t a = L.M * (L.kb * L.block_size + 8) * 2;
-  const int64_t r = (GEMV_WAVES - 1) * 64 * (L.op == OP_MLP ? 8 : 4) * 4;
-  return a > r ? a : r;
-}
-
-constexpr int64_t kMaxLds = 160 * 1024 - 1024;
-
 Kernel select_kernel(const Launch& L) {
-  if (q4_fast_ok(L)) {
-    if (L.M >= 1 && L.M <= 16 && gemv_lds_bytes(L) <= kMaxLds) return K_GEMV_Q4;
+  if (q4_fast_ok(L) && fits_i32(L)) {
+    if (L.M >= 1 && L.M <= 16 && gemv_tiles(L) != 0) return K_GEMV_Q4;
     if (L.M > 16 && L.op == OP_MATMUL && L.zp_kind != ZP_FLOAT) return K_GEMM_Q4;
   }
   return K_GENERIC;
@@ -648,40 +283,6 @@ const char* kernel_name(Kernel k) {
     case K_GEMM_Q4: return "gemm_q4_mfma";
     default: return "generic";
   }
-}
-
-template <int ZPK, int SPC, int OP>
-static hipError_t launch_gemv3(const Launch& L, hipStream_t st) {
-  const int64_t tiles = (L.p[0].N + 15) / 16 + (OP == OP_QKV ? (L.p[1].N + 15) / 16 + (L.p[2].N + 15) / 16 : 0);
-  const int64_t lds = gemv_lds_bytes(L);
-  auto kern = k_gemv_q4<ZPK, SPC, OP>;
-  if (lds > 64 * 1024) {
-    static bool raised = false;  // per instantiation
-    if (!raised) {
-      // Raises the dynamic-LDS cap where the runtime keeps one; an error here
-      // surfaces from the launch itself if the size is really unsupported.
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(kMaxLds));
-      (void)hipGetLastError();
-      raised = true;
-    }
-  }
-  hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(tiles)), dim3(GEMV_WAVES * 64), static_cast<size_t>(lds), st, L);
-  return hipGetLastError();
-}
-
-template <int ZPK, int SPC>
-static hipError_t launch_gemv2(const Launch& L, hipStream_t st) {
-  switch (L.op) {
-    case OP_QKV: return launch_gemv3<ZPK, SPC, OP_QKV>(L, st);
-    case OP_MLP: return launch_gemv3<ZPK, SPC, OP_MLP>(L, st);
-    default: return launch_gemv3<ZPK, SPC, OP_MATMUL>(L, st);
-  }
-}
-
-template <int ZPK>
-static hipError_t launch_gemv1(const Launch& L, hipStream_t st) {
-  return spc_of(L.block_size) == 1 ? launch_gemv2<ZPK, 1>(L, st) : launch_gemv2<ZPK, 2>(L, st);
 }
 
 template <int ZPK, int SPC>
@@ -710,9 +311,9 @@ hipError_t launch(const Launch& L, hipStream_t st) {
   const int zpk = effective_zpk(L);
   if (zpk < 0) k = K_GENERIC;  // mixed presence of zero points
   if (k == K_GEMV_Q4) {
-    if (zpk == ZP_NONE) return launch_gemv1<ZP_NONE>(L, st);
-    if (zpk == ZP_PACKED) return launch_gemv1<ZP_PACKED>(L, st);
-    return launch_gemv1<ZP_FLOAT>(L, st);
+    if (zpk == ZP_NONE) return launch_gemv_for<ZP_NONE>(L, st);
+    if (zpk == ZP_PACKED) return launch_gemv_for<ZP_PACKED>(L, st);
+    return launch_gemv_for<ZP_FLOAT>(L, st);
   }
   if (k == K_GEMM_Q4) {
     if (zpk == ZP_NONE) return launch_gemm1<ZP_NONE>(L, st);
@@ -729,7 +330,7 @@ hipError_t launch(const Launch& L, hipStream_t st) {
 hipError_t launch_dequantize(const Launch& L, void* W, int out_dtype, hipStream_t st) {
   const Proj& P = L.p[0];
   if (P.N == 0 || L.K == 0) return hipSuccess;
-  if (out_dtype == DT_F16 && L.bits == 4 && L.dtype == DT_F16 && L.block_size % 16 == 0 &&
+  if (out_dtype == DT_F16 && L.bits == 4 && L.dtype == DT_F16 && L.bs_log2 >= 4 &&
       (L.kb * L.block_size) % 32 == 0 && aligned16(P.B)) {
     const int64_t n = P.N * (L.kb * L.blob / 16);
     const dim3 grid(static_cast<uint32_t>((n + 255) / 256));
