@@ -27,6 +27,8 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
 FP16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, published
+PROFILES = os.path.join(ROOT, "profiles")
+SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048": 4}
 
 
 def _gen_weights(torch, g, n, kb, blob, dev):
@@ -110,20 +112,46 @@ def step_fn(ops, name, w):
 
 
 def time_steps(torch, fn, steps, warmup):
-    """Average device time per step with HIP events on the launch stream."""
+    """Device time per step over K steps with HIP events on the launch stream.
+
+    The K steps are captured once into a HIP graph (torch.cuda.CUDAGraph) and
+    the timed region replays it, so back-to-back kernels are not separated by
+    the Python/ctypes launch overhead of each call (about 10 us, longer than
+    a decode kernel). Every step is still one operator call on its own weight
+    replica. Returns (graph ms/step, eager ms/step, host wall ms/call).
+    """
     stream = torch.cuda.current_stream()
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
+    # eager: event-timed and host-timed, for reference
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(stream)
     for i in range(steps):
         fn(warmup + i)
     end.record(stream)
+    wall = (time.perf_counter() - t0) / steps * 1e3
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    return start.elapsed_time(end) / steps, wall / steps * 1e3
+    eager = start.elapsed_time(end) / steps
+    # graph of the same K steps
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            for i in range(steps):
+                fn(i)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    start.record(stream)
+    g.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    del g
+    return ms, eager, wall
 
 
 def per_launch_percentiles(torch, fn, n, warmup):
@@ -193,19 +221,30 @@ def main():
         names = [n for n in names if n in args.only.split(",")]
     for name in names:
         R = args.replicas if name != "prefill_m2048" else 2
-        w = make_replicas(torch, name, R, dev, seed=hash(name) & 0xFFFF)
+        w = make_replicas(torch, name, R, dev, seed=SEEDS[name])
         fn = step_fn(ops, name, w)
         steps = args.steps if name != "prefill_m2048" else max(10, args.steps // 10)
-        ms, wall_ms = time_steps(torch, fn, steps, args.warmup)
+        ms, eager_ms, wall_ms = time_steps(torch, fn, steps, args.warmup)
         p10, p50, p90 = per_launch_percentiles(torch, fn, min(100, steps), 5)
         wl = workloads.make(name, scale_down=1) if name == "decode_up_m1" else None
-        results[name] = dict(ms=ms, wall_ms=wall_ms, p10=p10, p50=p50, p90=p90, steps=steps, replicas=R)
+        results[name] = dict(ms=ms, eager_ms=eager_ms, wall_ms=wall_ms, p10=p10, p50=p50, p90=p90, steps=steps, replicas=R)
         del w, fn, wl
         torch.cuda.empty_cache()
+
+    def traffic_of(summary, dispatch_name):
+        """Calibrated HBM bytes per launch from the committed rocprofv3 summary,
+        when it describes the kernel the dispatcher runs now."""
+        from xrgpu_amd.rocprof_summary import read_field
+        path = os.path.join(PROFILES, summary)
+        if read_field(path, "dispatch_name") != dispatch_name:
+            return None
+        v = read_field(path, "traffic_bytes_per_launch")
+        return int(float(v)) if v else None
 
     out = {}
     if "decode_up_m1" in results:
         r = results["decode_up_m1"]
+        decode_kernel = ops.select_kernel("MatMulNBits", 1, 4096, 14336, 4, 32)
         nbytes = 33_067_008
         gbs = nbytes / (r["ms"] * 1e-3) / 1e9
         out = {
@@ -218,10 +257,13 @@ def main():
                        "parallelism": "single GPU"},
             "gemv_us": round(r["ms"] * 1e3, 3),
             "gemv_us_per_launch_p10_p50_p90": [round(x * 1e3, 3) for x in (r["p10"], r["p50"], r["p90"])],
+            "eager_us_per_call": round(r["eager_ms"] * 1e3, 3),
             "host_wall_us_per_call": round(r["wall_ms"] * 1e3, 3),
+            "timing": "HIP events around a graph replay of K steps (each step one operator call on its own replica)",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                         "kernel": "k_gemv_q4 (ZP none, 1 block per chunk, MatMul)", "bytes_per_launch": nbytes},
+                         "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": traffic_of("decode_up_m1_gemv.md", decode_kernel),
+                         "kernel": decode_kernel, "bytes_per_launch": nbytes},
         }
     if "prefill_m2048" in results:
         r = results["prefill_m2048"]
@@ -231,7 +273,8 @@ def main():
                           "us": round(r["ms"] * 1e3, 2), "tflops": round(tf, 2),
                           "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": FP16_PEAK_TFLOPS,
                                        "unit": "TFLOP/s", "frac": round(tf / FP16_PEAK_TFLOPS, 4),
-                                       "flops_per_launch": fl}}
+                                       "flops_per_launch": fl,
+                                       "kernel": ops.select_kernel("MatMulNBits", 2048, 4096, 14336, 4, 128, zp="packed")}}
     for name, nbytes in (("qkv_gqa_m4", 13_656_064), ("mlp_swiglu_m16", 66_650_112)):
         if name in results:
             r = results[name]

@@ -126,6 +126,114 @@ int xrmm_dequantize(const void* B, const void* scales, const void* zero_points, 
 const char* xrmm_select_kernel(int32_t op, int64_t M, int64_t K, int64_t N, int32_t bits,
                                int32_t block_size, int32_t dtype, int32_t zp_dtype);
 
+/* ---------------------------------------------------------------------------
+ * Request-level lifecycle: the C form of xrgpu::operators::extended
+ * (runtime/include/xrgpu/extended_operators.h:8-61, types
+ * runtime/include/xrgpu/operators.h:9-28). Tensors carry HOST bytes here, as
+ * the reference's owned Tensor does; prepare() uploads them once, run()
+ * launches and waits (with the options' timeout), read_outputs() copies the
+ * results back. Operation ids are "com.microsoft.MatMulNBits",
+ * "com.microsoft.MatMulNBitsQkv" and "com.microsoft.MatMulNBitsMlp"; input and
+ * output names are the contract's port names (aT, bT, scalesT, ...).
+ * ------------------------------------------------------------------------- */
+
+#define XRMM_MAX_RANK 16
+#define XRMM_NAME_MAX 32
+
+/* operators.h:16-23 Tensor. `data` is little-endian contiguous row-major
+ * storage of `nbytes` bytes (NULL for requested outputs). */
+typedef struct xrmm_tensor {
+  const char* name;
+  int32_t dtype;         /* logical dtype */
+  int32_t storage_dtype; /* XRMM_UNSPECIFIED = same as dtype */
+  int32_t rank;
+  int64_t shape[XRMM_MAX_RANK];
+  const void* data;
+  uint64_t nbytes;
+} xrmm_tensor;
+
+/* One entry of extended_operators.h:8-17 Attributes (scalar kinds only). */
+enum { XRMM_ATTR_INT = 0, XRMM_ATTR_FLOAT = 1, XRMM_ATTR_STRING = 2 };
+typedef struct xrmm_attr {
+  const char* key;
+  int32_t kind;
+  int64_t i;
+  double f;
+  const char* s;
+} xrmm_attr;
+
+/* extended_operators.h:22-28 Request; `args` override `attrs` by key. */
+typedef struct xrmm_request {
+  const char* operation;
+  const xrmm_tensor* inputs;
+  int32_t n_inputs;
+  const xrmm_attr* attrs;
+  int32_t n_attrs;
+  const xrmm_attr* args;
+  int32_t n_args;
+  const xrmm_tensor* requested_outputs;
+  int32_t n_requested_outputs;
+} xrmm_request;
+
+/* operators.h:24-28 Options (defaults: no profiling, 15 s, 256 MiB). */
+typedef struct xrmm_options {
+  int32_t profiling;
+  uint64_t timeout_ns;
+  uint64_t memory_limit_bytes;
+} xrmm_options;
+
+/* A planned output: name, dtypes, shape and storage byte count. */
+typedef struct xrmm_tensor_desc {
+  char name[XRMM_NAME_MAX];
+  int32_t dtype;
+  int32_t storage_dtype;
+  int32_t rank;
+  int64_t shape[XRMM_MAX_RANK];
+  uint64_t nbytes;
+} xrmm_tensor_desc;
+
+typedef struct xrmm_op xrmm_op;
+
+/* Fill `o` with the reference defaults (operators.h:24-28). */
+void xrmm_default_options(xrmm_options* o);
+
+/* extended::plan (kernels/_shared/extended/planner.cpp:67, complex branch
+ * complex_plan.cpp:117-120, contract rows contract_data.h:722-751): contract
+ * validation, attribute defaults, output shapes. Metadata only, no device
+ * work. Writes up to `capacity` descriptors and the count to *n_outputs. */
+int xrmm_plan(const xrmm_request* request, xrmm_tensor_desc* outputs, int32_t capacity,
+              int32_t* n_outputs);
+
+/* Operator::prepare (kernels/_shared/extended/vulkan.cpp:119): plan, check the
+ * input byte counts and the memory limit, upload the inputs to the current
+ * HIP device and create the operator's stream. */
+int xrmm_prepare(const xrmm_request* request, const xrmm_options* options, xrmm_op** op);
+
+/* Operator::run (vulkan.cpp:115,120): launch and wait up to timeout_ns. A
+ * failure or time-out poisons the operator: later calls fail until close. */
+int xrmm_run(xrmm_op* op);
+
+/* Planned outputs of a prepared operator (same descriptors as xrmm_plan). */
+int xrmm_output_descs(const xrmm_op* op, xrmm_tensor_desc* outputs, int32_t capacity,
+                      int32_t* n_outputs);
+
+/* Operator::read_outputs (vulkan.cpp:121): copy output i into dst[i], which
+ * holds dst_bytes[i] bytes (exactly the descriptor's nbytes), converting to
+ * the requested storage dtype. */
+int xrmm_read_outputs(xrmm_op* op, void* const* dst, const uint64_t* dst_bytes, int32_t n);
+
+/* Operator::info (vulkan.cpp:123): JSON with backend, device, operation,
+ * closed, executed, execution_ms, gpu_ms, dispatch_count, persistent_bytes,
+ * kernel. The string stays valid until the next xrmm_info or xrmm_destroy. */
+const char* xrmm_info(xrmm_op* op);
+
+/* Operator::close (vulkan.cpp:122): wait for the stream and release device
+ * memory; the handle stays valid for xrmm_info until xrmm_destroy. */
+int xrmm_close(xrmm_op* op);
+
+/* Close (if open) and free the handle (the reference's destructor). */
+void xrmm_destroy(xrmm_op* op);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,12 +56,6 @@ def _sig(lib):
       _vp, _vp, _i64, _i64, _i64, _i32, _i32, _f32, _i32, _i32, _vp)
     s("xrmm_dequantize", ctypes.c_int, _vp, _vp, _vp, _i32, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp)
     s("xrmm_select_kernel", ctypes.c_char_p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32)
-    for name, fn in _EXTRA_SIGS:
-        if hasattr(lib, name):
-            fn(s)
-
-
-_EXTRA_SIGS: list = []
 
 
 def lib():

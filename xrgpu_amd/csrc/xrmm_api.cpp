@@ -74,6 +74,14 @@ int run(const xrmm::Launch& L, void* stream) {
 
 }  // namespace
 
+namespace xrmm {
+// Status reporting shared with the request-level lifecycle (xrmm_operator.cpp).
+int set_status(int code, const std::string& msg) {
+  g_error = code == XRMM_OK ? std::string() : msg;
+  return code;
+}
+}  // namespace xrmm
+
 extern "C" {
 
 const char* xrmm_last_error(void) { return g_error.c_str(); }

@@ -52,6 +52,9 @@ const char* kernel_name(Kernel k);
 // Enqueue the operator on `stream`. Returns hipSuccess or the launch error.
 hipError_t launch(const Launch& L, hipStream_t stream);
 
+// Record the status of an ABI call for xrmm_last_error ("" when XRMM_OK).
+int set_status(int code, const std::string& msg);
+
 // W [N, K] in out_dtype (see xrmm_dequantize).
 hipError_t launch_dequantize(const Launch& L, void* W, int out_dtype, hipStream_t stream);
 
