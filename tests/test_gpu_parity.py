@@ -93,11 +93,52 @@ FAST_CASES = [
 def test_gemv_fp16_parity(gpu, M, K, N, bs, zp, bias):
     rng = np.random.default_rng(M * 1000 + K + N + bs)
     A, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, np.float16, zp, bias)
+    want = "gemv_q4_dot" if M <= 4 else "gemv_q4_mfma"
     assert ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16,
-                               None if zp is None else ("packed" if zp == "packed" else "float")) == "gemv_q4_mfma"
+                               None if zp is None else ("packed" if zp == "packed" else "float")) == want
     Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
     ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs)
     assert_parity(Y, ref, np.float16)
+
+
+DOT_CASES = [
+    # M, K, N, bs, zp, bias: every chunk-round count (1, 2, 4, 8), rows 1..4,
+    # block sizes 16..128, every zero-point kind, K tails, N below one wave's
+    # columns and N not a multiple of a workgroup's
+    (1, 1024, 37, 32, None, False),          # 32 chunks: one round, half the lanes idle
+    (1, 2048, 64, 64, "packed", True),       # 64 chunks
+    (1, 4096, 1000, 32, None, False),        # the decode layout
+    (2, 4096, 129, 128, "packed", True),
+    (3, 8192, 70, 32, "float_int", True),    # 256 chunks: four rounds, rows padded to 4
+    (4, 14336, 33, 64, "packed", False),     # 448 chunks: eight rounds (down projection)
+    (4, 16384, 9, 32, None, True),           # 512 chunks, kb = 512
+    (1, 288, 17, 32, "packed", True),        # K tail inside the last chunk round
+    (2, 320, 5, 64, "float", False),         # K tail inside a block, float zero points
+    (1, 256, 1, 16, "packed", True),         # bs = 16: two blocks per chunk, N = 1
+    (4, 512, 23, 16, "float", True),
+    (1, 4096, 2, 32, None, False),
+]
+
+
+@pytest.mark.parametrize("M,K,N,bs,zp,bias", DOT_CASES)
+def test_gemv_dot_parity(gpu, M, K, N, bs, zp, bias):
+    rng = np.random.default_rng(M * 7919 + K + N + bs)
+    A, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, np.float16, zp, bias)
+    assert ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16,
+                               None if zp is None else ("packed" if zp == "packed" else "float")) == "gemv_q4_dot"
+    Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
+    ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs)
+    assert_parity(Y, ref, np.float16)
+
+
+def test_gemv_dot_float32_zero_points(gpu):
+    """T3 = float32 zero points with float16 activations (T3 is independent of T1)."""
+    rng = np.random.default_rng(77)
+    M, K, N, bs = 2, 1024, 40, 32
+    A, B, S, _, b = rand_case(rng, M, K, N, 4, bs, np.float16, None, True)
+    Z = rng.uniform(0, 15, (N, K // bs)).astype(np.float32)
+    Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
+    assert_parity(Y, O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs), np.float16)
 
 
 GEMM_CASES = [
@@ -326,7 +367,7 @@ def test_workload_cpu_f32_k2048(gpu):
 def test_workload_decode_up_m1(gpu):
     w = workloads.make("decode_up_m1")
     i, at = w["inputs"], w["attrs"]
-    assert ops().select_kernel("MatMulNBits", 1, at["K"], at["N"], 4, 32) == "gemv_q4_mfma"
+    assert ops().select_kernel("MatMulNBits", 1, at["K"], at["N"], 4, 32) == "gemv_q4_dot"
     y = host(_run_workload(w)[0])
     ref = O.matmul_nbits(i["aT"], i["bT"], i["scalesT"], K=at["K"], N=at["N"], block_size=32)
     assert_parity(y, ref, np.float16)

@@ -1,0 +1,446 @@
+// Decode GEMV for M <= 4 rows (fp16 activations, 4-bit weights): no LDS, no
+// barriers, each wave independent.
+//
+// Work split. A wave owns C consecutive output columns (a column is one row
+// of B: kb * blob bytes) and walks them in order. Its lanes split K: lane l
+// takes the 16-byte chunks l, l + 64, l + 128, ... of every column, so each
+// wave load instruction reads 1 KB of contiguous weights. Loads of the next P
+// columns are in flight while a column is computed, so arithmetic overlaps the
+// HBM stream instead of following it.
+//
+// Activations live in registers. Lane l needs the same 32 activations per
+// chunk for every column. The workgroup stages them once in LDS, already in
+// the nibble-pair order below and laid out so that a wave's 64 lanes read
+// consecutive 16-byte pieces (no bank conflicts), together with the per-chunk
+// activation sums; every wave then copies its lanes' pairs into registers.
+// Reads past K go through a buffer resource and return zero, so padding
+// contributes nothing.
+//
+// Arithmetic. A dword x of a chunk holds the codes c0..c7 of eight
+// consecutive k (low nibble first, complex_kernel.glsl:80). OR-ing masked
+// nibbles into the mantissa of 1024.0h gives exact binary16 values:
+//   (x & 0x000F000F) | 0x6400  -> (1024 + c0, 1024 + c4)
+//   (x & 0x00F000F0) | 0x6400  -> (1024 + 16 c1, 1024 + 16 c5)
+// and the same on x >> 8 for (c2, c6), (c3, c7). v_dot2_f32_f16 multiplies
+// these pairs with the matching activation pairs and accumulates in float32
+// (fp16 products are exact in float32). With P_lo / P_hi the two sums of a
+// chunk,
+//   sum_k c_k a_k = P_lo + P_hi / 16 - (1024 sum_lo a + 64 sum_hi a),
+// and the block's contribution is s * (sum_k c_k a_k - z * sum_k a_k). The
+// bracketed activation sums are per-lane constants computed once, so a chunk
+// costs 9 VALU per dword plus three per row. Integer-valued inputs stay exact
+// (every intermediate is an integer below 2^24).
+//
+// Reduction. Each lane ends a column with a partial sum per row; DPP steps
+// reduce within rows of 16 lanes and four readlanes finish the wave sum.
+#pragma once
+#include "xrmm_device.h"
+
+namespace xrmm {
+
+__device__ __forceinline__ f16x2 h2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
+
+__device__ __forceinline__ float dot2(uint32_t w, f16x2 a, float acc) {
+  return __builtin_amdgcn_fdot2(h2(w), a, acc, false);
+}
+
+// Row sums over 16-lane rows with DPP, then the four row sums combined through
+// readlane: every lane returns the wave total.
+__device__ __forceinline__ float wave_total(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)); // row_half_mirror
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)); // row_mirror
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// Offset past the end of every buffer resource: such loads return zero.
+constexpr uint32_t kOOB = 0x80000000u;
+
+// 16-byte pieces per lane of a wave's scale (or zero-point) block: the block
+// holds at most DOT_META_PIECES KB.
+constexpr int DOT_META_PIECES = 4;
+
+// Compact kernel arguments: every field is read in the kernel's first scalar
+// batch, before any branch, so a wave issues its first weight loads after a
+// single kernel-argument round trip.
+struct DotArgs {
+  const void* A;
+  const uint8_t* B;
+  const void* S;
+  const void* Z;
+  const void* bias;
+  void* Y;
+  uint32_t N, K, kb, rowb, zrow, M;
+  uint32_t bsl;         // log2(block_size)
+  uint32_t zesz;        // bytes per float zero point (2 or 4)
+  uint32_t meta_bytes;  // per-wave LDS bytes: C*kb*2 scales (+ C*zrow zero points), 16-aligned
+  uint32_t zoff;        // offset of the zero points inside a wave's LDS slice
+  uint32_t act_bytes;   // LDS bytes of the staged activation pairs and sums
+};
+
+// LDS bytes of the staged activations: pairs [MR][CPL][4][64] x 16 B, then the
+// sums [MR][CPL][SPC][2][64] x 4 B (negated bias, activation sum).
+template <int MR, int CPL, int SPC>
+__host__ __device__ constexpr uint32_t dot_act_bytes() {
+  return MR * CPL * 4 * 64 * 16 + MR * CPL * SPC * 2 * 64 * 4;
+}
+
+template <int ZPK, int SPC, int CPL, int C, int P, int MR, int W, int MP>
+__global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
+  static_assert(MP >= 1 && MP <= DOT_META_PIECES, "scale pieces");
+  constexpr int DPH = 4 / SPC;  // dwords per block of a chunk
+  constexpr uint32_t PAIRS = MR * CPL * 4 * 64 * 16;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t N = a.N, K = a.K, kb = a.kb, rowb = a.rowb, zrow = a.zrow;
+  const uint32_t nchunk = rowb >> 4;
+  const int M = static_cast<int>(a.M);
+  const uint32_t col0 = (blockIdx.x * W + wave) * C;
+  // Columns past N (the grid's last waves) are clamped for loading and never
+  // stored; no early exit, so no branch separates the argument loads.
+  auto clampc = [&](uint32_t c) { return c < N ? c : N - 1; };
+
+  // Issue order matters: the vector-memory counter retires loads in issue
+  // order, so the small loads the prologue consumes (scales / zero points of
+  // the wave's columns, activations) go first and the weight stream follows;
+  // waiting for the small loads then never waits for weights.
+
+  // ---- scales / zero points of the wave's C columns: contiguous blocks,
+  // 16 bytes per lane per load (bytes past a block read as zero)
+  const uint32_t c0 = clampc(col0);
+  const uint32_t sbytes = C * kb * 2u;
+  const uint32_t zbytes = ZPK == ZP_NONE ? 0u : C * zrow;
+  u32x4 sv[MP], zv[ZPK == ZP_NONE ? 1 : MP];
+  {
+    // The range check zeroes a whole dword that straddles the bound, so the
+    // bound is rounded up to 16 bytes. Tensors on this path start 16-byte
+    // aligned, so the rounded bound stays inside the aligned 16-byte block
+    // holding the tensor's last byte; the extra bytes are never used.
+    const rsrc_t rS = mk_rsrc(a.S, (N * kb * 2u + 15u) & ~15u);
+#pragma unroll
+    for (int q = 0; q < MP; ++q) {
+      const uint32_t o = lane * 16u + 1024u * q;
+      sv[q] = bld16_nt(rS, o < sbytes ? c0 * kb * 2u + o : kOOB, 0);  // predicated, no branch: a branch here costs a full wait
+    }
+    if constexpr (ZPK != ZP_NONE) {
+      const rsrc_t rZ = mk_rsrc(a.Z, (N * zrow + 15u) & ~15u);
+#pragma unroll
+      for (int q = 0; q < MP; ++q) {
+        const uint32_t o = lane * 16u + 1024u * q;
+        zv[q] = bld16_nt(rZ, o < zbytes ? c0 * zrow + o : kOOB, 0);
+      }
+    }
+  }
+
+  // Keep the issue order: the compiler may not move later loads ahead.
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- activations of the workgroup's staging items: item (m, j, l) is
+  // chunk l + 64 j of row m (32 activations, four 16-byte groups)
+  constexpr int ITEMS = MR * CPL * 64;
+  constexpr int IPT = (ITEMS + W * 64 - 1) / (W * 64);  // items per thread
+  const rsrc_t rA = mk_rsrc(a.A, static_cast<uint32_t>(M) * K * 2u);
+  u32x4 raw[IPT][4];
+#pragma unroll
+  for (int it = 0; it < IPT; ++it) {
+    const int item = tid + it * W * 64;
+    const int m = item / (CPL * 64), jl = item % (CPL * 64);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t k = static_cast<uint32_t>(jl) * 32u + 8u * g;
+      const bool ok = item < ITEMS && m < M && k < K;  // K % 8 == 0 on this path: groups are whole
+      raw[it][g] = bld16(rA, ok ? (static_cast<uint32_t>(m) * K + k) * 2u : kOOB, 0);
+    }
+  }
+
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- weights of the first P columns: the HBM stream
+  const rsrc_t rB = mk_rsrc(a.B, N * rowb);
+  uint32_t vb[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const uint32_t ch = static_cast<uint32_t>(lane + 64 * j);
+    vb[j] = (ch < nchunk ? ch : nchunk - 1) * 16u;  // past-the-row lanes reuse the last chunk (zero activations)
+  }
+  u32x4 wbuf[P + 1][CPL];
+  auto issue = [&](u32x4(&w)[CPL], uint32_t col) {
+    const uint32_t cb = clampc(col) * rowb;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) w[j] = bld16_nt(rB, vb[j], cb);
+  };
+#pragma unroll
+  for (int i = 0; i < P; ++i) issue(wbuf[i], col0 + i);
+
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- stage: this wave's scales / zero points into its own LDS slice, the
+  // workgroup's activations into pair order, plus the per-chunk constants
+  unsigned char* meta = smem + a.act_bytes + wave * a.meta_bytes;
+#pragma unroll
+  for (int q = 0; q < MP; ++q) {
+    const uint32_t o = lane * 16u + 1024u * q;
+    if (o < sbytes) *reinterpret_cast<u32x4*>(meta + o) = sv[q];
+    if (ZPK != ZP_NONE && o < zbytes) *reinterpret_cast<u32x4*>(meta + a.zoff + o) = zv[ZPK == ZP_NONE ? 0 : q];
+  }
+  {
+    const f16x2 c1024 = {static_cast<f16>(1024.f), static_cast<f16>(1024.f)};
+    const f16x2 c64 = {static_cast<f16>(64.f), static_cast<f16>(64.f)};
+    const f16x2 c1032 = {static_cast<f16>(1032.f), static_cast<f16>(1032.f)};
+    const f16x2 c72 = {static_cast<f16>(72.f), static_cast<f16>(72.f)};
+    const f16x2 c1 = {static_cast<f16>(1.f), static_cast<f16>(1.f)};
+#pragma unroll
+    for (int it = 0; it < IPT; ++it) {
+      const int item = tid + it * W * 64;
+      if (item < ITEMS) {
+        const int m = item / (CPL * 64), j = (item / 64) % CPL, l = item % 64;
+        f16x2 pr[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const u32x4 r = raw[it][g];  // halfs a0..a7 as dwords (a0,a1) (a2,a3) (a4,a5) (a6,a7)
+          pr[4 * g + 0] = h2(__builtin_amdgcn_perm(r[2], r[0], 0x05040100u));  // (a0, a4)
+          pr[4 * g + 1] = h2(__builtin_amdgcn_perm(r[2], r[0], 0x07060302u));  // (a1, a5)
+          pr[4 * g + 2] = h2(__builtin_amdgcn_perm(r[3], r[1], 0x05040100u));  // (a2, a6)
+          pr[4 * g + 3] = h2(__builtin_amdgcn_perm(r[3], r[1], 0x07060302u));  // (a3, a7)
+          *reinterpret_cast<u32x4*>(smem + (((m * CPL + j) * 4 + g) * 64 + l) * 16) =
+              u32x4{__builtin_bit_cast(uint32_t, pr[4 * g]), __builtin_bit_cast(uint32_t, pr[4 * g + 1]),
+                    __builtin_bit_cast(uint32_t, pr[4 * g + 2]), __builtin_bit_cast(uint32_t, pr[4 * g + 3])};
+        }
+        // -(1024 sum_lo a + 64 sum_hi a) [- 8 sum a when z is implicit] and sum a,
+        // per block half; four partial chains keep the dependency depth short
+#pragma unroll
+        for (int h = 0; h < SPC; ++h) {
+          float b[4] = {0.f, 0.f, 0.f, 0.f}, t[2] = {0.f, 0.f};
+#pragma unroll
+          for (int e = 4 * DPH * h; e < 4 * DPH * (h + 1); ++e) {
+            const f16x2 w = ZPK == ZP_NONE ? ((e & 1) ? c72 : c1032) : ((e & 1) ? c64 : c1024);
+            b[e & 3] = __builtin_amdgcn_fdot2(pr[e], w, b[e & 3], false);
+            if constexpr (ZPK != ZP_NONE) t[e & 1] = __builtin_amdgcn_fdot2(pr[e], c1, t[e & 1], false);
+          }
+          float* sums = reinterpret_cast<float*>(smem + PAIRS) + (((m * CPL + j) * SPC + h) * 2) * 64 + l;
+          sums[0] = -((b[0] + b[1]) + (b[2] + b[3]));
+          sums[64] = t[0] + t[1];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- this lane's activation pairs and constants, into registers
+  f16x2 ap[MR][CPL][16];
+  float nbias[MR][CPL][SPC], asum[MR][CPL][SPC];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(smem + (((m * CPL + j) * 4 + g) * 64 + lane) * 16);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ap[m][j][4 * g + e] = h2(v[e]);
+      }
+#pragma unroll
+      for (int h = 0; h < SPC; ++h) {
+        const float* sums = reinterpret_cast<const float*>(smem + PAIRS) + (((m * CPL + j) * SPC + h) * 2) * 64 + lane;
+        nbias[m][j][h] = sums[0];
+        asum[m][j][h] = sums[64];
+      }
+    }
+
+  // per-lane LDS offsets of the scale / zero point of chunk round j
+  uint32_t ls[CPL], lz[CPL], zsh[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const uint32_t ch = static_cast<uint32_t>(lane + 64 * j);
+    const uint32_t chc = ch < nchunk ? ch : nchunk - 1;
+    const uint32_t b = SPC == 1 ? (chc * 32u) >> a.bsl : 2u * chc;  // first block of the chunk
+    ls[j] = b * 2u;
+    lz[j] = ZPK == ZP_PACKED ? (b >> 1) : b * a.zesz;
+    zsh[j] = (b & 1u) * 4u;
+  }
+
+  const f16* biasp = static_cast<const f16*>(a.bias);
+  f16* Y = static_cast<f16*>(a.Y);
+  float out[MR];  // lane i < C keeps column col0 + i
+#pragma unroll
+  for (int m = 0; m < MR; ++m) out[m] = 0.f;
+
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    if (col0 + i >= N) break;  // wave-uniform, after the loads are in flight
+    if (i + P < C) issue(wbuf[(i + P) % (P + 1)], col0 + i + P);
+    const u32x4(&w)[CPL] = wbuf[i % (P + 1)];
+    const unsigned char* ms = meta + i * kb * 2u;
+    const unsigned char* mz = meta + a.zoff + i * zrow;
+    float y[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) y[m] = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const uint32_t magic = 0x64006400u;
+      uint32_t lo[8], hi[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t x = w[j][q], x8 = x >> 8;
+        lo[2 * q] = and_or(x, 0x000F000Fu, magic);
+        hi[2 * q] = and_or(x, 0x00F000F0u, magic);
+        lo[2 * q + 1] = and_or(x8, 0x000F000Fu, magic);
+        hi[2 * q + 1] = and_or(x8, 0x00F000F0u, magic);
+      }
+      uint32_t zb = 0;
+      if constexpr (ZPK == ZP_PACKED) zb = mz[lz[j]];
+#pragma unroll
+      for (int h = 0; h < SPC; ++h) {
+        const float s = static_cast<float>(*reinterpret_cast<const f16*>(ms + ls[j] + 2u * h));
+        float z = 0.f;
+        if constexpr (ZPK == ZP_PACKED) {
+          z = static_cast<float>((zb >> (SPC == 1 ? zsh[j] : 4u * h)) & 15u);
+        } else if constexpr (ZPK == ZP_FLOAT) {
+          z = a.zesz == 4 ? *reinterpret_cast<const float*>(mz + lz[j] + 4u * h)
+                          : static_cast<float>(*reinterpret_cast<const f16*>(mz + lz[j] + 2u * h));
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          float pl = nbias[m][j][h], ph = 0.f;
+#pragma unroll
+          for (int q = DPH * h; q < DPH * (h + 1); ++q) {
+            pl = dot2(lo[2 * q], ap[m][j][4 * q + 0], pl);
+            ph = dot2(hi[2 * q], ap[m][j][4 * q + 1], ph);
+            pl = dot2(lo[2 * q + 1], ap[m][j][4 * q + 2], pl);
+            ph = dot2(hi[2 * q + 1], ap[m][j][4 * q + 3], ph);
+          }
+          float t = __builtin_fmaf(ph, 0.0625f, pl);
+          if constexpr (ZPK != ZP_NONE) t = __builtin_fmaf(-z, asum[m][j][h], t);
+          y[m] = __builtin_fmaf(s, t, y[m]);
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float tot = wave_total(y[m]);
+      out[m] = lane == i ? tot : out[m];
+    }
+  }
+
+  // lane i < C writes column col0 + i
+  const uint32_t mycol = col0 + static_cast<uint32_t>(lane);
+  if (lane < C && mycol < N) {
+    const float b = biasp ? static_cast<float>(biasp[mycol]) : 0.f;
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      if (m < M) Y[static_cast<uint32_t>(m) * N + mycol] = static_cast<f16>(out[m] + b);
+  }
+}
+
+// Host side: argument block for a geometry and C columns per wave, and the
+// workgroup's LDS bytes.
+inline DotArgs dot_args(const Launch& L, int C, uint32_t act_bytes) {
+  const Proj& P = L.p[0];
+  DotArgs a;
+  a.A = L.A;
+  a.B = P.B;
+  a.S = P.scales;
+  a.Z = P.zp;
+  a.bias = P.bias;
+  a.Y = P.Y;
+  a.N = static_cast<uint32_t>(P.N);
+  a.K = static_cast<uint32_t>(L.K);
+  a.kb = static_cast<uint32_t>(L.kb);
+  a.rowb = static_cast<uint32_t>(L.kb * L.blob);
+  a.zesz = L.zp_dtype == DT_F32 ? 4u : 2u;
+  a.zrow = L.zp_kind == ZP_PACKED ? static_cast<uint32_t>(L.zrow) : a.kb * a.zesz;
+  a.M = static_cast<uint32_t>(L.M);
+  a.bsl = static_cast<uint32_t>(L.bs_log2);
+  const uint32_t sb = static_cast<uint32_t>(C) * a.kb * 2u;
+  a.zoff = (sb + 15u) & ~15u;
+  const uint32_t zb = L.zp_kind == ZP_NONE ? 0u : static_cast<uint32_t>(C) * a.zrow;
+  a.meta_bytes = (a.zoff + zb + 15u) & ~15u;
+  a.act_bytes = act_bytes;
+  return a;
+}
+
+inline size_t dot_lds_bytes(const DotArgs& a, int W) { return a.act_bytes + static_cast<size_t>(W) * a.meta_bytes; }
+
+// Launch shape of the dot GEMV (measured on the decode workload: 2 columns
+// per wave, one column prefetched, 4 waves per workgroup).
+constexpr int DOT_C = 2, DOT_P = 1, DOT_W = 4;
+
+// Chunk rounds per lane (a power of two >= ceil(chunks / 64)) and rows (1, 2
+// or 4) the dot GEMV is instantiated for; 0 when it does not apply.
+inline int dot_cpl(const Launch& L) {
+  const int64_t chunks = L.kb * L.blob / 16;
+  for (int c = 1; c <= 8; c *= 2)
+    if (chunks <= 64 * c) return c;
+  return 0;
+}
+
+inline int dot_mr(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 0; }
+
+// 16-byte pieces per lane that a wave's scale / zero-point block needs: 1 or
+// DOT_META_PIECES (0 if the block is larger).
+inline int dot_meta_pieces(const Launch& L) {
+  const int64_t sb = DOT_C * L.kb * 2;
+  const int64_t zb = L.zp_kind == ZP_PACKED ? DOT_C * L.zrow
+                     : L.zp_kind == ZP_FLOAT ? DOT_C * L.kb * (L.zp_dtype == DT_F32 ? 4 : 2) : 0;
+  const int64_t mx = sb > zb ? sb : zb;
+  return mx <= 1024 ? 1 : mx <= 1024 * DOT_META_PIECES ? DOT_META_PIECES : 0;
+}
+
+inline bool dot_meta_fits(const Launch& L) { return dot_meta_pieces(L) != 0; }
+
+template <int ZPK, int SPC, int CPL, int MR, int MP>
+inline hipError_t launch_dot5(const Launch& L, hipStream_t st) {
+  const DotArgs a = dot_args(L, DOT_C, dot_act_bytes<MR, CPL, SPC>());
+  const uint32_t per = DOT_W * DOT_C;
+  const uint32_t grid = static_cast<uint32_t>((L.p[0].N + per - 1) / per);
+  const size_t lds = dot_lds_bytes(a, DOT_W);
+  auto kern = k_gemv_dot<ZPK, SPC, CPL, DOT_C, DOT_P, MR, DOT_W, MP>;
+  if (lds > 64 * 1024) {
+    static bool raised = false;  // per instantiation
+    if (!raised) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(160 * 1024 - 1024));
+      (void)hipGetLastError();
+      raised = true;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(DOT_W * 64), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int ZPK, int SPC, int CPL, int MR>
+inline hipError_t launch_dot4(const Launch& L, hipStream_t st) {
+  return dot_meta_pieces(L) == 1 ? launch_dot5<ZPK, SPC, CPL, MR, 1>(L, st)
+                                 : launch_dot5<ZPK, SPC, CPL, MR, DOT_META_PIECES>(L, st);
+}
+
+template <int ZPK, int SPC, int CPL>
+inline hipError_t launch_dot3(const Launch& L, hipStream_t st) {
+  switch (dot_mr(L.M)) {
+    case 1: return launch_dot4<ZPK, SPC, CPL, 1>(L, st);
+    case 2: return launch_dot4<ZPK, SPC, CPL, 2>(L, st);
+    default: return launch_dot4<ZPK, SPC, CPL, 4>(L, st);
+  }
+}
+
+template <int ZPK, int SPC>
+inline hipError_t launch_dot2(const Launch& L, hipStream_t st) {
+  switch (dot_cpl(L)) {
+    case 1: return launch_dot3<ZPK, SPC, 1>(L, st);
+    case 2: return launch_dot3<ZPK, SPC, 2>(L, st);
+    case 4: return launch_dot3<ZPK, SPC, 4>(L, st);
+    default: return launch_dot3<ZPK, SPC, 8>(L, st);
+  }
+}
+
+// Entry of one zero-point kind (defined in xrmm_gemv_dot_zp.hip).
+template <int ZPK>
+hipError_t launch_dot_for(const Launch& L, hipStream_t st);
+
+}  // namespace xrmm

@@ -24,6 +24,7 @@
 // the exponent-bias trick: OR-ing a nibble into the mantissa of 1024.0h gives
 // 1024 + code exactly (and 1024 + 16*code for the high nibble of a byte).
 #include "xrmm_gemv.h"
+#include "xrmm_gemv_dot.h"
 
 namespace xrmm {
 
@@ -271,6 +272,7 @@ static bool q4_fast_ok(const Launch& L) {
 
 Kernel select_kernel(const Launch& L) {
   if (q4_fast_ok(L) && fits_i32(L)) {
+    if (L.op == OP_MATMUL && L.M >= 1 && dot_mr(L.M) != 0 && dot_cpl(L) != 0 && dot_meta_fits(L)) return K_GEMV_DOT;
     if (L.M >= 1 && L.M <= 16 && gemv_tiles(L) != 0) return K_GEMV_Q4;
     if (L.M > 16 && L.op == OP_MATMUL && L.zp_kind != ZP_FLOAT) return K_GEMM_Q4;
   }
@@ -280,6 +282,7 @@ Kernel select_kernel(const Launch& L) {
 const char* kernel_name(Kernel k) {
   switch (k) {
     case K_GEMV_Q4: return "gemv_q4_mfma";
+    case K_GEMV_DOT: return "gemv_q4_dot";
     case K_GEMM_Q4: return "gemm_q4_mfma";
     default: return "generic";
   }
@@ -310,6 +313,11 @@ hipError_t launch(const Launch& L, hipStream_t st) {
   Kernel k = select_kernel(L);
   const int zpk = effective_zpk(L);
   if (zpk < 0) k = K_GENERIC;  // mixed presence of zero points
+  if (k == K_GEMV_DOT) {
+    if (zpk == ZP_NONE) return launch_dot_for<ZP_NONE>(L, st);
+    if (zpk == ZP_PACKED) return launch_dot_for<ZP_PACKED>(L, st);
+    return launch_dot_for<ZP_FLOAT>(L, st);
+  }
   if (k == K_GEMV_Q4) {
     if (zpk == ZP_NONE) return launch_gemv_for<ZP_NONE>(L, st);
     if (zpk == ZP_PACKED) return launch_gemv_for<ZP_PACKED>(L, st);
