@@ -53,7 +53,10 @@ def test_qkv_requires_norm_scale():
     (0, 1, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_dot"),
     (0, 4, 4096, 14336, 64, nat.F16, nat.U8, "gemv_q4_dot"),
     (0, 8, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),
-    (0, 2048, 4096, 14336, 128, nat.F16, nat.U8, "gemm_q4_mfma"),
+    (0, 2048, 4096, 14336, 128, nat.F16, nat.U8, "gemm_q4_big"),
+    (0, 128, 4096, 14336, 32, nat.F16, nat.F16, "gemm_q4_big"),
+    (0, 127, 4096, 14336, 32, nat.F16, nat.U8, "gemm_q4_mfma"),
+    (0, 64, 4096, 14336, 32, nat.F16, nat.F16, "generic"),
     (1, 4, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_mfma"),
     (2, 16, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),
     (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "generic"),

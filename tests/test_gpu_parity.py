@@ -142,11 +142,11 @@ def test_gemv_dot_float32_zero_points(gpu):
 
 
 GEMM_CASES = [
+    # M, K, N, bs, zp, bias: 17 <= M < 128 runs the 128 x 128 GEMM
     (17, 256, 64, 32, None, False),
     (64, 512, 130, 32, "packed", True),
-    (200, 1024, 256, 128, "packed", True),
-    (129, 320, 100, 64, None, False),
     (96, 288, 40, 32, "packed", True),   # K tail
+    (127, 1024, 256, 128, "packed", True),
 ]
 
 
@@ -159,6 +159,58 @@ def test_gemm_fp16_parity(gpu, M, K, N, bs, zp, bias):
     Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
     ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs)
     assert_parity(Y, ref, np.float16)
+
+
+BIG_CASES = [
+    # M, K, N, bs, zp, bias for the 256 x 256 GEMM (M >= 128): whole tiles,
+    # partial row and column tiles, odd and even K-step counts (the loop runs
+    # steps in pairs), K tails inside a block and inside a step, block sizes
+    # 16 (two blocks per chunk) to 128, every zero-point kind
+    (256, 4096, 512, 128, "packed", True),   # whole tiles, 64 steps
+    (128, 288, 40, 32, "packed", True),      # 5 steps (odd), K tail inside the last step
+    (300, 576, 300, 32, None, False),        # 9 steps, partial tiles both ways
+    (513, 256, 257, 16, "packed", False),    # bs = 16, one row and one column past a tile
+    (130, 200, 33, 32, "packed", True),      # K = 200 inside a block: kb = 7, 4 steps
+    (160, 1024, 96, 64, "float_int", True),  # float zero points with integer values
+    (140, 512, 72, 128, "float", False),     # float zero points of any value
+    (129, 320, 100, 64, None, False),
+    (200, 1024, 256, 128, "packed", True),
+]
+
+
+@pytest.mark.parametrize("M,K,N,bs,zp,bias", BIG_CASES)
+def test_gemm_big_parity(gpu, M, K, N, bs, zp, bias):
+    rng = np.random.default_rng(M * 31 + K + N + bs)
+    A, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, np.float16, zp, bias)
+    kind = None if zp is None else ("packed" if zp == "packed" else "float")
+    assert ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16, kind) == "gemm_q4_big"
+    Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
+    ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs)
+    assert_parity(Y, ref, np.float16)
+
+
+def test_gemm_big_float32_zero_points(gpu):
+    """T3 = float32 zero points with float16 activations on the 256 x 256 GEMM."""
+    rng = np.random.default_rng(78)
+    M, K, N, bs = 192, 1024, 80, 32
+    A, B, S, _, b = rand_case(rng, M, K, N, 4, bs, np.float16, None, True)
+    Z = rng.uniform(0, 15, (N, K // bs)).astype(np.float32)
+    Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
+    assert_parity(Y, O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs), np.float16)
+
+
+def test_gemm_big_repeat_and_rows_independent(gpu):
+    """Two launches give identical bytes, and row r of a 384-row product equals
+    the same row computed within a 128-row product (rows never mix)."""
+    rng = np.random.default_rng(79)
+    M, K, N, bs = 384, 512, 200, 32
+    A, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, np.float16, "packed", True)
+    args = (dev(B), dev(S), dev(Z), dev(b))
+    y1 = host(ops().matmul_nbits(dev(A), *args, K=K, N=N, block_size=bs))
+    y2 = host(ops().matmul_nbits(dev(A), *args, K=K, N=N, block_size=bs))
+    assert np.array_equal(y1.view(np.uint16), y2.view(np.uint16))
+    y3 = host(ops().matmul_nbits(dev(A[256:]), *args, K=K, N=N, block_size=bs))
+    assert np.array_equal(y1[256:].view(np.uint16), y3.view(np.uint16))
 
 
 GENERIC_CASES = [
@@ -399,7 +451,7 @@ def test_workload_prefill_m2048_row_sample(gpu):
     96 rows (plus the first and last) is checked against the oracle."""
     w = workloads.make("prefill_m2048")
     i, at = w["inputs"], w["attrs"]
-    assert ops().select_kernel("MatMulNBits", 2048, at["K"], at["N"], 4, 128, zp="packed") == "gemm_q4_mfma"
+    assert ops().select_kernel("MatMulNBits", 2048, at["K"], at["N"], 4, 128, zp="packed") == "gemm_q4_big"
     y = host(_run_workload(w)[0])
     rows = np.unique(np.concatenate([[0, 2047], np.random.default_rng(9).choice(2048, 96, replace=False)]))
     ref = O.matmul_nbits(i["aT"][rows], i["bT"], i["scalesT"], i["zeroPointsT"], i["biasT"], K=at["K"], N=at["N"],

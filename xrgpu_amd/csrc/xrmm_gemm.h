@@ -1,0 +1,235 @@
+// Prefill GEMM (M > 16): fp16 activations x 4-bit weights dequantised to fp16
+// in LDS, v_mfma_f32_32x32x16_f16 with float32 accumulation.
+//
+// Tiling. A workgroup of 8 waves (two per SIMD) owns a 256 x 256 output tile;
+// wave (wm, wn) owns rows 64 wm .. + 63 and columns 128 wn .. + 127 as 2 x 4
+// MFMA tiles of 32 x 32 (128 accumulator registers per lane, so two waves fit
+// a SIMD and the hardware interleaves one wave's dequantisation and LDS work
+// with the other's MFMAs). The 32x32x16 form is used because it reaches the
+// matrix cores' full fp16 rate on gfx950; the 16x16x32 form does not.
+//
+// Pipeline. K advances in steps of 64 over a double-buffered LDS. Global loads
+// run two steps ahead into two register sets (each thread: four 16-byte pieces
+// of the activation tile, one 16-byte chunk of one weight column and its raw
+// scale / zero-point bits), so a load has two steps of MFMAs to arrive before
+// its data is written to LDS. The weights are dequantised on the way into LDS
+// with the same routine and pair order as the GEMV and xrmm_dequantize;
+// fragments of the next K slice are read before the current slice's MFMAs.
+// One barrier per step separates the stages.
+#pragma once
+#include "xrmm_device.h"
+
+namespace xrmm {
+
+constexpr int GB_M = 256, GB_N = 256, GB_K = 64, GB_T = 512;
+constexpr int GB_LD = GB_K + 8;                      // halfs per staged row (pad spreads banks)
+constexpr int GB_STAGE = (GB_M + GB_N) * GB_LD;      // halfs per pipeline stage
+constexpr size_t GB_LDS = 2 * GB_STAGE * sizeof(_Float16);  // two stages: 147,456 bytes
+constexpr int GB_TM = 2, GB_TN = 4;                  // 32x32 MFMA tiles per wave
+
+// Global-load registers of one K step.
+template <int SPC>
+struct GbRegs {
+  u32x4 a[4];        // activations: pieces tid + 512 i of the 256 x 64 tile
+  u32x4 b;           // column n0 + tid / 2, chunk 2 ks + tid % 2
+  uint32_t s[SPC];   // raw scale bits per block half
+  uint32_t z[SPC];   // raw zero-point bits (packed: the byte)
+};
+
+template <int ZPK, int SPC>
+__global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big(Launch L) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  f16* lds = reinterpret_cast<f16*>(smem);
+  constexpr uint32_t OOB = 0x80000000u;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const Proj& P = L.p[0];
+  const int M = static_cast<int>(L.M), N = static_cast<int>(P.N), K = static_cast<int>(L.K);
+  const int m0 = static_cast<int>(blockIdx.y) * GB_M, n0 = static_cast<int>(blockIdx.x) * GB_N;
+  const int Kp = static_cast<int>(L.kb * L.block_size);
+  const uint32_t rowb = static_cast<uint32_t>(Kp / 2);
+  const int nchunk = static_cast<int>(rowb / 16);
+  const int ksteps = (Kp + GB_K - 1) / GB_K;
+  const uint32_t kb = static_cast<uint32_t>(L.kb);
+
+  const rsrc_t rA = mk_rsrc(L.A, static_cast<uint32_t>(M) * static_cast<uint32_t>(K) * 2u);
+  // Thread t loads half h = t % 2 of column n0 + t / 2 each step. Its offsets
+  // are past every resource bound when the column does not exist, so loads
+  // return zero with no per-step select (a divergent select would become a
+  // branch around the load).
+  const int bc = tid >> 1, bh = tid & 1;
+  const int bn = n0 + bc;
+  const bool bnval = bn < N;
+  const uint32_t zrow = ZPK == ZP_PACKED ? static_cast<uint32_t>(L.zrow) : kb * (L.zp_dtype == DT_F32 ? 4u : 2u);
+  const rsrc_t rB = mk_rsrc(P.B, static_cast<uint32_t>(N) * rowb);
+  // scale / zero-point bounds rounded to 16 bytes: the range check zeroes a
+  // whole dword straddling the bound, and 16-byte aligned tensors keep the
+  // rounded bound inside the block holding their last byte
+  const rsrc_t rS = mk_rsrc(P.scales, (static_cast<uint32_t>(N) * kb * 2u + 15u) & ~15u);
+  const rsrc_t rZ = mk_rsrc(P.zp ? P.zp : P.scales, (static_cast<uint32_t>(N) * zrow + 15u) & ~15u);
+  const uint32_t bcol = bnval ? static_cast<uint32_t>(bn) * rowb : OOB;
+  const uint32_t scol = bnval ? static_cast<uint32_t>(bn) * kb * 2u : OOB;
+  const uint32_t zcol = bnval ? static_cast<uint32_t>(bn) * zrow : OOB;
+
+  auto gload = [&](GbRegs<SPC>& r, int ks) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = tid + GB_T * i, row = p >> 3, grp = p & 7;
+      const int m = m0 + row, k = ks * GB_K + grp * 8;
+      const bool ok = m < M && k < K;  // K % 8 == 0: groups are whole
+      r.a[i] = bld16(rA, ok ? static_cast<uint32_t>(m * K + k) * 2u : OOB, 0);
+    }
+    const int ch = ks * 2 + bh;
+    const uint32_t past = ch < nchunk ? 0u : OOB;
+    r.b = bld16(rB, bcol + past + static_cast<uint32_t>(ch) * 16u, 0);
+#pragma unroll
+    for (int q = 0; q < SPC; ++q) {
+      const uint32_t b = static_cast<uint32_t>(ch * 32 + q * 16) >> L.bs_log2;  // block of this half-chunk
+      r.s[q] = bld_u16(rS, scol + past + b * 2u, 0);
+      if constexpr (ZPK == ZP_PACKED) r.z[q] = bld_u8(rZ, zcol + past + (b >> 1), 0);
+      else if constexpr (ZPK == ZP_FLOAT)
+        r.z[q] = L.zp_dtype == DT_F32 ? bld_u32(rZ, zcol + past + b * 4u, 0) : bld_u16(rZ, zcol + past + b * 2u, 0);
+    }
+  };
+  // Metadata of the chunk held in r (step ks): the scale and zero point of each
+  // 16-code half, as the constants the dequantisation uses.
+  struct StepMeta {
+    Dq c[SPC];
+    float z[SPC], s[SPC];
+  };
+  auto meta = [&](const GbRegs<SPC>& r, int ks) {
+    StepMeta mt;
+#pragma unroll
+    for (int q = 0; q < SPC; ++q) {
+      const f16 sc = __builtin_bit_cast(f16, static_cast<uint16_t>(r.s[q]));
+      float z;
+      if constexpr (ZPK == ZP_NONE) {
+        z = 8.f;
+      } else if constexpr (ZPK == ZP_PACKED) {
+        const uint32_t b = static_cast<uint32_t>((ks * 2 + bh) * 32 + q * 16) >> L.bs_log2;
+        z = static_cast<float>((r.z[q] >> ((b & 1u) * 4u)) & 15u);
+      } else {
+        z = L.zp_dtype == DT_F32 ? __builtin_bit_cast(float, r.z[q])
+                                 : static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(r.z[q])));
+      }
+      mt.z[q] = z;
+      mt.s[q] = static_cast<float>(sc);
+      if constexpr (ZPK != ZP_FLOAT) mt.c[q] = dq_consts(z, sc);
+    }
+    return mt;
+  };
+  // Part d (0..3) of writing a step's registers to LDS stage `stage`:
+  // activation piece d and weight dword d (codes 8 d .. 8 d + 7 of the chunk).
+  auto store_part = [&](const GbRegs<SPC>& r, const StepMeta& mt, int stage, int d) {
+    f16* As = lds + stage * GB_STAGE;
+    f16* Bs = As + GB_M * GB_LD;
+    const int p = tid + GB_T * d, row = p >> 3, grp = p & 7;
+    *reinterpret_cast<f16x8*>(As + row * GB_LD + grp * 8) = pair_order(__builtin_bit_cast(f16x8, r.a[d]));
+    const int q = d / (4 / SPC);
+    f16x8 b;
+    if constexpr (ZPK == ZP_FLOAT) b = dq8_f32z(r.b[d], mt.z[q], mt.s[q]);
+    else b = dq8(r.b[d], mt.c[q]);
+    *reinterpret_cast<f16x8*>(Bs + bc * GB_LD + bh * 32 + d * 8) = b;
+  };
+
+  f32x16 acc[GB_TM][GB_TN];
+#pragma unroll
+  for (int i = 0; i < GB_TM; ++i)
+#pragma unroll
+    for (int j = 0; j < GB_TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Fragments of K slice kk (0..3) of a stage: lane (r, g) = (lane % 32,
+  // lane / 32) reads row / column r, k = 16 kk + 8 g .. + 7.
+  f16x8 fa[2][GB_TM], fb[2][GB_TN];
+  auto read_frags = [&](int stage, int kk, int buf) {
+    const int ko = kk * 16 + (lane >> 5) * 8;
+    const f16* As = lds + stage * GB_STAGE + (wm * 64 + (lane & 31)) * GB_LD + ko;
+    const f16* Bs = lds + stage * GB_STAGE + (GB_M + wn * 128 + (lane & 31)) * GB_LD + ko;
+#pragma unroll
+    for (int i = 0; i < GB_TM; ++i) fa[buf][i] = *reinterpret_cast<const f16x8*>(As + i * 32 * GB_LD);
+#pragma unroll
+    for (int j = 0; j < GB_TN; ++j) fb[buf][j] = *reinterpret_cast<const f16x8*>(Bs + j * 32 * GB_LD);
+  };
+  auto mfmas = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < GB_TN; ++j)
+#pragma unroll
+      for (int i = 0; i < GB_TM; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0);
+  };
+  // One K step on LDS stage `stage`: `fill` receives step ks + 2 (its previous
+  // contents, step ks, are already in LDS) and `nxt` (step ks + 1, loaded a step
+  // earlier) is written to the other stage in four parts, one beside each K
+  // slice's MFMAs, so the dequantisation overlaps the matrix cores. Steps past
+  // the last one load with offsets beyond every bound (zeros) and write a stage
+  // nothing reads, so the step has no branches.
+  auto step = [&](int ks, int stage, GbRegs<SPC>& nxt, GbRegs<SPC>& fill) {
+    gload(fill, ks + 2);
+    const StepMeta mt = meta(nxt, ks + 1);
+#pragma unroll
+    for (int kk = 0; kk < GB_K / 16; ++kk) {
+      if (kk + 1 < GB_K / 16) read_frags(stage, kk + 1, (kk + 1) & 1);
+      store_part(nxt, mt, stage ^ 1, kk);
+      mfmas(kk & 1);
+    }
+    __syncthreads();
+    read_frags(stage ^ 1, 0, 0);
+  };
+
+  GbRegs<SPC> r0, r1;
+  gload(r0, 0);
+  gload(r1, 1);
+  {
+    const StepMeta mt = meta(r0, 0);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) store_part(r0, mt, 0, d);
+  }
+  __syncthreads();
+  read_frags(0, 0, 0);
+  int ks = 0;
+  for (; ks + 1 < ksteps; ks += 2) {
+    step(ks, 0, r1, r0);      // r1 holds step ks + 1, r0 receives ks + 2
+    step(ks + 1, 1, r0, r1);  // r0 holds step ks + 2, r1 receives ks + 3
+  }
+  if (ks < ksteps) step(ks, 0, r1, r0);
+
+  // epilogue: lane holds D[8 (e / 4) + 4 (lane / 32) + e % 4][lane % 32] of each 32x32 tile
+  const f16* biasp = static_cast<const f16*>(P.bias);
+  f16* Y = static_cast<f16*>(P.Y);
+#pragma unroll
+  for (int j = 0; j < GB_TN; ++j) {
+    const int n = n0 + wn * 128 + j * 32 + (lane & 31);
+    if (n >= N) continue;
+    const float bias = biasp ? static_cast<float>(biasp[n]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < GB_TM; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (m < M) Y[static_cast<int64_t>(m) * N + n] = static_cast<f16>(acc[i][j][e] + bias);
+      }
+    }
+  }
+}
+
+template <int ZPK, int SPC>
+inline hipError_t launch_gemm_big(const Launch& L, hipStream_t st) {
+  auto kern = k_gemm_q4_big<ZPK, SPC>;
+  // more than 64 KB of dynamic LDS needs the attribute; set once per instantiation
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     static_cast<int>(GB_LDS));
+  if (attr != hipSuccess) return attr;
+  const dim3 grid(static_cast<uint32_t>((L.p[0].N + GB_N - 1) / GB_N), static_cast<uint32_t>((L.M + GB_M - 1) / GB_M));
+  hipLaunchKernelGGL(kern, grid, dim3(GB_T), GB_LDS, st, L);
+  return hipGetLastError();
+}
+
+// Defined once per zero-point kind (xrmm_gemm_zp.hip).
+template <int ZPK>
+hipError_t launch_gemm_big_for(const Launch& L, hipStream_t st);
+
+}  // namespace xrmm

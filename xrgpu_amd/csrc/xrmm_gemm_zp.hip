@@ -1,0 +1,16 @@
+// One zero-point kind of the prefill GEMM; the build compiles this file once
+// per kind with -DXRMM_ZPK=<0|1|2>.
+#include "xrmm_gemm.h"
+
+#ifndef XRMM_ZPK
+#error "XRMM_ZPK must be defined"
+#endif
+
+namespace xrmm {
+
+template <>
+hipError_t launch_gemm_big_for<XRMM_ZPK>(const Launch& L, hipStream_t st) {
+  return L.block_size >= 32 ? launch_gemm_big<XRMM_ZPK, 1>(L, st) : launch_gemm_big<XRMM_ZPK, 2>(L, st);
+}
+
+}  // namespace xrmm

@@ -11,9 +11,11 @@
 //                are dequantised in registers to fp16 and multiplied on
 //                v_mfma_f32_16x16x32_f16 against the activations staged once
 //                in LDS. Qkv/Mlp fuse the RMS prologue and the SwiGLU epilogue.
-//  * k_gemm_q4   M > 16, fp16, 4-bit. LDS-tiled MFMA GEMM: activation tiles and
-//                weight tiles dequantised to fp16 are staged in LDS and fed to
-//                v_mfma_f32_32x32x16_f16.
+//  * k_gemm_q4   16 < M < 128, fp16, 4-bit. LDS-tiled MFMA GEMM with 128 x 128
+//                tiles: activation tiles and weight tiles dequantised to fp16
+//                are staged in LDS and fed to v_mfma_f32_32x32x16_f16.
+//  * k_gemm_q4_big  M >= 128, fp16, 4-bit (xrmm_gemm.h): 256 x 256 tiles on
+//                eight waves, dequantisation interleaved with the MFMAs.
 //  * k_generic   every other geometry (fp32, 2/8-bit, float zero points with a
 //                non-fast block size, unaligned tensors): one wave per column
 //                and row block, the reference's float32 weight formula.
@@ -25,6 +27,7 @@
 // 1024 + code exactly (and 1024 + 16*code for the high nibble of a byte).
 #include "xrmm_gemv.h"
 #include "xrmm_gemv_dot.h"
+#include "xrmm_gemm.h"
 
 namespace xrmm {
 
@@ -270,10 +273,15 @@ static bool q4_fast_ok(const Launch& L) {
   return true;
 }
 
+// From this many rows the 256 x 256 GEMM wastes less on partial row tiles than
+// the 128 x 128 one loses to its lower MFMA rate.
+constexpr int64_t kGemmBigMinM = 128;
+
 Kernel select_kernel(const Launch& L) {
   if (q4_fast_ok(L) && fits_i32(L)) {
     if (L.op == OP_MATMUL && L.M >= 1 && dot_mr(L.M) != 0 && dot_cpl(L) != 0 && dot_meta_fits(L)) return K_GEMV_DOT;
     if (L.M >= 1 && L.M <= 16 && gemv_tiles(L) != 0) return K_GEMV_Q4;
+    if (L.M >= kGemmBigMinM && L.op == OP_MATMUL) return K_GEMM_BIG;
     if (L.M > 16 && L.op == OP_MATMUL && L.zp_kind != ZP_FLOAT) return K_GEMM_Q4;
   }
   return K_GENERIC;
@@ -284,6 +292,7 @@ const char* kernel_name(Kernel k) {
     case K_GEMV_Q4: return "gemv_q4_mfma";
     case K_GEMV_DOT: return "gemv_q4_dot";
     case K_GEMM_Q4: return "gemm_q4_mfma";
+    case K_GEMM_BIG: return "gemm_q4_big";
     default: return "generic";
   }
 }
@@ -322,6 +331,11 @@ hipError_t launch(const Launch& L, hipStream_t st) {
     if (zpk == ZP_NONE) return launch_gemv_for<ZP_NONE>(L, st);
     if (zpk == ZP_PACKED) return launch_gemv_for<ZP_PACKED>(L, st);
     return launch_gemv_for<ZP_FLOAT>(L, st);
+  }
+  if (k == K_GEMM_BIG) {
+    if (zpk == ZP_NONE) return launch_gemm_big_for<ZP_NONE>(L, st);
+    if (zpk == ZP_PACKED) return launch_gemm_big_for<ZP_PACKED>(L, st);
+    return launch_gemm_big_for<ZP_FLOAT>(L, st);
   }
   if (k == K_GEMM_Q4) {
     if (zpk == ZP_NONE) return launch_gemm1<ZP_NONE>(L, st);
