@@ -1,5 +1,6 @@
-// Decode GEMV for M <= 4 rows (fp16 activations, 4-bit weights): no LDS, no
-// barriers, each wave independent.
+// Decode GEMV for M <= 4 rows (fp16 activations, 4-bit weights). After one
+// barrier that publishes the staged activations, each wave runs on its own:
+// no LDS traffic and no barrier on the weight stream.
 //
 // Work split. A wave owns C consecutive output columns (a column is one row
 // of B: kb * blob bytes) and walks them in order. Its lanes split K: lane l
