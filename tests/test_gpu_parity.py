@@ -117,6 +117,8 @@ DOT_CASES = [
     (1, 256, 1, 16, "packed", True),         # bs = 16: two blocks per chunk, N = 1
     (4, 512, 23, 16, "float", True),
     (1, 4096, 2, 32, None, False),
+    (4, 8192, 70, 16, "packed", True),       # four rows on 8 waves x 4 columns, 4 KB scale blocks
+    (3, 4096, 100, 32, None, False),         # three rows padded to four, 8 x 4 shape
 ]
 
 
@@ -325,6 +327,42 @@ def test_qkv_parity(gpu, M, K, Nq, Nkv, bs, dtype, zp, skip):
     assert np.array_equal(host(R), ref[3])  # residual A + skip: bit-exact
 
 
+QKV_DOT_CASES = [
+    # M, K, Nq, Nkv, bs, zp, skip on the dot GEMV (M <= 4): every chunk-round
+    # count, rows 1..4, bs 16..64, every zero-point kind, K tails, column counts
+    # that leave a projection's last wave partly empty
+    (4, 4096, 256, 64, 64, "packed", False),   # the GQA decode layout, narrower
+    (2, 2048, 96, 40, 32, None, True),
+    (3, 8192, 33, 17, 32, "float", True),      # four chunk rounds, odd widths
+    (1, 1024, 20, 12, 16, "packed", True),     # bs = 16: two blocks per chunk
+    (4, 288, 40, 24, 32, "float_int", True),   # K tail inside the only chunk round
+    (4, 16384, 64, 32, 64, None, False),       # eight chunk rounds
+    (1, 64, 1, 1, 32, None, True),             # one column per projection
+]
+
+
+@pytest.mark.parametrize("M,K,Nq,Nkv,bs,zp,skip", QKV_DOT_CASES)
+def test_qkv_dot_parity(gpu, M, K, Nq, Nkv, bs, zp, skip):
+    rng = np.random.default_rng(M * 131 + K + Nq + Nkv + bs)
+    dt = np.float16
+    A = rng.standard_normal((M, K)).astype(dt)
+    sk = rng.standard_normal((M, K)).astype(dt) if skip else None
+    g = rng.uniform(0.5, 1.5, K).astype(dt)
+    parts = [rand_case(rng, 1, K, n, 4, bs, dt, zp)[1:4] for n in (Nq, Nkv, Nkv)]
+    kind = None if zp is None else ("packed" if zp == "packed" else "float")
+    o = ops()
+    assert o.select_kernel("MatMulNBitsQkv", M, K, Nq, 4, bs, torch.float16, kind) == "gemv_q4_dot"
+    Q, Kk, V, R = o.matmul_nbits_qkv(dev(A), *[dev(x) for p in parts for x in p[:2]], norm_scale=dev(g), skip=dev(sk),
+                                     block_size=bs, q_zero_points=dev(parts[0][2]), k_zero_points=dev(parts[1][2]),
+                                     v_zero_points=dev(parts[2][2]))
+    ref = O.matmul_nbits_qkv(A, parts[0][0], parts[0][1], parts[1][0], parts[1][1], parts[2][0], parts[2][1], K=K,
+                             Nq=Nq, Nkv=Nkv, norm_scale=g, skip=sk, block_size=bs, q_zero_points=parts[0][2],
+                             k_zero_points=parts[1][2], v_zero_points=parts[2][2])
+    for got, exp, nm in zip((Q, Kk, V), ref[:3], "qkv"):
+        assert_parity(host(got), exp, dt, nm)
+    assert np.array_equal(host(R), ref[3])  # residual A + skip: bit-exact
+
+
 MLP_CASES = [
     # M, K, N, bs, dtype, skip, norm, biases, act
     (1, 256, 64, 32, np.float16, False, False, False, "silu"),
@@ -428,6 +466,7 @@ def test_workload_decode_up_m1(gpu):
 def test_workload_qkv_gqa_m4(gpu):
     w = workloads.make("qkv_gqa_m4")
     i, at = w["inputs"], w["attrs"]
+    assert ops().select_kernel("MatMulNBitsQkv", 4, at["K"], at["Nq"], 4, at["block_size"], zp="packed") == "gemv_q4_dot"
     outs = [host(t) for t in _run_workload(w)]
     ref = O.matmul_nbits_qkv(i["aT"], i["qBT"], i["qScalesT"], i["kBT"], i["kScalesT"], i["vBT"], i["vScalesT"],
                              K=at["K"], Nq=at["Nq"], Nkv=at["Nkv"], norm_scale=i["normScaleT"],

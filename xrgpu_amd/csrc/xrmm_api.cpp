@@ -184,6 +184,7 @@ const char* xrmm_select_kernel(int32_t op, int64_t M, int64_t K, int64_t N, int3
   static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
   L.nproj = op == xrmm::OP_QKV ? 3 : op == xrmm::OP_MLP ? 2 : 1;
   L.A = dummy;
+  if (op == xrmm::OP_QKV) L.gamma = dummy;  // normScaleT is required for Qkv
   for (int i = 0; i < L.nproj; ++i) L.p[i] = xrmm::Proj{dummy, dummy, zp_dtype == XRMM_UNSPECIFIED ? nullptr : dummy, nullptr, nullptr, N};
   ok();
   return xrmm::kernel_name(xrmm::select_kernel(L));

@@ -59,6 +59,11 @@ __device__ __forceinline__ float wave_total(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
+
 // Offset past the end of every buffer resource: such loads return zero.
 constexpr uint32_t kOOB = 0x80000000u;
 
@@ -69,14 +74,24 @@ constexpr int DOT_META_PIECES = 4;
 // Compact kernel arguments: every field is read in the kernel's first scalar
 // batch, before any branch, so a wave issues its first weight loads after a
 // single kernel-argument round trip.
-struct DotArgs {
-  const void* A;
+struct DotProj {
   const uint8_t* B;
   const void* S;
   const void* Z;
-  const void* bias;
   void* Y;
-  uint32_t N, K, kb, rowb, zrow, M;
+  uint32_t N;
+  uint32_t wg0;  // first workgroup of this projection on the grid
+};
+
+struct DotArgs {
+  const void* A;
+  const void* bias;   // MatMulNBits only
+  const void* skip;   // Qkv: nullable, added to A
+  const void* gamma;  // Qkv: RMS scale [K]
+  void* residual;     // Qkv: nullable, receives A + skip
+  float eps;
+  DotProj p[3];       // MatMulNBits: p[0]; Qkv: Q, K, V side by side on the grid
+  uint32_t K, kb, rowb, zrow, M;
   uint32_t bsl;         // log2(block_size)
   uint32_t zesz;        // bytes per float zero point (2 or 4)
   uint32_t meta_bytes;  // per-wave LDS bytes: C*kb*2 scales (+ C*zrow zero points), 16-aligned
@@ -91,18 +106,35 @@ __host__ __device__ constexpr uint32_t dot_act_bytes() {
   return MR * CPL * 4 * 64 * 16 + MR * CPL * SPC * 2 * 64 * 4;
 }
 
-template <int ZPK, int SPC, int CPL, int C, int P, int MR, int W, int MP>
+// OPK: OP_MATMUL, or OP_QKV with SK = whether the skip input is present.
+template <int ZPK, int SPC, int CPL, int C, int P, int MR, int W, int MP, int OPK, bool SK = false>
 __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
   static_assert(MP >= 1 && MP <= DOT_META_PIECES, "scale pieces");
+  static_assert(OPK == OP_MATMUL || OPK == OP_QKV, "operator");
+  static_assert(OPK == OP_QKV || !SK, "skip is a Qkv input");
+  constexpr bool QKV = OPK == OP_QKV;
   constexpr int DPH = 4 / SPC;  // dwords per block of a chunk
   constexpr uint32_t PAIRS = MR * CPL * 4 * 64 * 16;
   extern __shared__ __align__(16) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t N = a.N, K = a.K, kb = a.kb, rowb = a.rowb, zrow = a.zrow;
+  // The workgroup's projection: Qkv lays Q, K and V side by side on the grid.
+  // Every projection's fields are loaded with the other arguments and picked
+  // with scalar selects, so no load depends on the choice.
+  const uint32_t bid = blockIdx.x;
+  uint32_t pi = 0;
+  if constexpr (QKV) pi = (bid >= a.p[1].wg0 ? 1u : 0u) + (bid >= a.p[2].wg0 ? 1u : 0u);
+  auto pick = [&](auto v0, auto v1, auto v2) { return QKV ? (pi == 0 ? v0 : pi == 1 ? v1 : v2) : v0; };
+  const uint8_t* Bp = pick(a.p[0].B, a.p[1].B, a.p[2].B);
+  const void* Sp = pick(a.p[0].S, a.p[1].S, a.p[2].S);
+  const void* Zp = pick(a.p[0].Z, a.p[1].Z, a.p[2].Z);
+  void* Yp = pick(a.p[0].Y, a.p[1].Y, a.p[2].Y);
+  const uint32_t N = pick(a.p[0].N, a.p[1].N, a.p[2].N);
+  const uint32_t wg0 = pick(a.p[0].wg0, a.p[1].wg0, a.p[2].wg0);
+  const uint32_t K = a.K, kb = a.kb, rowb = a.rowb, zrow = a.zrow;
   const uint32_t nchunk = rowb >> 4;
   const int M = static_cast<int>(a.M);
-  const uint32_t col0 = (blockIdx.x * W + wave) * C;
+  const uint32_t col0 = ((bid - wg0) * W + wave) * C;
   // Columns past N (the grid's last waves) are clamped for loading and never
   // stored; no early exit, so no branch separates the argument loads.
   auto clampc = [&](uint32_t c) { return c < N ? c : N - 1; };
@@ -123,14 +155,14 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
     // bound is rounded up to 16 bytes. Tensors on this path start 16-byte
     // aligned, so the rounded bound stays inside the aligned 16-byte block
     // holding the tensor's last byte; the extra bytes are never used.
-    const rsrc_t rS = mk_rsrc(a.S, (N * kb * 2u + 15u) & ~15u);
+    const rsrc_t rS = mk_rsrc(Sp, (N * kb * 2u + 15u) & ~15u);
 #pragma unroll
     for (int q = 0; q < MP; ++q) {
       const uint32_t o = lane * 16u + 1024u * q;
       sv[q] = bld16_nt(rS, o < sbytes ? c0 * kb * 2u + o : kOOB, 0);  // predicated, no branch: a branch here costs a full wait
     }
     if constexpr (ZPK != ZP_NONE) {
-      const rsrc_t rZ = mk_rsrc(a.Z, (N * zrow + 15u) & ~15u);
+      const rsrc_t rZ = mk_rsrc(Zp, (N * zrow + 15u) & ~15u);
 #pragma unroll
       for (int q = 0; q < MP; ++q) {
         const uint32_t o = lane * 16u + 1024u * q;
@@ -147,7 +179,14 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
   constexpr int ITEMS = MR * CPL * 64;
   constexpr int IPT = (ITEMS + W * 64 - 1) / (W * 64);  // items per thread
   const rsrc_t rA = mk_rsrc(a.A, static_cast<uint32_t>(M) * K * 2u);
-  u32x4 raw[IPT][4];
+  // Qkv also loads skip (when present) and the RMS scale of the same k. When
+  // every item of a thread has the same chunk index (W a multiple of CPL), the
+  // thread loads the scale once.
+  constexpr bool GSAME = W % CPL == 0;
+  constexpr int GI = !QKV ? 1 : GSAME ? 1 : IPT;
+  const rsrc_t rK = mk_rsrc(a.skip, SK ? static_cast<uint32_t>(M) * K * 2u : 0u);
+  const rsrc_t rG = mk_rsrc(a.gamma, QKV ? K * 2u : 0u);
+  u32x4 raw[IPT][4], rsk[SK ? IPT : 1][4], rgm[GI][4];
 #pragma unroll
   for (int it = 0; it < IPT; ++it) {
     const int item = tid + it * W * 64;
@@ -156,14 +195,19 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
     for (int g = 0; g < 4; ++g) {
       const uint32_t k = static_cast<uint32_t>(jl) * 32u + 8u * g;
       const bool ok = item < ITEMS && m < M && k < K;  // K % 8 == 0 on this path: groups are whole
-      raw[it][g] = bld16(rA, ok ? (static_cast<uint32_t>(m) * K + k) * 2u : kOOB, 0);
+      const uint32_t off = ok ? (static_cast<uint32_t>(m) * K + k) * 2u : kOOB;
+      raw[it][g] = bld16(rA, off, 0);
+      if constexpr (SK) rsk[it][g] = bld16(rK, off, 0);
+      if constexpr (QKV) {
+        if (!GSAME || it == 0) rgm[GSAME ? 0 : it][g] = bld16(rG, k < K ? k * 2u : kOOB, 0);
+      }
     }
   }
 
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- weights of the first P columns: the HBM stream
-  const rsrc_t rB = mk_rsrc(a.B, N * rowb);
+  const rsrc_t rB = mk_rsrc(Bp, N * rowb);
   uint32_t vb[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
@@ -189,6 +233,85 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
     const uint32_t o = lane * 16u + 1024u * q;
     if (o < sbytes) *reinterpret_cast<u32x4*>(meta + o) = sv[q];
     if (ZPK != ZP_NONE && o < zbytes) *reinterpret_cast<u32x4*>(meta + a.zoff + o) = zv[ZPK == ZP_NONE ? 0 : q];
+  }
+  // Qkv: r = A + skip in float32 and x = r * inv * gamma with
+  // inv = 1 / sqrt(sum_k r^2 / K + eps) per row (packedInput,
+  // complex_kernel.glsl:81); x is staged in binary16, so it is normalised
+  // before rounding (r * gamma alone could leave the binary16 range). The
+  // workgroup holds whole rows: the row sums of squares reduce once through
+  // LDS. Per element each pass is one or two mixed-precision FMAs (binary16
+  // operands, float32 arithmetic).
+  if constexpr (QKV) {
+    __shared__ float red[W][MR];
+    auto rval = [&](const f16x8& av, const f16x8& sv, int e) {
+      if constexpr (SK) return __fadd_rn(static_cast<float>(av[e]), static_cast<float>(sv[e]));
+      else return static_cast<float>(av[e]);
+    };
+    float sq[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) sq[m] = 0.f;
+#pragma unroll
+    for (int it = 0; it < IPT; ++it) {
+      const int item = tid + it * W * 64;
+      const int m = item / (CPL * 64);
+      float part[2] = {0.f, 0.f};
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f16x8 av = __builtin_bit_cast(f16x8, raw[it][g]);
+        const f16x8 sv = __builtin_bit_cast(f16x8, rsk[SK ? it : 0][g]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float r = rval(av, sv, e);
+          part[e & 1] = __builtin_fmaf(r, r, part[e & 1]);
+        }
+      }
+#pragma unroll
+      for (int mm = 0; mm < MR; ++mm) sq[mm] += (item < ITEMS && m == mm) ? part[0] + part[1] : 0.f;
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float t = wave_total(sq[m]);
+      if (lane == 0) red[wave][m] = t;
+    }
+    __syncthreads();
+    float inv[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) t += red[w][m];
+      inv[m] = __builtin_amdgcn_rsqf(t / static_cast<float>(K) + a.eps);
+    }
+    f16* res = static_cast<f16*>(a.residual);
+    const bool write_res = res != nullptr && bid == 0;
+#pragma unroll
+    for (int it = 0; it < IPT; ++it) {
+      const int item = tid + it * W * 64;
+      const int m = item / (CPL * 64), jl = item % (CPL * 64);
+      float im = inv[0];
+#pragma unroll
+      for (int mm = 1; mm < MR; ++mm) im = m == mm ? inv[mm] : im;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f16x8 av = __builtin_bit_cast(f16x8, raw[it][g]);
+        const f16x8 sv = __builtin_bit_cast(f16x8, rsk[SK ? it : 0][g]);
+        const f16x8 gv = __builtin_bit_cast(f16x8, rgm[GSAME ? 0 : it][g]);
+        f16x8 x;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float t = __builtin_fmaf(static_cast<float>(gv[e]), im, 0.f);
+          x[e] = static_cast<f16>(rval(av, sv, e) * t);
+        }
+        raw[it][g] = __builtin_bit_cast(u32x4, x);
+        const uint32_t k = static_cast<uint32_t>(jl) * 32u + 8u * g;
+        if (write_res && item < ITEMS && m < M && k < K) {
+          f16x8 rr;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) rr[e] = static_cast<f16>(rval(av, sv, e));
+          *reinterpret_cast<f16x8*>(res + static_cast<uint32_t>(m) * K + k) = rr;
+        }
+      }
+    }
   }
   {
     const f16x2 c1024 = {static_cast<f16>(1024.f), static_cast<f16>(1024.f)};
@@ -266,8 +389,8 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
     zsh[j] = (b & 1u) * 4u;
   }
 
-  const f16* biasp = static_cast<const f16*>(a.bias);
-  f16* Y = static_cast<f16*>(a.Y);
+  const f16* biasp = QKV ? nullptr : static_cast<const f16*>(a.bias);
+  f16* Y = static_cast<f16*>(Yp);
   float out[MR];  // lane i < C keeps column col0 + i
 #pragma unroll
   for (int m = 0; m < MR; ++m) out[m] = 0.f;
@@ -341,16 +464,23 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
 
 // Host side: argument block for a geometry and C columns per wave, and the
 // workgroup's LDS bytes.
-inline DotArgs dot_args(const Launch& L, int C, uint32_t act_bytes) {
-  const Proj& P = L.p[0];
+inline uint32_t dot_wgs(int64_t N, int C, int W) { return static_cast<uint32_t>((N + C * W - 1) / (C * W)); }
+
+inline DotArgs dot_args(const Launch& L, int C, int W, uint32_t act_bytes) {
   DotArgs a;
   a.A = L.A;
-  a.B = P.B;
-  a.S = P.scales;
-  a.Z = P.zp;
-  a.bias = P.bias;
-  a.Y = P.Y;
-  a.N = static_cast<uint32_t>(P.N);
+  a.bias = L.p[0].bias;
+  a.skip = L.skip;
+  a.gamma = L.gamma;
+  a.residual = L.residual;
+  a.eps = L.eps;
+  uint32_t wg = 0;
+  for (int i = 0; i < 3; ++i) {
+    const bool used = i < L.nproj;
+    const Proj& P = L.p[used ? i : 0];
+    a.p[i] = DotProj{P.B, P.scales, P.zp, P.Y, static_cast<uint32_t>(P.N), used ? wg : 0xFFFFFFFFu};
+    if (used) wg += dot_wgs(P.N, C, W);
+  }
   a.K = static_cast<uint32_t>(L.K);
   a.kb = static_cast<uint32_t>(L.kb);
   a.rowb = static_cast<uint32_t>(L.kb * L.blob);
@@ -368,9 +498,15 @@ inline DotArgs dot_args(const Launch& L, int C, uint32_t act_bytes) {
 
 inline size_t dot_lds_bytes(const DotArgs& a, int W) { return a.act_bytes + static_cast<size_t>(W) * a.meta_bytes; }
 
-// Launch shape of the dot GEMV (measured on the decode workload: 2 columns
-// per wave, one column prefetched, 4 waves per workgroup).
-constexpr int DOT_C = 2, DOT_P = 1, DOT_W = 4;
+// Launch shape of the dot GEMV: columns per wave (C) and waves per workgroup
+// (W), one column prefetched. Measured: 2 x 4 on the one-row decode workload;
+// 4 x 8 with four rows, where the activation staging is four times larger and
+// fewer, larger workgroups amortise it (Qkv GQA decode 14.0 -> 11.5 us), as
+// long as the staging leaves LDS room for eight waves' scale blocks.
+constexpr int DOT_P = 1;
+constexpr bool dot_wide(int mr, int cpl) { return mr >= 4 && cpl <= 4; }
+constexpr int dot_c(int mr, int cpl) { return dot_wide(mr, cpl) ? 4 : 2; }
+constexpr int dot_w(int mr, int cpl) { return dot_wide(mr, cpl) ? 8 : 4; }
 
 // Chunk rounds per lane (a power of two >= ceil(chunks / 64)) and rows (1, 2
 // or 4) the dot GEMV is instantiated for; 0 when it does not apply.
@@ -386,22 +522,38 @@ inline int dot_mr(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 0; 
 // 16-byte pieces per lane that a wave's scale / zero-point block needs: 1 or
 // DOT_META_PIECES (0 if the block is larger).
 inline int dot_meta_pieces(const Launch& L) {
-  const int64_t sb = DOT_C * L.kb * 2;
-  const int64_t zb = L.zp_kind == ZP_PACKED ? DOT_C * L.zrow
-                     : L.zp_kind == ZP_FLOAT ? DOT_C * L.kb * (L.zp_dtype == DT_F32 ? 4 : 2) : 0;
+  const int64_t c = dot_c(dot_mr(L.M), dot_cpl(L));
+  const int64_t sb = c * L.kb * 2;
+  const int64_t zb = L.zp_kind == ZP_PACKED ? c * L.zrow
+                     : L.zp_kind == ZP_FLOAT ? c * L.kb * (L.zp_dtype == DT_F32 ? 4 : 2) : 0;
   const int64_t mx = sb > zb ? sb : zb;
   return mx <= 1024 ? 1 : mx <= 1024 * DOT_META_PIECES ? DOT_META_PIECES : 0;
 }
 
-inline bool dot_meta_fits(const Launch& L) { return dot_meta_pieces(L) != 0; }
+// Whether the dot GEMV applies: rows, chunk rounds and scale blocks within its
+// instantiations, and the workgroup's LDS (staged activations, eight or four
+// waves' scale / zero-point slices, the Qkv row-sum scratch) within 160 KB.
+inline bool dot_fits(const Launch& L) {
+  const int mr = dot_mr(L.M), cpl = dot_cpl(L);
+  if (mr == 0 || cpl == 0 || dot_meta_pieces(L) == 0) return false;
+  const int c = dot_c(mr, cpl), w = dot_w(mr, cpl), spc = L.block_size >= 32 ? 1 : 2;
+  const int64_t act = int64_t(mr) * cpl * 4 * 64 * 16 + int64_t(mr) * cpl * spc * 2 * 64 * 4;
+  const int64_t zesz = L.zp_dtype == DT_F32 ? 4 : 2;
+  const int64_t zrow = L.zp_kind == ZP_PACKED ? L.zrow : L.kb * zesz;
+  const int64_t zoff = (int64_t(c) * L.kb * 2 + 15) & ~int64_t(15);
+  const int64_t meta = (zoff + (L.zp_kind == ZP_NONE ? 0 : int64_t(c) * zrow) + 15) & ~int64_t(15);
+  const int64_t stat = int64_t(w) * mr * 4;
+  return act + w * meta + stat <= 160 * 1024;
+}
 
-template <int ZPK, int SPC, int CPL, int MR, int MP>
-inline hipError_t launch_dot5(const Launch& L, hipStream_t st) {
-  const DotArgs a = dot_args(L, DOT_C, dot_act_bytes<MR, CPL, SPC>());
-  const uint32_t per = DOT_W * DOT_C;
-  const uint32_t grid = static_cast<uint32_t>((L.p[0].N + per - 1) / per);
-  const size_t lds = dot_lds_bytes(a, DOT_W);
-  auto kern = k_gemv_dot<ZPK, SPC, CPL, DOT_C, DOT_P, MR, DOT_W, MP>;
+template <int ZPK, int SPC, int CPL, int MR, int MP, int OPK, bool SK>
+inline hipError_t launch_dot6(const Launch& L, hipStream_t st) {
+  constexpr int C = dot_c(MR, CPL), W = dot_w(MR, CPL);
+  const DotArgs a = dot_args(L, C, W, dot_act_bytes<MR, CPL, SPC>());
+  uint32_t grid = 0;
+  for (int i = 0; i < L.nproj; ++i) grid += dot_wgs(L.p[i].N, C, W);
+  const size_t lds = dot_lds_bytes(a, W);
+  auto kern = k_gemv_dot<ZPK, SPC, CPL, C, DOT_P, MR, W, MP, OPK, SK>;
   if (lds > 64 * 1024) {
     static bool raised = false;  // per instantiation
     if (!raised) {
@@ -411,32 +563,40 @@ inline hipError_t launch_dot5(const Launch& L, hipStream_t st) {
       raised = true;
     }
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(DOT_W * 64), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(W * 64), lds, st, a);
   return hipGetLastError();
 }
 
-template <int ZPK, int SPC, int CPL, int MR>
-inline hipError_t launch_dot4(const Launch& L, hipStream_t st) {
-  return dot_meta_pieces(L) == 1 ? launch_dot5<ZPK, SPC, CPL, MR, 1>(L, st)
-                                 : launch_dot5<ZPK, SPC, CPL, MR, DOT_META_PIECES>(L, st);
+template <int ZPK, int SPC, int CPL, int MR, int MP, int OPK>
+inline hipError_t launch_dot5(const Launch& L, hipStream_t st) {
+  if constexpr (OPK == OP_QKV)
+    return L.skip ? launch_dot6<ZPK, SPC, CPL, MR, MP, OPK, true>(L, st) : launch_dot6<ZPK, SPC, CPL, MR, MP, OPK, false>(L, st);
+  else
+    return launch_dot6<ZPK, SPC, CPL, MR, MP, OPK, false>(L, st);
 }
 
-template <int ZPK, int SPC, int CPL>
+template <int ZPK, int SPC, int CPL, int MR, int OPK>
+inline hipError_t launch_dot4(const Launch& L, hipStream_t st) {
+  return dot_meta_pieces(L) == 1 ? launch_dot5<ZPK, SPC, CPL, MR, 1, OPK>(L, st)
+                                 : launch_dot5<ZPK, SPC, CPL, MR, DOT_META_PIECES, OPK>(L, st);
+}
+
+template <int ZPK, int SPC, int CPL, int OPK>
 inline hipError_t launch_dot3(const Launch& L, hipStream_t st) {
   switch (dot_mr(L.M)) {
-    case 1: return launch_dot4<ZPK, SPC, CPL, 1>(L, st);
-    case 2: return launch_dot4<ZPK, SPC, CPL, 2>(L, st);
-    default: return launch_dot4<ZPK, SPC, CPL, 4>(L, st);
+    case 1: return launch_dot4<ZPK, SPC, CPL, 1, OPK>(L, st);
+    case 2: return launch_dot4<ZPK, SPC, CPL, 2, OPK>(L, st);
+    default: return launch_dot4<ZPK, SPC, CPL, 4, OPK>(L, st);
   }
 }
 
-template <int ZPK, int SPC>
+template <int ZPK, int SPC, int OPK>
 inline hipError_t launch_dot2(const Launch& L, hipStream_t st) {
   switch (dot_cpl(L)) {
-    case 1: return launch_dot3<ZPK, SPC, 1>(L, st);
-    case 2: return launch_dot3<ZPK, SPC, 2>(L, st);
-    case 4: return launch_dot3<ZPK, SPC, 4>(L, st);
-    default: return launch_dot3<ZPK, SPC, 8>(L, st);
+    case 1: return launch_dot3<ZPK, SPC, 1, OPK>(L, st);
+    case 2: return launch_dot3<ZPK, SPC, 2, OPK>(L, st);
+    case 4: return launch_dot3<ZPK, SPC, 4, OPK>(L, st);
+    default: return launch_dot3<ZPK, SPC, 8, OPK>(L, st);
   }
 }
 

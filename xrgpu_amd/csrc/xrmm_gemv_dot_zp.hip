@@ -10,7 +10,9 @@ namespace xrmm {
 
 template <>
 hipError_t launch_dot_for<XRMM_ZPK>(const Launch& L, hipStream_t st) {
-  return L.block_size >= 32 ? launch_dot2<XRMM_ZPK, 1>(L, st) : launch_dot2<XRMM_ZPK, 2>(L, st);
+  if (L.op == OP_QKV)
+    return L.block_size >= 32 ? launch_dot2<XRMM_ZPK, 1, OP_QKV>(L, st) : launch_dot2<XRMM_ZPK, 2, OP_QKV>(L, st);
+  return L.block_size >= 32 ? launch_dot2<XRMM_ZPK, 1, OP_MATMUL>(L, st) : launch_dot2<XRMM_ZPK, 2, OP_MATMUL>(L, st);
 }
 
 }  // namespace xrmm

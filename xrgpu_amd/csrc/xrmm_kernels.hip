@@ -279,7 +279,7 @@ constexpr int64_t kGemmBigMinM = 128;
 
 Kernel select_kernel(const Launch& L) {
   if (q4_fast_ok(L) && fits_i32(L)) {
-    if (L.op == OP_MATMUL && L.M >= 1 && dot_mr(L.M) != 0 && dot_cpl(L) != 0 && dot_meta_fits(L)) return K_GEMV_DOT;
+    if ((L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 && dot_fits(L)) return K_GEMV_DOT;
     if (L.M >= 1 && L.M <= 16 && gemv_tiles(L) != 0) return K_GEMV_Q4;
     if (L.M >= kGemmBigMinM && L.op == OP_MATMUL) return K_GEMM_BIG;
     if (L.M > 16 && L.op == OP_MATMUL && L.zp_kind != ZP_FLOAT) return K_GEMM_Q4;
