@@ -52,14 +52,18 @@ def test_qkv_requires_norm_scale():
 @pytest.mark.parametrize("op,M,K,N,bs,dtype,zp,expect", [
     (0, 1, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_dot"),
     (0, 4, 4096, 14336, 64, nat.F16, nat.U8, "gemv_q4_dot"),
-    (0, 8, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),
+    (0, 8, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_splitk"),
+    (0, 5, 2048, 14336, 64, nat.F16, nat.F16, "gemv_q4_splitk"),
+    (0, 16, 1024, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),   # 32 chunks: no even split
+    (0, 16, 4096, 14336, 16, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),   # bs = 16
     (0, 2048, 4096, 14336, 128, nat.F16, nat.U8, "gemm_q4_big"),
     (0, 128, 4096, 14336, 32, nat.F16, nat.F16, "gemm_q4_big"),
     (0, 127, 4096, 14336, 32, nat.F16, nat.U8, "gemm_q4_mfma"),
     (0, 64, 4096, 14336, 32, nat.F16, nat.F16, "generic"),
     (1, 4, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_dot"),
-    (1, 8, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_mfma"),
-    (2, 16, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),
+    (1, 8, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_splitk"),
+    (2, 16, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_splitk"),
+    (2, 16, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),
     (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "generic"),
     (0, 4, 16384, 14336, 16, nat.F16, nat.UNSPECIFIED, "generic"),  # dot staging would exceed 160 KB of LDS
     (0, 1, 33, 8, 32, nat.F16, nat.UNSPECIFIED, "generic"),

@@ -297,6 +297,42 @@ def test_fixture_shapes_with_oracle(gpu):
     assert ran >= 60
 
 
+SPLITK_CASES = [
+    # M, K, N, bs, zp, bias on the split-K GEMV (4 < M <= 16, a column's chunks
+    # split evenly over 8 waves x 4 lane groups): chunks per lane 2 and 4,
+    # 1, 2 or 4 blocks per lane (and blocks shared by lanes), every zero-point
+    # kind, N below one tile, tile counts that leave the last workgroup short
+    (8, 4096, 1000, 32, None, False),        # four blocks per lane
+    (16, 4096, 333, 64, "packed", True),     # two blocks per lane
+    (5, 2048, 70, 32, "float", True),        # two chunks per lane
+    (12, 4096, 16, 128, "packed", False),    # one block per lane, odd first blocks
+    (16, 2048, 4100, 256, "float_int", True),  # blocks shared by lane groups; 257 tiles
+    (7, 4096, 8200, 32, None, True),         # 513 tiles: three per workgroup, last one short
+    (16, 4096, 3, 32, "packed", True),       # N below one tile
+]
+
+
+@pytest.mark.parametrize("M,K,N,bs,zp,bias", SPLITK_CASES)
+def test_gemv_splitk_parity(gpu, M, K, N, bs, zp, bias):
+    rng = np.random.default_rng(M * 977 + K + N + bs)
+    A, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, np.float16, zp, bias)
+    assert ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16,
+                               None if zp is None else ("packed" if zp == "packed" else "float")) == "gemv_q4_splitk"
+    Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
+    ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs)
+    assert_parity(Y, ref, np.float16)
+
+
+def test_gemv_splitk_float32_zero_points(gpu):
+    rng = np.random.default_rng(4242)
+    M, K, N, bs = 9, 4096, 130, 64
+    A, B, S, _, b = rand_case(rng, M, K, N, 4, bs, np.float16, None, True)
+    Z = rng.uniform(0, 15, (N, K // bs)).astype(np.float32)
+    Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
+    ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs)
+    assert_parity(Y, ref, np.float16)
+
+
 # --------------------------------------------------------------------------- Qkv / Mlp
 
 QKV_CASES = [
@@ -361,6 +397,66 @@ def test_qkv_dot_parity(gpu, M, K, Nq, Nkv, bs, zp, skip):
     for got, exp, nm in zip((Q, Kk, V), ref[:3], "qkv"):
         assert_parity(host(got), exp, dt, nm)
     assert np.array_equal(host(R), ref[3])  # residual A + skip: bit-exact
+
+
+QKV_SPLITK_CASES = [
+    # M, K, Nq, Nkv, bs, zp, skip on the split-K GEMV (5 <= M <= 16)
+    (8, 4096, 256, 64, 64, "packed", True),
+    (16, 2048, 40, 24, 32, None, False),
+    (6, 4096, 100, 36, 128, "float", True),
+]
+
+
+@pytest.mark.parametrize("M,K,Nq,Nkv,bs,zp,skip", QKV_SPLITK_CASES)
+def test_qkv_splitk_parity(gpu, M, K, Nq, Nkv, bs, zp, skip):
+    rng = np.random.default_rng(M * 313 + K + Nq + Nkv + bs)
+    dt = np.float16
+    A = rng.standard_normal((M, K)).astype(dt)
+    sk = rng.standard_normal((M, K)).astype(dt) if skip else None
+    g = rng.uniform(0.5, 1.5, K).astype(dt)
+    parts = [rand_case(rng, 1, K, n, 4, bs, dt, zp)[1:4] for n in (Nq, Nkv, Nkv)]
+    kind = None if zp is None else ("packed" if zp == "packed" else "float")
+    o = ops()
+    assert o.select_kernel("MatMulNBitsQkv", M, K, Nq, 4, bs, torch.float16, kind) == "gemv_q4_splitk"
+    Q, Kk, V, R = o.matmul_nbits_qkv(dev(A), *[dev(x) for p in parts for x in p[:2]], norm_scale=dev(g), skip=dev(sk),
+                                     block_size=bs, q_zero_points=dev(parts[0][2]), k_zero_points=dev(parts[1][2]),
+                                     v_zero_points=dev(parts[2][2]))
+    ref = O.matmul_nbits_qkv(A, parts[0][0], parts[0][1], parts[1][0], parts[1][1], parts[2][0], parts[2][1], K=K,
+                             Nq=Nq, Nkv=Nkv, norm_scale=g, skip=sk, block_size=bs, q_zero_points=parts[0][2],
+                             k_zero_points=parts[1][2], v_zero_points=parts[2][2])
+    for got, exp, nm in zip((Q, Kk, V), ref[:3], "qkv"):
+        assert_parity(host(got), exp, dt, nm)
+    assert np.array_equal(host(R), ref[3])  # residual A + skip: bit-exact
+
+
+MLP_SPLITK_CASES = [
+    # M, K, N, bs, skip, norm, biases, act, residual on the split-K GEMV
+    (16, 4096, 1000, 32, False, False, False, "silu", False),   # the batched SwiGLU layout, narrower
+    (8, 2048, 72, 64, True, True, True, "silu", True),
+    (12, 4096, 40, 32, True, False, False, "gelu", True),
+    (5, 4096, 33, 128, False, True, False, "relu", False),
+    (16, 4096, 7, 32, False, False, True, "silu", True),       # N below one tile; residual = A
+]
+
+
+@pytest.mark.parametrize("M,K,N,bs,skip,norm,biases,act,res", MLP_SPLITK_CASES)
+def test_mlp_splitk_parity(gpu, M, K, N, bs, skip, norm, biases, act, res):
+    rng = np.random.default_rng(M * 29 + K + N + bs)
+    dt = np.float16
+    A = rng.standard_normal((M, K)).astype(dt)
+    sk = rng.standard_normal((M, K)).astype(dt) if skip else None
+    g = rng.uniform(0.5, 1.5, K).astype(dt) if norm else None
+    _, gB, gS, _, gb = rand_case(rng, 1, K, N, 4, bs, dt, None, biases)
+    _, uB, uS, _, ub = rand_case(rng, 1, K, N, 4, bs, dt, None, biases)
+    assert ops().select_kernel("MatMulNBitsMlp", M, K, N, 4, bs, torch.float16) == "gemv_q4_splitk"
+    Y, R = ops().matmul_nbits_mlp(dev(A), dev(gB), dev(gS), dev(uB), dev(uS), skip=dev(sk), norm_scale=dev(g),
+                                  gate_bias=dev(gb), up_bias=dev(ub), block_size=bs, activation=act,
+                                  want_residual=res)
+    ref, r = O.matmul_nbits_mlp(A, gB, gS, uB, uS, K=K, N=N, skip=sk, norm_scale=g, gate_bias=gb, up_bias=ub,
+                                block_size=bs, activation=act)
+    assert_parity(host(Y), ref, dt)
+    if res:
+        assert np.array_equal(host(R), r)
 
 
 MLP_CASES = [

@@ -30,6 +30,9 @@ UNITS = [
     ("xrmm_gemv_dot_zp.hip", ["-DXRMM_ZPK=0"], "dot_zp0.o"),
     ("xrmm_gemv_dot_zp.hip", ["-DXRMM_ZPK=1"], "dot_zp1.o"),
     ("xrmm_gemv_dot_zp.hip", ["-DXRMM_ZPK=2"], "dot_zp2.o"),
+    ("xrmm_gemv_sk_zp.hip", ["-DXRMM_ZPK=0"], "sk_zp0.o"),
+    ("xrmm_gemv_sk_zp.hip", ["-DXRMM_ZPK=1"], "sk_zp1.o"),
+    ("xrmm_gemv_sk_zp.hip", ["-DXRMM_ZPK=2"], "sk_zp2.o"),
     ("xrmm_gemm_zp.hip", ["-DXRMM_ZPK=0"], "gemm_zp0.o"),
     ("xrmm_gemm_zp.hip", ["-DXRMM_ZPK=1"], "gemm_zp1.o"),
     ("xrmm_gemm_zp.hip", ["-DXRMM_ZPK=2"], "gemm_zp2.o"),

@@ -503,10 +503,27 @@ inline size_t dot_lds_bytes(const DotArgs& a, int W) { return a.act_bytes + stat
 // 4 x 8 with four rows, where the activation staging is four times larger and
 // fewer, larger workgroups amortise it (Qkv GQA decode 14.0 -> 11.5 us), as
 // long as the staging leaves LDS room for eight waves' scale blocks.
-constexpr int DOT_P = 1;
+// The XRMM_DOT_* macros override the shape for tuning builds; every
+// translation unit of one library must see the same values.
+#ifndef XRMM_DOT_P
+#define XRMM_DOT_P 1
+#endif
+#ifndef XRMM_DOT_NARROW_C
+#define XRMM_DOT_NARROW_C 2
+#endif
+#ifndef XRMM_DOT_NARROW_W
+#define XRMM_DOT_NARROW_W 4
+#endif
+#ifndef XRMM_DOT_WIDE_C
+#define XRMM_DOT_WIDE_C 4
+#endif
+#ifndef XRMM_DOT_WIDE_W
+#define XRMM_DOT_WIDE_W 8
+#endif
 constexpr bool dot_wide(int mr, int cpl) { return mr >= 4 && cpl <= 4; }
-constexpr int dot_c(int mr, int cpl) { return dot_wide(mr, cpl) ? 4 : 2; }
-constexpr int dot_w(int mr, int cpl) { return dot_wide(mr, cpl) ? 8 : 4; }
+constexpr int dot_c(int mr, int cpl) { return dot_wide(mr, cpl) ? XRMM_DOT_WIDE_C : XRMM_DOT_NARROW_C; }
+constexpr int dot_w(int mr, int cpl) { return dot_wide(mr, cpl) ? XRMM_DOT_WIDE_W : XRMM_DOT_NARROW_W; }
+constexpr int dot_p(int mr, int cpl) { return XRMM_DOT_P < dot_c(mr, cpl) ? XRMM_DOT_P : dot_c(mr, cpl); }
 
 // Chunk rounds per lane (a power of two >= ceil(chunks / 64)) and rows (1, 2
 // or 4) the dot GEMV is instantiated for; 0 when it does not apply.
@@ -553,7 +570,7 @@ inline hipError_t launch_dot6(const Launch& L, hipStream_t st) {
   uint32_t grid = 0;
   for (int i = 0; i < L.nproj; ++i) grid += dot_wgs(L.p[i].N, C, W);
   const size_t lds = dot_lds_bytes(a, W);
-  auto kern = k_gemv_dot<ZPK, SPC, CPL, C, DOT_P, MR, W, MP, OPK, SK>;
+  auto kern = k_gemv_dot<ZPK, SPC, CPL, C, dot_p(MR, CPL), MR, W, MP, OPK, SK>;
   if (lds > 64 * 1024) {
     static bool raised = false;  // per instantiation
     if (!raised) {

@@ -27,6 +27,7 @@
 // 1024 + code exactly (and 1024 + 16*code for the high nibble of a byte).
 #include "xrmm_gemv.h"
 #include "xrmm_gemv_dot.h"
+#include "xrmm_gemv_sk.h"
 #include "xrmm_gemm.h"
 
 namespace xrmm {
@@ -277,9 +278,17 @@ static bool q4_fast_ok(const Launch& L) {
 // the 128 x 128 one loses to its lower MFMA rate.
 constexpr int64_t kGemmBigMinM = 128;
 
+// From this many rows (to 16) the split-K MFMA GEMV takes over from the dot
+// GEMV: the dot kernel's VALU work grows with every row, the MFMA's does not.
+#ifndef XRMM_SK_MIN_M
+#define XRMM_SK_MIN_M 5
+#endif
+constexpr int64_t kSplitKMinM = XRMM_SK_MIN_M;
+
 Kernel select_kernel(const Launch& L) {
   if (q4_fast_ok(L) && fits_i32(L)) {
     if ((L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 && dot_fits(L)) return K_GEMV_DOT;
+    if (L.M >= kSplitKMinM && sk_fits(L)) return K_GEMV_SK;
     if (L.M >= 1 && L.M <= 16 && gemv_tiles(L) != 0) return K_GEMV_Q4;
     if (L.M >= kGemmBigMinM && L.op == OP_MATMUL) return K_GEMM_BIG;
     if (L.M > 16 && L.op == OP_MATMUL && L.zp_kind != ZP_FLOAT) return K_GEMM_Q4;
@@ -291,6 +300,7 @@ const char* kernel_name(Kernel k) {
   switch (k) {
     case K_GEMV_Q4: return "gemv_q4_mfma";
     case K_GEMV_DOT: return "gemv_q4_dot";
+    case K_GEMV_SK: return "gemv_q4_splitk";
     case K_GEMM_Q4: return "gemm_q4_mfma";
     case K_GEMM_BIG: return "gemm_q4_big";
     default: return "generic";
@@ -326,6 +336,11 @@ hipError_t launch(const Launch& L, hipStream_t st) {
     if (zpk == ZP_NONE) return launch_dot_for<ZP_NONE>(L, st);
     if (zpk == ZP_PACKED) return launch_dot_for<ZP_PACKED>(L, st);
     return launch_dot_for<ZP_FLOAT>(L, st);
+  }
+  if (k == K_GEMV_SK) {
+    if (zpk == ZP_NONE) return launch_sk_for<ZP_NONE>(L, st);
+    if (zpk == ZP_PACKED) return launch_sk_for<ZP_PACKED>(L, st);
+    return launch_sk_for<ZP_FLOAT>(L, st);
   }
   if (k == K_GEMV_Q4) {
     if (zpk == ZP_NONE) return launch_gemv_for<ZP_NONE>(L, st);
