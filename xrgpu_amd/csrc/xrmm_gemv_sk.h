@@ -65,7 +65,10 @@ struct SkArgs {
 // Tiles per workgroup at most: the LDS holds every wave's partial sum of
 // every tile (W x TMAX KB) beside the transpose slices.
 constexpr int sk_tmax(int w) { return w >= 16 ? 7 : 8; }
-constexpr int SK_TQ = 4;    // tiles whose weights a wave keeps in flight
+#ifndef XRMM_SK_TQ
+#define XRMM_SK_TQ 2
+#endif
+constexpr int SK_TQ = XRMM_SK_TQ;  // tiles whose weights a wave keeps in flight
 
 // Scales (and zero points) of one lane's CPL chunks of one column: SPL
 // consecutive blocks, SPL = max(1, 32 CPL / block_size). Raw dwords: binary16
@@ -108,8 +111,13 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
   static_assert(!NRM || OPK != OP_MATMUL, "normalisation is a Qkv / Mlp prologue");
   constexpr int CPW = 4 * CPL;            // chunks of one column in a wave's K slice
   constexpr int XS = CPW * 16 + 16;       // LDS bytes per column of a transposed tile (padded)
-  __shared__ __align__(16) f32x4 part[W][TMAX][64];
-  __shared__ __align__(16) unsigned char xbuf[W][16 * XS];
+  // LDS: one region per wave. It first stages the wave's activation slice
+  // (16 rows x OPR 16-byte pieces, padded rows), then holds the wave's tile
+  // partial sums (TMAX x 1 KB) and its weight transpose slice (16 x XS).
+  constexpr int OPR = CPW * 4;            // 16-byte pieces of one row of the K slice
+  constexpr int XA = OPR * 16 + 16;       // LDS bytes per staged activation row (padded)
+  constexpr int RG = (16 * XA > TMAX * 1024 + 16 * XS ? 16 * XA : TMAX * 1024 + 16 * XS);
+  __shared__ __align__(16) unsigned char lds[W][RG];
   __shared__ float rsq[W][16];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -122,25 +130,27 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
   const uint32_t tb = blockIdx.x * a.tpw;  // first tile of the workgroup
   const uint32_t tpw = a.tpw < a.tiles - tb ? a.tpw : a.tiles - tb;
 
-  // ---- activations of row j, k in [k0, k0 + 32 CPL): CPL x 4 groups of 8
+  // ---- activations: the wave's K slice of all 16 rows, loaded coalesced
+  // (consecutive lanes read consecutive 16-byte pieces of a row); the LDS
+  // region transposes them to the MFMA operand order below. (Loaded in that
+  // order directly, every load instruction touched 64 different lines.)
+  constexpr int AI = 16 * OPR / 64;  // coalesced loads per lane
+  static_assert(AI == 4 * CPL, "activation staging");
   const rsrc_t rA = mk_rsrc(a.A, M * K * 2u);
-  u32x4 araw[CPL][4];
-  uint32_t aoff[CPL][4];
+  u32x4 craw[AI];
+  uint32_t coff[AI];
 #pragma unroll
-  for (int i = 0; i < CPL; ++i)
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint32_t k = k0 + 32u * i + 8u * d;
-      aoff[i][d] = (j < M && k < K) ? (j * K + k) * 2u : 0x80000000u;  // K % 8 == 0: groups are whole
-      araw[i][d] = bld16(rA, aoff[i][d], 0);
-    }
-  u32x4 sraw[NRM ? CPL : 1][4];
+  for (int r = 0; r < AI; ++r) {
+    const uint32_t e = static_cast<uint32_t>(r * 64 + lane), row = e / OPR, o = e % OPR;
+    const uint32_t k = w * CPW * 32u + o * 8u;
+    coff[r] = (row < M && k < K) ? (row * K + k) * 2u : 0x80000000u;  // K % 8 == 0: pieces are whole
+    craw[r] = bld16(rA, coff[r], 0);
+  }
+  u32x4 csk[NRM ? AI : 1];
   if constexpr (NRM) {
     const rsrc_t rK = mk_rsrc(a.skip, a.skip ? M * K * 2u : 0u);
 #pragma unroll
-    for (int i = 0; i < CPL; ++i)
-#pragma unroll
-      for (int d = 0; d < 4; ++d) sraw[i][d] = bld16(rK, aoff[i][d], 0);
+    for (int r = 0; r < AI; ++r) csk[r] = bld16(rK, coff[r], 0);
   }
 
   // Keep the issue order (activations, metadata, weights): the vector-memory
@@ -159,18 +169,15 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
     const uint8_t* s;
     const uint8_t* z;
   };
-  // Scale / zero-point pointers of this lane's column in tile t. Tiles past
-  // the workgroup's last are still loaded (conditional loads would make every
-  // later wait a full drain), from column 0: cache hits, never used.
+  // Scale / zero-point pointers of this lane's column in tile t.
   auto ptrs = [&](int t) -> Ptrs {
-    const uint32_t live = t < static_cast<int>(tpw) ? 0xFFFFFFFFu : 0u;
-    const uint32_t tt = tb + (static_cast<uint32_t>(t) & live);
+    const uint32_t tt = tb + static_cast<uint32_t>(t);
     const uint32_t pi = proj_of(tt);
     const uint32_t N = sel(pi, a.p[0].N, a.p[1].N, a.p[2].N);
     uint32_t col;
     if constexpr (MLP) col = tt * 8u + (j & 7u);
     else col = (tt - sel(pi, a.p[0].t0, a.p[1].t0, a.p[2].t0)) * 16u + j;
-    col = (col < N ? col : N - 1u) & live;  // columns past N: loaded, never stored
+    col = col < N ? col : N - 1u;  // columns past N: loaded, never stored
     Ptrs p;
     p.s = static_cast<const uint8_t*>(sel(pi, a.p[0].S, a.p[1].S, a.p[2].S)) + (static_cast<size_t>(col) * kb + b0) * 2u;
     if constexpr (ZPK == ZP_PACKED)
@@ -182,55 +189,80 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
     return p;
   };
 
-  // ---- scales / zero points of every tile (small; ahead of the weights)
-  SkMeta<SPL> meta[TMAX];
-#pragma unroll
-  for (int t = 0; t < TMAX; ++t) {
-    const Ptrs p = ptrs(t);
-    ld_small<2 * SPL>(p.s, meta[t].s);
-    if constexpr (ZPK == ZP_PACKED) {
-      ld_small<SPL <= 2 ? 1 : SPL / 2>(p.z, meta[t].z);
-    } else if constexpr (ZPK == ZP_FLOAT) {
-      if (a.zesz == 4) ld_small<4 * SPL>(p.z, meta[t].z);
-      else ld_small<2 * SPL>(p.z, meta[t].z);
-    }
-  }
-
-  __builtin_amdgcn_sched_barrier(0);
-
   // ---- weights of the first TQ tiles: the HBM stream starts here
   // Weights are loaded coalesced: load q of a tile reads pieces q*64 + lane
   // of the tile's 16 x CPW chunks in column-major order, so consecutive lanes
   // read consecutive 16-byte pieces of one column (whole 128-byte lines).
   // The wave's LDS slice then transposes them to the MFMA lane order.
   u32x4 wbuf[TQ][CPL];
-  auto issue = [&](int t) {
-    // Tiles past the workgroup's last re-read the first row of a projection
-    // (cache hits, never used). The choice is arithmetic: a branch around the
-    // loads would make every later wait a full drain.
-    const uint32_t live = t < static_cast<int>(tpw) ? 0xFFFFFFFFu : 0u;
-    const uint32_t tt = tb + (static_cast<uint32_t>(t) & live);
+  SkMeta<SPL> mbuf[TQ];
+  // Buffer resources bound each projection's weights: a load of a tile past
+  // the workgroup's last gets an out-of-range offset and returns zeros
+  // without touching memory. (A branch around those loads would make every
+  // later wait a full drain; re-reading real lines would cost bandwidth.)
+  // Each load instruction covers 64 / CPW <= 8 columns that lie in one
+  // projection (Mlp: all gate or all up), so its resource is wave-uniform.
+  static_assert(CPW >= 8, "a load must not straddle the gate / up halves");
+  const rsrc_t rB0 = mk_rsrc(a.p[0].B, a.p[0].N * rowb);
+  const rsrc_t rB1 = mk_rsrc(QKV || MLP ? a.p[1].B : a.p[0].B, (QKV || MLP ? a.p[1].N : a.p[0].N) * rowb);
+  const rsrc_t rB2 = mk_rsrc(QKV ? a.p[2].B : a.p[0].B, (QKV ? a.p[2].N : a.p[0].N) * rowb);
+  // Tile t's scales / zero points, then its weights, into slot u = t % TQ.
+  auto issue = [&](int t, int u) {
+    // all-ones for a live tile; opaque to the compiler, which would otherwise
+    // turn the selects below into branches around the loads
+    uint32_t lm = __builtin_amdgcn_readfirstlane(t < static_cast<int>(tpw) ? 0xFFFFFFFFu : 0u);
+    asm volatile("s_mov_b32 %0, %0" : "+s"(lm));
+    {
+      const Ptrs p = ptrs(static_cast<int>(static_cast<uint32_t>(t) & lm));  // past the last: the first tile's (cached)
+      ld_small<2 * SPL>(p.s, mbuf[u].s);
+      if constexpr (ZPK == ZP_PACKED) {
+        ld_small<SPL <= 2 ? 1 : SPL / 2>(p.z, mbuf[u].z);
+      } else if constexpr (ZPK == ZP_FLOAT) {
+        if (a.zesz == 4) ld_small<4 * SPL>(p.z, mbuf[u].z);
+        else ld_small<2 * SPL>(p.z, mbuf[u].z);
+      }
+    }
+    const uint32_t tt = tb + (static_cast<uint32_t>(t) & lm);
 #pragma unroll
     for (int q = 0; q < CPL; ++q) {
       const uint32_t pc = static_cast<uint32_t>(q * 64 + lane);
       const uint32_t c = pc / CPW, pp = pc % CPW;  // MFMA column and piece of this load
       uint32_t pi, col;
       if constexpr (MLP) {
-        pi = c >> 3;
+        pi = (q * 64 / CPW) >> 3;  // the instruction's half: gate or up
         col = tt * 8u + (c & 7u);
       } else {
         pi = proj_of(tt);
         col = (tt - sel(pi, a.p[0].t0, a.p[1].t0, a.p[2].t0)) * 16u + c;
       }
       const uint32_t N = sel(pi, a.p[0].N, a.p[1].N, a.p[2].N);
-      col = (col < N ? col : N - 1u) & live;  // columns past N: loaded, never stored
-      const uint8_t* src = sel(pi, a.p[0].B, a.p[1].B, a.p[2].B) + (static_cast<size_t>(col) * rowb + (w * CPW + pp) * 16u);
-      wbuf[t % TQ][q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+      col = col < N ? col : N - 1u;  // columns past N: loaded, never stored
+      const uint32_t off = ((col * rowb + (w * CPW + pp) * 16u) & lm) | (0x80000000u & ~lm);
+      wbuf[u][q] = bld16_nt(pi == 0 ? rB0 : pi == 1 ? rB1 : rB2, off, 0);
     }
   };
 #pragma unroll
-  for (int t = 0; t < TQ && t < TMAX; ++t) issue(t);
+  for (int t = 0; t < TQ; ++t) issue(t, t);
   __builtin_amdgcn_sched_barrier(0);
+
+  // ---- transpose the staged activations: lane (j, g) takes row j's pieces
+  // of its chunks g CPL .. g CPL + CPL - 1 (piece 4 chunk + d holds k of
+  // dword d of that chunk)
+  unsigned char* rg = lds[w];
+  auto restage = [&](const u32x4(&src)[AI], u32x4(&dst)[CPL][4]) {
+#pragma unroll
+    for (int r = 0; r < AI; ++r) {
+      const uint32_t e = static_cast<uint32_t>(r * 64 + lane);
+      *reinterpret_cast<u32x4*>(rg + (e / OPR) * XA + (e % OPR) * 16) = src[r];
+    }
+#pragma unroll
+    for (int i = 0; i < CPL; ++i)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) dst[i][d] = *reinterpret_cast<const u32x4*>(rg + j * XA + ((g * CPL + i) * 4 + d) * 16);
+  };
+  u32x4 araw[CPL][4], sraw[NRM ? CPL : 1][4];
+  restage(craw, araw);
+  if constexpr (NRM) restage(csk, sraw);
 
   // ---- prologue (Qkv / Mlp with skip or RMS scale): r = A + skip in
   // float32, x = r * inv * gamma with inv = 1 / sqrt(sum_k r^2 / K + eps)
@@ -291,52 +323,56 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
       for (int d = 0; d < 4; ++d) aop[i][d] = pair_order(__builtin_bit_cast(f16x8, araw[i][d]));
   }
 
-  // ---- tiles: transpose, refill, dequantise, multiply, park the partial
-  // sum in LDS
+  // ---- tiles, in a loop over groups of TQ (the code stays small enough for
+  // the instruction cache): transpose, refill the slot with the tile TQ
+  // ahead, dequantise, multiply, park the partial sum in LDS
+  f32x4* part = reinterpret_cast<f32x4*>(rg);  // [TMAX][64]
+  unsigned char* xb = rg + TMAX * 1024;
+  for (int t0 = 0; t0 < static_cast<int>(tpw); t0 += TQ) {
 #pragma unroll
-  for (int t = 0; t < TMAX; ++t) {
-    // transpose: piece (c, pp) -> lane (j = c, g = pp / CPL), slot pp % CPL;
-    // unconditional, like the refill that follows it
-    unsigned char* xb = xbuf[w];
+    for (int u = 0; u < TQ; ++u) {
+      const int t = t0 + u;
+      // piece (c, pp) -> lane (j = c, g = pp / CPL), slot pp % CPL
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) {
-      const uint32_t pc = static_cast<uint32_t>(q * 64 + lane);
-      *reinterpret_cast<u32x4*>(xb + (pc / CPW) * XS + (pc % CPW) * 16) = wbuf[t % TQ][q];
-    }
-    // refill as soon as the registers are free, pinned there
-    __builtin_amdgcn_sched_barrier(0);
-    if (t + TQ < TMAX) issue(t + TQ);
-    __builtin_amdgcn_sched_barrier(0);
-    u32x4 wt[CPL];
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) wt[i] = *reinterpret_cast<const u32x4*>(xb + j * XS + (g * CPL + i) * 16);
-    if (t < static_cast<int>(tpw)) {  // wave-uniform
-      const SkMeta<SPL>& m = meta[t];
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        const int bi = i * SPL / CPL;  // this chunk's block among the lane's SPL
-        const f16 s = __builtin_bit_cast(f16, static_cast<uint16_t>(m.s[bi >> 1] >> (16 * (bi & 1))));
-        float z = 8.f;
-        if constexpr (ZPK == ZP_PACKED) {
-          const uint32_t sh = SPL == 1 ? (b0 & 1u) * 4u : 4u * bi;
-          z = static_cast<float>((m.z[0] >> sh) & 15u);
-        } else if constexpr (ZPK == ZP_FLOAT) {
-          z = a.zesz == 4 ? __builtin_bit_cast(float, m.z[bi])
-                          : static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(m.z[bi >> 1] >> (16 * (bi & 1)))));
-        }
-        const u32x4 wv = wt[i];
-        if constexpr (ZPK == ZP_FLOAT) {
-          const float sf = static_cast<float>(s);
-#pragma unroll
-          for (int d = 0; d < 4; ++d) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop[i][d], dq8_f32z(wv[d], z, sf), acc, 0, 0, 0);
-        } else {
-          const Dq cst = dq_consts(z, s);
-#pragma unroll
-          for (int d = 0; d < 4; ++d) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop[i][d], dq8(wv[d], cst), acc, 0, 0, 0);
-        }
+      for (int q = 0; q < CPL; ++q) {
+        const uint32_t pc = static_cast<uint32_t>(q * 64 + lane);
+        *reinterpret_cast<u32x4*>(xb + (pc / CPW) * XS + (pc % CPW) * 16) = wbuf[u][q];
       }
-      part[w][t][lane] = acc;
+      const SkMeta<SPL> m = mbuf[u];
+      // refill as soon as the registers are free, pinned there
+      __builtin_amdgcn_sched_barrier(0);
+      issue(t + TQ, u);
+      __builtin_amdgcn_sched_barrier(0);
+      u32x4 wt[CPL];
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) wt[i] = *reinterpret_cast<const u32x4*>(xb + j * XS + (g * CPL + i) * 16);
+      if (t < static_cast<int>(tpw)) {  // wave-uniform
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+          const int bi = i * SPL / CPL;  // this chunk's block among the lane's SPL
+          const f16 s = __builtin_bit_cast(f16, static_cast<uint16_t>(m.s[bi >> 1] >> (16 * (bi & 1))));
+          float z = 8.f;
+          if constexpr (ZPK == ZP_PACKED) {
+            const uint32_t sh = SPL == 1 ? (b0 & 1u) * 4u : 4u * bi;
+            z = static_cast<float>((m.z[0] >> sh) & 15u);
+          } else if constexpr (ZPK == ZP_FLOAT) {
+            z = a.zesz == 4 ? __builtin_bit_cast(float, m.z[bi])
+                            : static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(m.z[bi >> 1] >> (16 * (bi & 1)))));
+          }
+          const u32x4 wv = wt[i];
+          if constexpr (ZPK == ZP_FLOAT) {
+            const float sf = static_cast<float>(s);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop[i][d], dq8_f32z(wv[d], z, sf), acc, 0, 0, 0);
+          } else {
+            const Dq cst = dq_consts(z, s);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop[i][d], dq8(wv[d], cst), acc, 0, 0, 0);
+          }
+        }
+        part[t * 64 + lane] = acc;
+      }
     }
   }
   __syncthreads();
@@ -348,9 +384,10 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
   const uint32_t l = static_cast<uint32_t>(lane);
   const uint32_t jj = l & 15u, gg = l >> 4;
   if (MLP && jj >= 8) return;  // up columns are read by their gate lane
-  f32x4 y = part[0][t][l];
+  auto part_of = [&](int v, uint32_t tl) { return reinterpret_cast<const f32x4*>(lds[v])[tl]; };
+  f32x4 y = part_of(0, t * 64 + l);
 #pragma unroll
-  for (int v = 1; v < W; ++v) y += part[v][t][l];
+  for (int v = 1; v < W; ++v) y += part_of(v, t * 64 + l);
   const uint32_t tt = tb + t;
   const uint32_t pi = MLP ? 0u : proj_of(tt);
   const SkProj& P = a.p[pi];
@@ -359,9 +396,9 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
   if (col >= N) return;
   f16* Y = static_cast<f16*>(P.Y);
   if constexpr (MLP) {
-    f32x4 u = part[0][t][l + 8];
+    f32x4 u = part_of(0, t * 64 + l + 8);
 #pragma unroll
-    for (int v = 1; v < W; ++v) u += part[v][t][l + 8];
+    for (int v = 1; v < W; ++v) u += part_of(v, t * 64 + l + 8);
     const float gb = a.p[0].bias ? static_cast<float>(static_cast<const f16*>(a.p[0].bias)[col]) : 0.f;
     const float ub = a.p[1].bias ? static_cast<float>(static_cast<const f16*>(a.p[1].bias)[col]) : 0.f;
 #pragma unroll
@@ -390,10 +427,13 @@ struct SkShape {
   int w, cpl;
 };
 
+#ifndef XRMM_SK_W128
+#define XRMM_SK_W128 8
+#endif
 inline SkShape sk_shape(const Launch& L) {
   const int64_t chunks = L.kb * L.blob / 16;
   if (chunks == 64) return {8, 2};
-  if (chunks == 128) return {8, 4};
+  if (chunks == 128) return XRMM_SK_W128 == 16 ? SkShape{16, 2} : SkShape{8, 4};
   return {0, 0};
 }
 
@@ -485,7 +525,9 @@ inline hipError_t launch_sk3(const Launch& L, hipStream_t st) {
 
 template <int ZPK, int OPK>
 inline hipError_t launch_sk2(const Launch& L, hipStream_t st) {
-  return sk_shape(L).cpl == 2 ? launch_sk3<ZPK, OPK, 8, 2>(L, st) : launch_sk3<ZPK, OPK, 8, 4>(L, st);
+  const SkShape sh = sk_shape(L);
+  if (sh.w == 16) return launch_sk3<ZPK, OPK, 16, 2>(L, st);
+  return sh.cpl == 2 ? launch_sk3<ZPK, OPK, 8, 2>(L, st) : launch_sk3<ZPK, OPK, 8, 4>(L, st);
 }
 
 // Entry of one zero-point kind (defined in xrmm_gemv_sk_zp.hip).
