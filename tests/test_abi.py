@@ -51,7 +51,9 @@ def test_qkv_requires_norm_scale():
 
 @pytest.mark.parametrize("op,M,K,N,bs,dtype,zp,expect", [
     (0, 1, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_dot"),
-    (0, 4, 4096, 14336, 64, nat.F16, nat.U8, "gemv_q4_dot"),
+    (0, 4, 4096, 14336, 64, nat.F16, nat.U8, "gemv_q4_splitk"),
+    (0, 2, 4096, 14336, 64, nat.F16, nat.U8, "gemv_q4_dot"),
+    (2, 1, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_splitk"),
     (0, 8, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_splitk"),
     (0, 5, 2048, 14336, 64, nat.F16, nat.F16, "gemv_q4_splitk"),
     (0, 16, 1024, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),   # 32 chunks: no even split

@@ -118,7 +118,7 @@ DOT_CASES = [
     (4, 512, 23, 16, "float", True),
     (1, 4096, 2, 32, None, False),
     (4, 8192, 70, 16, "packed", True),       # four rows on 8 waves x 4 columns, 4 KB scale blocks
-    (3, 4096, 100, 32, None, False),         # three rows padded to four, 8 x 4 shape
+    (2, 4096, 100, 32, None, False),         # two rows, the decode layout
 ]
 
 

@@ -278,17 +278,18 @@ static bool q4_fast_ok(const Launch& L) {
 // the 128 x 128 one loses to its lower MFMA rate.
 constexpr int64_t kGemmBigMinM = 128;
 
-// From this many rows (to 16) the split-K MFMA GEMV takes over from the dot
-// GEMV: the dot kernel's VALU work grows with every row, the MFMA's does not.
-#ifndef XRMM_SK_MIN_M
-#define XRMM_SK_MIN_M 5
-#endif
-constexpr int64_t kSplitKMinM = XRMM_SK_MIN_M;
+// Rows from which the split-K MFMA GEMV takes over from the dot GEMV (up to
+// 16 rows): the dot kernel's VALU work grows with every row, the MFMA's does
+// not. Measured with K = 4096: MatMulNBits at two rows is a tie (10.0 vs
+// 10.2 us at N = 14336), at four rows split-K wins (10.8 vs 16.2 us); Qkv at
+// four rows stays on the dot kernel (10.9 vs 16.6 us: 384 tiles leave the
+// split-K grid short of workgroups); Mlp has no dot kernel.
+inline int64_t split_k_min_rows(int op) { return op == OP_MATMUL ? 3 : op == OP_QKV ? 5 : 1; }
 
 Kernel select_kernel(const Launch& L) {
   if (q4_fast_ok(L) && fits_i32(L)) {
+    if (L.M >= split_k_min_rows(L.op) && sk_fits(L)) return K_GEMV_SK;
     if ((L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 && dot_fits(L)) return K_GEMV_DOT;
-    if (L.M >= kSplitKMinM && sk_fits(L)) return K_GEMV_SK;
     if (L.M >= 1 && L.M <= 16 && gemv_tiles(L) != 0) return K_GEMV_Q4;
     if (L.M >= kGemmBigMinM && L.op == OP_MATMUL) return K_GEMM_BIG;
     if (L.M > 16 && L.op == OP_MATMUL && L.zp_kind != ZP_FLOAT) return K_GEMM_Q4;
