@@ -169,6 +169,29 @@ def per_launch_percentiles(torch, fn, n, warmup):
     return t[len(t) // 10], t[len(t) // 2], t[(9 * len(t)) // 10]
 
 
+def dense_fp16_reference(torch, steps: int = 30):
+    """torch.matmul (hipBLASLt) on the prefill shape with dense fp16 weights and
+    random data: the vendor library's dense rate, the context for the fused
+    dequant GEMM's MFMA fraction (it does no dequantisation)."""
+    M, K, N = 2048, 4096, 14336
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    A = torch.randn((M, K), device="cuda", generator=g).half()
+    Ws = [torch.randn((N, K), device="cuda", generator=g).half() for _ in range(2)]
+    for i in range(5):
+        A @ Ws[i % 2].t()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(steps):
+        A @ Ws[i % 2].t()
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / steps
+    return {"what": "torch.matmul fp16 (hipBLASLt), same shape, dense fp16 weights, random data, no dequantisation",
+            "us": round(ms * 1e3, 1), "tflops": round(2 * M * K * N / (ms * 1e-3) / 1e12, 1)}
+
+
 def cpu_baseline(budget_s: float = 20.0):
     """The NumPy oracle on this host for the decode GEMV workload (bounded)."""
     import numpy as np
@@ -274,7 +297,8 @@ def main():
                           "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": FP16_PEAK_TFLOPS,
                                        "unit": "TFLOP/s", "frac": round(tf / FP16_PEAK_TFLOPS, 4),
                                        "flops_per_launch": fl,
-                                       "kernel": ops.select_kernel("MatMulNBits", 2048, 4096, 14336, 4, 128, zp="packed")}}
+                                       "kernel": ops.select_kernel("MatMulNBits", 2048, 4096, 14336, 4, 128, zp="packed")},
+                          "dense_fp16_library": dense_fp16_reference(torch)}
     for name, nbytes in (("qkv_gqa_m4", 13_656_064), ("mlp_swiglu_m16", 66_650_112)):
         if name in results:
             r = results[name]
