@@ -1,11 +1,12 @@
-"""Extract the MatMulNBits-family golden vectors from the reference's fixture JSON.
+"""Extract golden vectors from the reference's fixture JSON: the MatMulNBits
+family and the next operators built on the same dequantisation (QMoE,
+GatherBlockQuantized, MatMulBnb4).
 
 Run in a container that has the reference checkout:
 
     python tests/golden/extract_fixtures.py /root/reference
 
-It reads only data files (the frozen upstream ``test.json`` of the three
-operators) and writes ``tests/golden/fixtures.json``: every case whose inputs
+It reads only data files (the frozen upstream ``test.json`` of those operators) and writes ``tests/golden/fixtures.json``: every case whose inputs
 use the generators the reference's own harness can materialise
 (``values``/``constant``/``cycle``/``linspace``, kernels/_shared/verify_upstream.py:90-122)
 with their explicit expected outputs and tolerances, plus the structural
@@ -20,7 +21,8 @@ import json
 import os
 import sys
 
-OPS = ("com.microsoft.MatMulNBits", "com.microsoft.MatMulNBitsQkv", "com.microsoft.MatMulNBitsMlp")
+OPS = ("com.microsoft.MatMulNBits", "com.microsoft.MatMulNBitsQkv", "com.microsoft.MatMulNBitsMlp",
+       "com.microsoft.QMoE", "com.microsoft.GatherBlockQuantized", "com.microsoft.MatMulBnb4")
 MATERIALIZABLE = {"values", "constant", "cycle", "linspace"}
 
 
