@@ -1,4 +1,4 @@
-/* xrmm: MI355X (gfx950) MatMulNBits / MatMulNBitsQkv / MatMulNBitsMlp.
+/* xrmm: MI355X (gfx950) MatMulNBits / MatMulNBitsQkv / MatMulNBitsMlp, and QMoE.
  *
  * C ABI of libxrmm.so. Plain pointers and sizes only. Every entry point
  * returns XRMM_OK or an error class and leaves a thread-local message for
@@ -233,6 +233,31 @@ int xrmm_close(xrmm_op* op);
 
 /* Close (if open) and free the handle (the reference's destructor). */
 void xrmm_destroy(xrmm_op* op);
+
+/* ---------------------------------------------------------------------------
+ * com.microsoft.QMoE, opcode 1030 (zero-copy, device pointers).
+ * Replaces the serial moe path of
+ * kernels/_shared/extended/shaders/complex_kernel.glsl:158-160 as planned by
+ * kernels/_shared/extended/complex_plan.cpp:121-128 (inputs
+ * inputT,routerT,fc1T,fc1ScalesT,fc2T,fc2ScalesT; output outputT = inputT's
+ * shape). float32 input [T,H] and router [T,E]; fc1 [E,F1,H*bits/8] and fc2
+ * [E,H,I*bits/8] u8, codes low-first, zero point 2^(bits-1); float32 scales
+ * [E,rows] (block_size 0) or [E,rows,cols/block_size]. `activation` is
+ * XRMM_ACT_RELU (swiglu_fusion 0) or XRMM_ACT_SWIGLU (swiglu_fusion 1: FC1
+ * rows 2j / 2j+1 are gate / linear, I = F1/2). `workspace` is device memory of
+ * at least xrmm_qmoe_workspace_bytes(T, k, I) bytes (routing table and the
+ * activated FC1 outputs); calls that share a workspace must not overlap. */
+int64_t xrmm_qmoe_workspace_bytes(int64_t tokens, int32_t k, int64_t inter);
+int xrmm_qmoe(const void* input, const void* router, const void* fc1, const void* fc1_scales, const void* fc2,
+              const void* fc2_scales, void* output, void* workspace, int64_t workspace_bytes, int64_t tokens,
+              int64_t hidden, int64_t experts, int64_t fc1_rows, int32_t k, int32_t bits, int32_t block_size,
+              int32_t activation, int32_t swiglu_fusion, float alpha, float beta, float swiglu_limit,
+              int32_t has_limit, void* stream);
+
+/* Name of the kernel family xrmm_qmoe dispatches a geometry to ("qmoe_rows"
+ * or "qmoe_scalar"), NULL for an invalid geometry. No device work. */
+const char* xrmm_qmoe_kernel(int64_t tokens, int64_t hidden, int64_t experts, int64_t fc1_rows, int32_t k, int32_t bits,
+                             int32_t block_size, int32_t activation, int32_t swiglu_fusion);
 
 #ifdef __cplusplus
 }

@@ -86,8 +86,17 @@ def qmoe(x, router, fc1, fc1_scales, fc2, fc2_scales, *, k: int = 1, activation:
     act = ACT_SWIGLU if activation == "swiglu" else ACT_RELU
     fusion = 2 if (act == ACT_SWIGLU and swiglu_fusion) else 1
     inter = F1 // fusion
-    W1 = expert_weights(fc1, fc1_scales, F1, H, bits, block_size).astype(np.float64)
-    W2 = expert_weights(fc2, fc2_scales, H, inter, bits, block_size).astype(np.float64)
+    fc1 = np.asarray(fc1, np.uint8)
+    fc2 = np.asarray(fc2, np.uint8)
+    s1 = np.asarray(fc1_scales, np.float32)
+    s2 = np.asarray(fc2_scales, np.float32)
+    cache = {}
+
+    def weights(e):  # dequantised per selected expert only (bounded memory)
+        if e not in cache:
+            cache[e] = (expert_weights(fc1[e:e + 1], s1[e:e + 1], F1, H, bits, block_size)[0].astype(np.float64),
+                        expert_weights(fc2[e:e + 1], s2[e:e + 1], H, inter, bits, block_size)[0].astype(np.float64))
+        return cache[e]
     sel, w = route(router, k)
     a = np.float64(np.float32(alpha))
     bta = np.float64(np.float32(beta))
@@ -96,7 +105,8 @@ def qmoe(x, router, fc1, fc1_scales, fc2, fc2_scales, *, k: int = 1, activation:
         for e in range(E):  # ascending expert index, as the shader
             if not sel[t, e]:
                 continue
-            proj = W1[e] @ xr[t]
+            W1e, W2e = weights(e)
+            proj = W1e @ xr[t]
             if act == ACT_SWIGLU:
                 gate = proj[0::2] if fusion == 2 else proj[:inter]
                 lin = proj[1::2] if fusion == 2 else np.zeros(inter)
@@ -107,5 +117,5 @@ def qmoe(x, router, fc1, fc1_scales, fc2, fc2_scales, *, k: int = 1, activation:
                 h = gate * logistic(a * gate) * (lin + bta)
             else:
                 h = np.maximum(proj[:inter], 0.0)
-            out[t] += w[t, e] * (W2[e] @ h)
+            out[t] += w[t, e] * (W2e @ h)
     return out.astype(np.float32).reshape(shape)

@@ -62,6 +62,14 @@ def materialize(spec, seed_key: str = "", substitute: bool = False):
     return arr.reshape(shape)
 
 
+MATERIALIZABLE = ("values", "constant", "cycle", "linspace")
+
+
+def materializable(case) -> bool:
+    """True when every input of ``case`` is given by data the fixture holds."""
+    return all((s.get("data") or {}).get("kind") in MATERIALIZABLE for s in case["inputs"].values())
+
+
 def case_inputs(case, substitute: bool = False):
     return {n: materialize(s, case["name"] + "/" + n, substitute) for n, s in case["inputs"].items()}
 

@@ -9,6 +9,7 @@
 
 #include "../../include/xrmm.h"
 #include "xrmm_internal.h"
+#include "xrmm_moe.h"
 
 namespace {
 
@@ -191,3 +192,94 @@ const char* xrmm_select_kernel(int32_t op, int64_t M, int64_t K, int64_t N, int3
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// com.microsoft.QMoE (opcode 1030)
+
+namespace {
+
+// The planner checks of complex_plan.cpp:121-127 over plain sizes (messages
+// follow the reference's wording); fills the launch block.
+int qmoe_geometry(xrmm::MoeArgs& a, int64_t tokens, int64_t hidden, int64_t experts, int64_t fc1_rows, int32_t k,
+                  int32_t bits, int32_t block_size, int32_t activation, int32_t swiglu_fusion) {
+  if (tokens < 0 || hidden <= 0 || experts < 1 || k < 1 || k > experts)
+    return fail(XRMM_EINVAL, "Invalid MoE input or routing geometry");
+  const bool swiglu = activation == XRMM_ACT_SWIGLU;
+  const int64_t fusion = swiglu && swiglu_fusion ? 2 : 1;
+  if (fc1_rows < 0 || fc1_rows % fusion != 0) return fail(XRMM_EINVAL, "Invalid MoE weight geometry");
+  if (bits != 4 && bits != 8) return fail(XRMM_EINVAL, "Unsupported QMoE integer layout");
+  if (!((activation == XRMM_ACT_RELU && swiglu_fusion == 0) || (swiglu && swiglu_fusion == 1)))
+    return fail(XRMM_EINVAL, "Invalid quantized SwiGLU fusion");
+  const int64_t inter = fc1_rows / fusion;
+  if ((hidden * bits) % 8 != 0 || (inter * bits) % 8 != 0) return fail(XRMM_EINVAL, "Invalid packed expert projection");
+  if (block_size != 0 && (block_size < 16 || (block_size & (block_size - 1)) != 0 || hidden % block_size != 0 ||
+                          inter % block_size != 0))
+    return fail(XRMM_EINVAL, "Invalid quantized expert block size");
+  if (tokens * k > int64_t(1) << 31 || hidden > int64_t(1) << 24 || inter > int64_t(1) << 24)
+    return fail(XRMM_EINVAL, "QMoE geometry beyond 32-bit indexing");
+  std::memset(&a, 0, sizeof(a));
+  a.T = tokens;
+  a.H = hidden;
+  a.E = experts;
+  a.F1 = fc1_rows;
+  a.I = inter;
+  a.k = k;
+  a.bits = bits;
+  a.bs = block_size;
+  a.act = activation;
+  return XRMM_OK;
+}
+
+}  // namespace
+
+int64_t xrmm_qmoe_workspace_bytes(int64_t tokens, int32_t k, int64_t inter) {
+  if (tokens < 0 || k < 1 || inter < 0) return -1;
+  return xrmm::moe_workspace_bytes(tokens, k, inter);
+}
+
+int xrmm_qmoe(const void* input, const void* router, const void* fc1, const void* fc1_scales, const void* fc2,
+              const void* fc2_scales, void* output, void* workspace, int64_t workspace_bytes, int64_t tokens,
+              int64_t hidden, int64_t experts, int64_t fc1_rows, int32_t k, int32_t bits, int32_t block_size,
+              int32_t activation, int32_t swiglu_fusion, float alpha, float beta, float swiglu_limit,
+              int32_t has_limit, void* stream) {
+  xrmm::MoeArgs a;
+  if (int rc = qmoe_geometry(a, tokens, hidden, experts, fc1_rows, k, bits, block_size, activation, swiglu_fusion))
+    return rc;
+  // empty tensors (no intermediate width) may come without storage
+  if (tokens > 0 && (!input || !router || !output || (a.I > 0 && (!fc1 || !fc2 || !fc1_scales || !fc2_scales))))
+    return fail(XRMM_EINVAL, "null tensor pointer");
+  const int64_t need = xrmm::moe_workspace_bytes(tokens, k, a.I);
+  if (tokens > 0 && (!workspace || workspace_bytes < need))
+    return fail(XRMM_EINVAL, "QMoE workspace smaller than xrmm_qmoe_workspace_bytes");
+  auto al = [](int64_t b) { return (b + 255) / 256 * 256; };
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  a.x = static_cast<const float*>(input);
+  a.router = static_cast<const float*>(router);
+  a.fc1 = static_cast<const uint8_t*>(fc1);
+  a.s1 = static_cast<const float*>(fc1_scales);
+  a.fc2 = static_cast<const uint8_t*>(fc2);
+  a.s2 = static_cast<const float*>(fc2_scales);
+  a.y = static_cast<float*>(output);
+  a.sel = reinterpret_cast<int32_t*>(ws);
+  a.wts = reinterpret_cast<float*>(ws + al(tokens * k * 4));
+  a.h = reinterpret_cast<float*>(ws + 2 * al(tokens * k * 4));
+  a.alpha = alpha;
+  a.beta = beta;
+  a.limit = swiglu_limit;
+  a.has_limit = has_limit != 0;
+  const hipError_t e = xrmm::launch_qmoe(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return dev_fail(e, "QMoE launch");
+  return ok();
+}
+
+const char* xrmm_qmoe_kernel(int64_t tokens, int64_t hidden, int64_t experts, int64_t fc1_rows, int32_t k, int32_t bits,
+                             int32_t block_size, int32_t activation, int32_t swiglu_fusion) {
+  xrmm::MoeArgs a;
+  if (qmoe_geometry(a, tokens, hidden, experts, fc1_rows, k, bits, block_size, activation, swiglu_fusion)) return nullptr;
+  // pointers of 16-byte aligned allocations: the choice then depends on the geometry only
+  static const uint8_t probe[16] __attribute__((aligned(16))) = {};
+  a.x = reinterpret_cast<const float*>(probe);
+  a.fc1 = a.fc2 = probe;
+  a.h = reinterpret_cast<float*>(const_cast<uint8_t*>(probe));
+  return xrmm::moe_kernel_name(a);
+}

@@ -173,3 +173,54 @@ def select_kernel(op: str, M, K, N, bits=4, block_size=32, dtype=torch.float16, 
     if r is None:
         raise nat.XrmmInvalid(nat.last_error())
     return r.decode()
+
+
+def qmoe(x, router, fc1, fc1_scales, fc2, fc2_scales, *, k=1, activation="relu", swiglu_fusion=0,
+         expert_weight_bits=4, block_size=0, activation_alpha=1.0, activation_beta=0.0, swiglu_limit=None,
+         workspace=None, stream=None):
+    """com.microsoft.QMoE: ``output`` of ``x``'s shape (float32).
+
+    x ``[..., H]`` float32, router ``[T, E]`` float32, fc1 ``[E, F1, H*bits/8]``
+    and fc2 ``[E, H, I*bits/8]`` uint8, float32 scales ``[E, rows]`` or
+    ``[E, rows, cols/block_size]``. ``workspace`` (uint8 device tensor) is
+    allocated per call when not given.
+    """
+    if activation not in ("relu", "swiglu"):
+        raise nat.XrmmInvalid("Invalid quantized SwiGLU fusion")
+    _check_dev(x, router, fc1, fc1_scales, fc2, fc2_scales, workspace)
+    for t, dt, nm in ((x, torch.float32, "input"), (router, torch.float32, "router"), (fc1, torch.uint8, "fc1"),
+                      (fc2, torch.uint8, "fc2"), (fc1_scales, torch.float32, "fc1 scales"),
+                      (fc2_scales, torch.float32, "fc2 scales")):
+        if t.dtype != dt:
+            raise nat.XrmmInvalid(f"{nm} has the wrong dtype")
+    H = int(x.shape[-1])
+    T = x.numel() // H if H else 0
+    E = int(router.shape[1])
+    F1 = int(fc1.shape[1])
+    act = nat.ACT[activation]
+    fusion = 2 if (activation == "swiglu" and swiglu_fusion) else 1
+    inter = F1 // fusion
+    if int(router.shape[0]) != T or fc1.shape[0] != E or fc2.shape[0] != E or fc2.shape[1] != H:
+        raise nat.XrmmInvalid("Invalid MoE weight geometry")
+    per = 8 // int(expert_weight_bits)
+    if fc1.dim() != 3 or fc2.dim() != 3 or fc1.shape[2] * per != H or fc2.shape[2] * per != inter:
+        raise nat.XrmmInvalid("Invalid packed expert projection")
+    for sc, rows, cols in ((fc1_scales, F1, H), (fc2_scales, H, inter)):
+        want = (E, rows, cols // block_size) if block_size else (E, rows)
+        if tuple(sc.shape) != want:
+            raise nat.XrmmInvalid("Invalid quantized expert scales")
+    y = torch.empty_like(x)
+    need = nat.lib().xrmm_qmoe_workspace_bytes(T, int(k), inter)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    nat.check(nat.lib().xrmm_qmoe(
+        _ptr(x), _ptr(router), _ptr(fc1), _ptr(fc1_scales), _ptr(fc2), _ptr(fc2_scales), _ptr(y), _ptr(workspace),
+        workspace.numel(), T, H, E, F1, int(k), int(expert_weight_bits), int(block_size), act, int(swiglu_fusion),
+        float(activation_alpha), float(activation_beta), float(swiglu_limit or 0.0), int(swiglu_limit is not None),
+        _stream(stream)))
+    return y
+
+
+def qmoe_kernel(T, H, E, F1, k=1, bits=4, block_size=0, activation="relu", swiglu_fusion=0) -> str:
+    r = nat.lib().xrmm_qmoe_kernel(T, H, E, F1, k, bits, block_size, nat.ACT[activation], swiglu_fusion)
+    return r.decode() if r else ""
