@@ -28,7 +28,19 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
 FP16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, published
 PROFILES = os.path.join(ROOT, "profiles")
-SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048": 4}
+SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048": 4, "qmoe_mixtral_t1": 6}
+# com.microsoft.QMoE decode, Mixtral-8x7B expert geometry: T=1, H=4096, I=14336,
+# E=8, k=2, 4-bit codes, float32 scales per block of 64, interleaved SwiGLU
+QMOE = dict(T=1, H=4096, I=14336, E=8, k=2, bits=4, bs=64)
+
+
+def qmoe_algorithmic_bytes(T=1, H=4096, I=14336, k=2, bits=4, bs=64, **_):
+    """Bytes one call must move: the k selected experts' codes and scales of
+    FC1 (2I x H) and FC2 (H x I), the activations, the router row and the
+    output (the float32 intermediate h is the implementation's own)."""
+    fc1 = 2 * I * H * bits // 8 + 2 * I * (H // bs) * 4
+    fc2 = H * I * bits // 8 + H * (I // bs) * 4
+    return k * (fc1 + fc2) + T * (2 * H * 4 + QMOE["E"] * 4)
 
 
 def _gen_weights(torch, g, n, kb, blob, dev):
@@ -72,6 +84,23 @@ def make_replicas(torch, name, R, dev, seed):
                 r[p + "Z"] = torch.randint(0, 256, (n, (kb + 1) // 2), dtype=torch.uint8, device=dev, generator=g)
             reps.append(r)
         return dict(A=A, gamma=gamma, reps=reps, K=K, Nq=Nq, Nkv=Nkv, bs=bs)
+    if name == "qmoe_mixtral_t1":
+        q = QMOE
+        H, I, E, bits, bs = q["H"], q["I"], q["E"], q["bits"], q["bs"]
+        x = torch.randn((q["T"], H), device=dev, generator=g) * 0.5
+        # router rows selecting experts {0,1}, {2,3}, {4,5}, {6,7} with unequal weights
+        routers = []
+        for j in range(E // 2):
+            r = torch.full((q["T"], E), -4.0, device=dev)
+            r[:, 2 * j], r[:, 2 * j + 1] = 1.0, 0.25
+            routers.append(r)
+        for _ in range(R):
+            reps.append(dict(
+                fc1=torch.randint(0, 256, (E, 2 * I, H * bits // 8), dtype=torch.uint8, device=dev, generator=g),
+                s1=torch.rand((E, 2 * I, H // bs), device=dev, generator=g) * 0.019 + 0.001,
+                fc2=torch.randint(0, 256, (E, H, I * bits // 8), dtype=torch.uint8, device=dev, generator=g),
+                s2=torch.rand((E, H, I // bs), device=dev, generator=g) * 0.019 + 0.001))
+        return dict(A=x, routers=routers, reps=reps)
     if name == "mlp_swiglu_m16":
         K, N, bs = 4096, 14336, 32
         A = torch.randn((16, K), device=dev, generator=g).half()
@@ -107,6 +136,18 @@ def step_fn(ops, name, w):
         def f(i):
             r = reps[i % len(reps)]
             return ops.matmul_nbits_mlp(A, r["gB"], r["gS"], r["uB"], r["uS"], block_size=w["bs"])
+        return f
+    if name == "qmoe_mixtral_t1":
+        routers, q = w["routers"], QMOE
+        ws = torch.empty(ops.qmoe_workspace_bytes(q["T"], q["k"], q["H"], q["I"]), dtype=torch.uint8, device=A.device)
+
+        def f(i):
+            # consecutive steps route to disjoint expert pairs of rotating weight
+            # sets, so no step finds its experts in the 256 MB Infinity Cache
+            r = reps[(i // len(routers)) % len(reps)]
+            return ops.qmoe(A, routers[i % len(routers)], r["fc1"], r["s1"], r["fc2"], r["s2"], k=q["k"],
+                            activation="swiglu", swiglu_fusion=1, expert_weight_bits=q["bits"], block_size=q["bs"],
+                            workspace=ws)
         return f
     raise KeyError(name)
 
@@ -239,11 +280,11 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     results = {}
-    names = ["decode_up_m1", "prefill_m2048", "qkv_gqa_m4", "mlp_swiglu_m16"]
+    names = ["decode_up_m1", "prefill_m2048", "qkv_gqa_m4", "mlp_swiglu_m16", "qmoe_mixtral_t1"]
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
     for name in names:
-        R = args.replicas if name != "prefill_m2048" else 2
+        R = {"prefill_m2048": 2, "qmoe_mixtral_t1": 2}.get(name, args.replicas)
         w = make_replicas(torch, name, R, dev, seed=SEEDS[name])
         fn = step_fn(ops, name, w)
         steps = args.steps if name != "prefill_m2048" else max(10, args.steps // 10)
@@ -305,6 +346,15 @@ def main():
             gbs = nbytes / (r["ms"] * 1e-3) / 1e9
             out[name] = {"us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                          "bytes_per_launch": nbytes}
+    if "qmoe_mixtral_t1" in results:
+        r, q = results["qmoe_mixtral_t1"], QMOE
+        nbytes = qmoe_algorithmic_bytes(**q)
+        gbs = nbytes / (r["ms"] * 1e-3) / 1e9
+        out["qmoe_mixtral_t1"] = {
+            "workload": "QMoE T=1 H=4096 I=14336 E=8 k=2 bits=4 block_size=64 interleaved SwiGLU (Mixtral-8x7B experts)",
+            "us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": nbytes, "kernel": ops.qmoe_kernel(q["T"], q["H"], q["E"], 2 * q["I"], q["k"], q["bits"],
+                                                                   q["bs"], "swiglu", 1)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

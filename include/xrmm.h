@@ -245,9 +245,10 @@ void xrmm_destroy(xrmm_op* op);
  * [E,rows] (block_size 0) or [E,rows,cols/block_size]. `activation` is
  * XRMM_ACT_RELU (swiglu_fusion 0) or XRMM_ACT_SWIGLU (swiglu_fusion 1: FC1
  * rows 2j / 2j+1 are gate / linear, I = F1/2). `workspace` is device memory of
- * at least xrmm_qmoe_workspace_bytes(T, k, I) bytes (routing table and the
- * activated FC1 outputs); calls that share a workspace must not overlap. */
-int64_t xrmm_qmoe_workspace_bytes(int64_t tokens, int32_t k, int64_t inter);
+ * at least xrmm_qmoe_workspace_bytes(T, k, H, I) bytes (routing table, the
+ * activated FC1 outputs, per-slot FC2 partials and their arrival counters);
+ * calls that share a workspace must not overlap. */
+int64_t xrmm_qmoe_workspace_bytes(int64_t tokens, int32_t k, int64_t hidden, int64_t inter);
 int xrmm_qmoe(const void* input, const void* router, const void* fc1, const void* fc1_scales, const void* fc2,
               const void* fc2_scales, void* output, void* workspace, int64_t workspace_bytes, int64_t tokens,
               int64_t hidden, int64_t experts, int64_t fc1_rows, int32_t k, int32_t bits, int32_t block_size,

@@ -95,6 +95,12 @@ RAND = [
     (2, 96, 40, 3, 2, 4, 0, "swiglu", None, "qmoe_scalar"),       # rows of 48 / 20 bytes
     (3, 72, 40, 4, 1, 8, 0, "relu", None, "qmoe_scalar"),         # rows of 72 / 40 bytes
     (3, 80, 48, 4, 1, 8, 16, "relu", None, "qmoe_rows"),          # 8-bit block 16: one scale per chunk
+    # long FC1 / FC2 rows: several row groups per wave in FC1, FC2 reductions
+    # split into segments combined by the last workgroup of each row tile
+    (1, 1024, 16384, 4, 2, 4, 64, "swiglu", None, "qmoe_rows"),
+    (2, 512, 8192, 4, 2, 8, 0, "relu", None, "qmoe_rows"),
+    (1, 256, 20480, 3, 3, 4, 16, "swiglu", 4.0, "qmoe_rows"),
+    (1, 256, 4096, 2, 1, 4, 32, "swiglu", None, "qmoe_rows"),     # k = 1: segments only
 ]
 
 
@@ -110,6 +116,22 @@ def test_seeded_shapes(gpu, T, H, I, E, k, bits, bs, act, limit, kernel):
     ref = run_oracle(i, at)
     ok, err, lim = O.tolerance_ok(got, ref, np.float32)
     assert ok, f"max|d|={err} > {lim}"
+
+
+def test_split_reduction_is_deterministic(gpu):
+    # the combined FC2 partials are summed in a fixed order: repeated calls
+    # (fresh and reused workspaces) give identical bits
+    rng = np.random.default_rng(99)
+    i = rand_case(rng, 1, 1024, 16384, 4, 4, 64, True)
+    at = dict(k=2, activation="swiglu", swiglu_fusion=1, bits=4, block_size=64, alpha=1.0, beta=0.0, swiglu_limit=None)
+    first = run_gpu(i, at)
+    d = {n: dev(v) for n, v in i.items()}
+    ws = torch.empty(ops().qmoe_workspace_bytes(1, 2, 1024, 16384), dtype=torch.uint8, device="cuda")
+    for _ in range(3):
+        again = ops().qmoe(d["inputT"], d["routerT"], d["fc1T"], d["fc1ScalesT"], d["fc2T"], d["fc2ScalesT"], k=2,
+                           activation="swiglu", swiglu_fusion=1, expert_weight_bits=4, block_size=64,
+                           workspace=ws).cpu().numpy()
+        assert np.array_equal(first, again)
 
 
 def test_rank3_and_empty(gpu):

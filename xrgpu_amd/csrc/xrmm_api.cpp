@@ -232,9 +232,9 @@ int qmoe_geometry(xrmm::MoeArgs& a, int64_t tokens, int64_t hidden, int64_t expe
 
 }  // namespace
 
-int64_t xrmm_qmoe_workspace_bytes(int64_t tokens, int32_t k, int64_t inter) {
-  if (tokens < 0 || k < 1 || inter < 0) return -1;
-  return xrmm::moe_workspace_bytes(tokens, k, inter);
+int64_t xrmm_qmoe_workspace_bytes(int64_t tokens, int32_t k, int64_t hidden, int64_t inter) {
+  if (tokens < 0 || k < 1 || hidden < 0 || inter < 0) return -1;
+  return xrmm::moe_workspace_bytes(tokens, k, hidden, inter);
 }
 
 int xrmm_qmoe(const void* input, const void* router, const void* fc1, const void* fc1_scales, const void* fc2,
@@ -248,7 +248,7 @@ int xrmm_qmoe(const void* input, const void* router, const void* fc1, const void
   // empty tensors (no intermediate width) may come without storage
   if (tokens > 0 && (!input || !router || !output || (a.I > 0 && (!fc1 || !fc2 || !fc1_scales || !fc2_scales))))
     return fail(XRMM_EINVAL, "null tensor pointer");
-  const int64_t need = xrmm::moe_workspace_bytes(tokens, k, a.I);
+  const int64_t need = xrmm::moe_workspace_bytes(tokens, k, hidden, a.I);
   if (tokens > 0 && (!workspace || workspace_bytes < need))
     return fail(XRMM_EINVAL, "QMoE workspace smaller than xrmm_qmoe_workspace_bytes");
   auto al = [](int64_t b) { return (b + 255) / 256 * 256; };
@@ -263,6 +263,10 @@ int xrmm_qmoe(const void* input, const void* router, const void* fc1, const void
   a.sel = reinterpret_cast<int32_t*>(ws);
   a.wts = reinterpret_cast<float*>(ws + al(tokens * k * 4));
   a.h = reinterpret_cast<float*>(ws + 2 * al(tokens * k * 4));
+  const int64_t ksmax = xrmm::moe_fc2_segments_max(tokens, k, hidden, (a.I + 1023) / 1024);
+  a.yp = reinterpret_cast<float*>(ws + 2 * al(tokens * k * 4) + al(tokens * k * a.I * 4));
+  a.cnt = reinterpret_cast<uint32_t*>(ws + 2 * al(tokens * k * 4) + al(tokens * k * a.I * 4) +
+                                      al(tokens * k * ksmax * hidden * 4));
   a.alpha = alpha;
   a.beta = beta;
   a.limit = swiglu_limit;

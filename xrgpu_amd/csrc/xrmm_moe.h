@@ -21,17 +21,39 @@ struct MoeArgs {
   int32_t* sel;          // workspace [T, k]: selected experts, ascending index
   float* wts;            // workspace [T, k]: their softmax weights
   float* h;              // workspace [T, k, I]: activated FC1 outputs
+  float* yp;             // workspace [T, k, ks, H]: FC2 partial outputs per slot and segment
+  uint32_t* cnt;         // workspace [T, moe_tiles2(H)]: FC2 arrival counters
   int64_t T, H, E, F1, I;
   int k, bits, bs, act;
   float alpha, beta, limit;
   int has_limit;
+  int ks, seg, clear;    // FC2 reduction segments, steps per segment; FC1 clears cnt
+  int lbs;               // log2(block_size) (block sizes are powers of two)
 };
 
-// Workspace bytes for T tokens, k slots, intermediate width I (three
-// 256-byte-aligned regions: sel, wts, h).
-inline int64_t moe_workspace_bytes(int64_t T, int64_t k, int64_t I) {
+// Row tiles of the FC2 launch (32 rows each): one arrival counter per token
+// and tile.
+inline int64_t moe_tiles2(int64_t H) { return (H + 31) / 32; }
+
+// FC2 splits its reduction into up to this many segments so that a small
+// batch still launches about `wgs` (at most 1024) workgroups: steps is the
+// number of 64-chunk steps of an FC2 row.
+inline int64_t moe_fc2_segments_max(int64_t T, int64_t k, int64_t H, int64_t steps, int64_t wgs = 1024) {
+  const int64_t base = T * k * moe_tiles2(H);
+  if (base <= 0) return 1;
+  if (wgs > 1024) wgs = 1024;
+  int64_t ks = (wgs + base - 1) / base;
+  if (ks > steps) ks = steps;
+  return ks < 1 ? 1 : ks;
+}
+
+// Workspace bytes for T tokens, k slots, hidden width H, intermediate width
+// I: five 256-byte-aligned regions (sel, wts, h, yp, cnt). The segment bound
+// uses 8-bit rows, which have the most steps.
+inline int64_t moe_workspace_bytes(int64_t T, int64_t k, int64_t H, int64_t I) {
   auto al = [](int64_t b) { return (b + 255) / 256 * 256; };
-  return al(T * k * 4) + al(T * k * 4) + al(T * k * I * 4);
+  const int64_t ks = moe_fc2_segments_max(T, k, H, (I + 1023) / 1024);
+  return al(T * k * 4) + al(T * k * 4) + al(T * k * I * 4) + al(T * k * ks * H * 4) + al(T * moe_tiles2(H) * 4);
 }
 
 bool moe_fast_ok(const MoeArgs& a);

@@ -10,22 +10,23 @@
 // experts only; FC1 rows 2j / 2j + 1 are gate / linear for SwiGLU (fusion 1),
 // row j for ReLU; experts are combined in ascending index order.
 //
-// Three launches on the caller's stream:
-//  1. k_moe_route: one wave per token; writes the k selected experts (ascending
-//     index) and their softmax weights into the workspace.
-//  2. k_moe_rows (FC1): a workgroup stages the token's activation vector once
-//     in LDS; each wave owns RPW consecutive rows of the selected expert's FC1
-//     and walks K with 16-byte weight loads per lane (the next step's loads in
-//     flight while the current step is computed); activation applied in the
-//     epilogue; h [T, k, I] float32 in the workspace.
-//  3. k_moe_rows (FC2): the same kernel over the hidden rows of each selected
-//     expert's FC2, the activation vector being h of that (token, slot),
-//     accumulated with the routing weight over the k slots.
-// Arithmetic is float32 throughout: per dword the codes convert with
-// v_cvt_f32_ubyte (low and high nibbles masked into separate bytes) and
-// accumulate (code - midpoint, exact) with FMAs against the activations; the
-// scale multiplies the group's sum (block scales) or the row's total (row
-// scales).
+// Geometries with 16-byte rows (every practical one) take two launches on the
+// caller's stream:
+//  1. k_moe_gemv FC1: one workgroup per (token, slot) pair and tile of 64
+//     FC1 rows. It routes the token itself (the rank rule above, softmax over
+//     the selected logits), stages x in LDS and streams the selected expert's
+//     rows with 16-byte loads per lane, the next unit's weights and scales in
+//     flight while the current one is computed; the activation runs in the
+//     epilogue; h [T, k, I] float32 goes to the workspace.
+//  2. k_moe_gemv FC2: the same loop over each pair's FC2 rows against h,
+//     partial outputs per slot; the last workgroup of a (token, tile) to
+//     arrive sums the k partials with the routing weights in slot order.
+// Codes become (code - midpoint) exactly in binary16 (magic-number
+// construction) and multiply into float32 sums with v_fma_mix_f32; a scale
+// multiplies the sum of its block (or the row's total for row scales). Other
+// geometries take a routing kernel and one-thread-per-output kernels.
+#include <algorithm>
+
 #include "xrmm_device.h"
 #include "xrmm_moe.h"
 
@@ -98,6 +99,9 @@ __global__ __launch_bounds__(MOE_T) void k_moe_route(const float* __restrict__ r
 enum Stage { ST_FC1_RELU = 0, ST_FC1_SWIGLU = 1, ST_FC2 = 2 };
 enum ScaleMode { SM_ROW = 0, SM_CHUNK = 1, SM_HALF = 2 };  // scales per row / per 16-byte chunk / per 8-byte half
 
+constexpr int MOE_RPW = 8;     // rows of one group: loaded together, reduced together
+constexpr int MOE_MAX_K = 64;  // slots of one token in the fused routing
+
 __device__ __forceinline__ float swiglu(float gate, float lin, const MoeArgs& a) {
   if (a.has_limit) {
     gate = fminf(gate, a.limit);
@@ -108,154 +112,387 @@ __device__ __forceinline__ float swiglu(float gate, float lin, const MoeArgs& a)
   return gate * lg * (lin + a.beta);
 }
 
-// sum over the codes of one dword of a chunk against their activations:
-// (q - mid) is formed exactly in float32 before its product (taking mid out
-// through the activation sum instead would cancel most of the bits for
-// 8-bit codes, whose midpoint is 128)
+// The codes of one dword minus the midpoint, as exact binary16 pairs
+// (0x6400 | c is 1024 + c and 0x6400 | (c << 4) is 1024 + 16c, so one
+// subtraction or one multiply-add by 1/16 leaves c - mid), each multiplied
+// into the float32 sum against its activation (binary16 -> float32 is exact;
+// the compiler fuses the conversion into v_fma_mix_f32). 4-bit pairs:
+// (c0,c4) (c1,c5) (c2,c6) (c3,c7); 8-bit pairs: (c0,c2) (c1,c3).
 template <int BITS>
 __device__ __forceinline__ float dword_dot(uint32_t w, const float* x, float acc) {
-  constexpr float mid = static_cast<float>(1 << (BITS - 1));
+  const uint32_t magic = 0x64006400u;
   if constexpr (BITS == 4) {
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-    acc = __builtin_fmaf(static_cast<float>(lo & 0xFFu) - mid, x[0], acc);
-    acc = __builtin_fmaf(static_cast<float>(hi & 0xFFu) - mid, x[1], acc);
-    acc = __builtin_fmaf(static_cast<float>((lo >> 8) & 0xFFu) - mid, x[2], acc);
-    acc = __builtin_fmaf(static_cast<float>((hi >> 8) & 0xFFu) - mid, x[3], acc);
-    acc = __builtin_fmaf(static_cast<float>((lo >> 16) & 0xFFu) - mid, x[4], acc);
-    acc = __builtin_fmaf(static_cast<float>((hi >> 16) & 0xFFu) - mid, x[5], acc);
-    acc = __builtin_fmaf(static_cast<float>(lo >> 24) - mid, x[6], acc);
-    return __builtin_fmaf(static_cast<float>(hi >> 24) - mid, x[7], acc);
+    const f16x2 n1032 = {static_cast<f16>(-1032.f), static_cast<f16>(-1032.f)};
+    const f16x2 inv16 = {static_cast<f16>(0.0625f), static_cast<f16>(0.0625f)};
+    const f16x2 n72 = {static_cast<f16>(-72.f), static_cast<f16>(-72.f)};
+    const uint32_t w8 = w >> 8;
+    const f16x2 d0 = as_h2(and_or(w, 0x000F000Fu, magic)) + n1032;
+    const f16x2 d1 = __builtin_elementwise_fma(as_h2(and_or(w, 0x00F000F0u, magic)), inv16, n72);
+    const f16x2 d2 = as_h2(and_or(w8, 0x000F000Fu, magic)) + n1032;
+    const f16x2 d3 = __builtin_elementwise_fma(as_h2(and_or(w8, 0x00F000F0u, magic)), inv16, n72);
+    acc = __builtin_fmaf(static_cast<float>(d0[0]), x[0], acc);
+    acc = __builtin_fmaf(static_cast<float>(d1[0]), x[1], acc);
+    acc = __builtin_fmaf(static_cast<float>(d2[0]), x[2], acc);
+    acc = __builtin_fmaf(static_cast<float>(d3[0]), x[3], acc);
+    acc = __builtin_fmaf(static_cast<float>(d0[1]), x[4], acc);
+    acc = __builtin_fmaf(static_cast<float>(d1[1]), x[5], acc);
+    acc = __builtin_fmaf(static_cast<float>(d2[1]), x[6], acc);
+    return __builtin_fmaf(static_cast<float>(d3[1]), x[7], acc);
   } else {
-    acc = __builtin_fmaf(static_cast<float>(w & 0xFFu) - mid, x[0], acc);
-    acc = __builtin_fmaf(static_cast<float>((w >> 8) & 0xFFu) - mid, x[1], acc);
-    acc = __builtin_fmaf(static_cast<float>((w >> 16) & 0xFFu) - mid, x[2], acc);
-    return __builtin_fmaf(static_cast<float>(w >> 24) - mid, x[3], acc);
+    const f16x2 n1152 = {static_cast<f16>(-1152.f), static_cast<f16>(-1152.f)};
+    const f16x2 d0 = as_h2(and_or(w, 0x00FF00FFu, magic)) + n1152;
+    const f16x2 d1 = as_h2(and_or(w >> 8, 0x00FF00FFu, magic)) + n1152;
+    acc = __builtin_fmaf(static_cast<float>(d0[0]), x[0], acc);
+    acc = __builtin_fmaf(static_cast<float>(d1[0]), x[1], acc);
+    acc = __builtin_fmaf(static_cast<float>(d0[1]), x[2], acc);
+    return __builtin_fmaf(static_cast<float>(d1[1]), x[3], acc);
   }
 }
 
-template <int BITS, int SM, int ST, int RPW>
-__global__ __launch_bounds__(MOE_T) void k_moe_rows(MoeArgs a) {
+// Wave sums of eight per-lane values in 10 exchanges instead of 48: each
+// exchange over lane bit 5, 4 and 3 halves the values a lane keeps, then
+// bits 2..0 finish the sum. Lane l returns the sum of row
+// row8(l) = 4*bit3 + 2*bit4 + bit5.
+__device__ __forceinline__ int row8(int lane) { return ((lane >> 3) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 5) & 1); }
+
+__device__ __forceinline__ float reduce8(const float (&v)[8], int lane) {
+  float a4[4], a2[2];
+  const bool h5 = (lane & 32) != 0, h4 = (lane & 16) != 0, h3 = (lane & 8) != 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a4[i] = (h5 ? v[2 * i + 1] : v[2 * i]) + __shfl_xor(h5 ? v[2 * i] : v[2 * i + 1], 32, 64);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) a2[i] = (h4 ? a4[2 * i + 1] : a4[2 * i]) + __shfl_xor(h4 ? a4[2 * i] : a4[2 * i + 1], 16, 64);
+  float a1 = (h3 ? a2[1] : a2[0]) + __shfl_xor(h3 ? a2[0] : a2[1], 8, 64);
+  a1 += __shfl_xor(a1, 4, 64);
+  a1 += __shfl_xor(a1, 2, 64);
+  return a1 + __shfl_xor(a1, 1, 64);
+}
+
+__device__ __forceinline__ float bld_f32(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, bld_u32(r, voff, soff));
+}
+
+// LDS layout of an activation vector: the CPC floats of 16-byte chunk c sit
+// at c * (CPC + 4), so the 64 lanes of a wave reading their own chunks with
+// 16-byte reads hit disjoint banks in every group of 16 lanes.
+template <int CPC>
+__device__ __forceinline__ int64_t lds_index(int64_t i) {
+  return (i / CPC) * (CPC + 4) + (i % CPC);
+}
+
+// Copies n floats (a multiple of 4, 16-byte aligned) into LDS in the chunk
+// layout above, zero-filled up to kpad (a multiple of 1024): float4 loads,
+// four per thread in flight before their stores.
+template <int CPC>
+__device__ __forceinline__ void stage_vec(float* dst, const float* __restrict__ src, int64_t n, int64_t kpad) {
+  const int tid = threadIdx.x;
+  for (int64_t base = 0; base < kpad; base += 16 * MOE_T) {
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t i = base + (static_cast<int64_t>(j) * MOE_T + tid) * 4;
+      v[j] = i < n ? *reinterpret_cast<const float4*>(src + i) : float4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t i = base + (static_cast<int64_t>(j) * MOE_T + tid) * 4;
+      if (i < kpad) *reinterpret_cast<float4*>(dst + lds_index<CPC>(i)) = v[j];
+    }
+  }
+}
+
+// Routing of one token inside the FC1 prologue (complex_kernel.glsl:159-160):
+// an expert's rank counts the experts with a larger logit, or an equal logit
+// and a larger index; the experts of rank < k, in ascending index order, fill
+// the slots; the weights are the softmax over the selected logits, maximum and
+// denominator taken in ascending index order. Every thread of the workgroup
+// calls it; `lr` holds the token's E logits in LDS, `fl` (E ints) and `sl`
+// (MOE_MAX_K ints) are LDS scratch. The slot's expert and weight come back
+// through `out_e` / `out_w` (LDS) after the final barrier.
+__device__ void route_slot(int E, int k, int slot, const float* lr, int* fl, int* sl, int* out_e, float* out_w) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  for (int e = tid; e < E; e += MOE_T) {
+    const float v = lr[e];
+    int rank = 0;
+    for (int e2 = 0; e2 < E; ++e2) {
+      const float o = lr[e2];
+      rank += (o > v || (o == v && e2 > e)) ? 1 : 0;
+    }
+    fl[e] = rank < k ? 1 : 0;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    // NaN logits rank 0 and can push the count past k: slots past k are dropped
+    int base = 0;
+    for (int e0 = 0; e0 < E && base < k; e0 += 64) {
+      const int e = e0 + lane;
+      const bool s = e < E && fl[e] != 0;
+      const uint64_t m = __ballot(s);
+      const int pos = base + __popcll(m & ((uint64_t(1) << lane) - 1));
+      if (s && pos < k) sl[pos] = e;
+      base += __popcll(m);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    if (tid == 0) {
+      float mx = -__builtin_huge_valf();
+      for (int s = 0; s < k; ++s) mx = fmaxf(mx, lr[sl[s]]);
+      float den = 0.f;
+      for (int s = 0; s < k; ++s) den += expf(lr[sl[s]] - mx);
+      *out_e = sl[slot];
+      *out_w = expf(lr[sl[slot]] - mx) / den;
+    }
+  }
+  __syncthreads();
+}
+
+// One expert matrix (FC1 or FC2) against the activation vector of each
+// (token, slot) pair. Workgroup b covers pair, row tile and reduction segment
+// (b / (tiles * a.ks), (b / a.ks) % tiles, b % a.ks): rows
+// [tile * 32 * gpw, +32 * gpw), steps [kseg * a.seg, +a.seg) of 64
+// sixteen-byte chunks. Each of its 4 waves owns gpw groups of 8 consecutive
+// rows; a unit of work is one group over one step (one chunk per lane), and
+// the loads of unit u + 1 (weights and their scales) are in flight while unit
+// u is computed. Rows and chunks past the end load through out-of-range
+// buffer offsets, which read zero and touch no memory.
+//
+// FC1 (ST_FC1_*, one segment): routes the pair's token, stages x in LDS,
+// writes the activated outputs h[pair] (SwiGLU rows 2j / 2j+1 fall in one
+// group) and clears the FC2 arrival counters. FC2: stages its segment of
+// h[pair] and writes a partial output per (slot, segment); the last of the
+// k * a.ks workgroups of a (token, row tile) to arrive sums the partials
+// (segments, then slots with their routing weights) in a fixed order, so the
+// result does not depend on scheduling. With k = 1 and one segment FC2
+// writes the output directly.
+#ifndef XRMM_MOE_FC1_WGS
+#define XRMM_MOE_FC1_WGS 1024  // FC1 workgroups to aim at: four resident per CU
+#endif
+#ifndef XRMM_MOE_FC2_WGS
+#define XRMM_MOE_FC2_WGS 1024  // FC2 workgroups to aim at through reduction segments
+#endif
+
+template <int BITS, int SM, int ST>
+__global__ __launch_bounds__(MOE_T) void k_moe_gemv(MoeArgs a, int gpw, int tiles, int tiles2) {
   extern __shared__ __align__(16) float xs[];
+  __shared__ int s_e, s_last;
+  __shared__ float s_w;
+  constexpr int RPW = MOE_RPW;
   constexpr int CPC = 128 / BITS;  // codes per 16-byte chunk
   constexpr int CPD = 32 / BITS;   // codes per dword
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const bool fc2 = ST == ST_FC2;
-  const int64_t Kd = fc2 ? a.I : a.H;    // reduction length (codes per row)
-  const int64_t Nd = fc2 ? a.H : a.F1;   // rows of one expert's matrix
+  constexpr int NS = SM == SM_HALF ? 2 : 1;
+  constexpr bool fc2 = ST == ST_FC2;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ks = fc2 ? a.ks : 1;
+  const int64_t pair = blockIdx.x / (static_cast<uint32_t>(tiles) * ks);
+  const int tile = static_cast<int>((blockIdx.x / ks) % tiles);
+  const int kseg = static_cast<int>(blockIdx.x % ks);
+  const int64_t t = pair / a.k;
+  const int slot = static_cast<int>(pair % a.k);
+  const int64_t Kd = fc2 ? a.I : a.H;            // reduction length (codes per row)
+  const int Nd = static_cast<int>(fc2 ? a.H : a.F1);  // rows of one expert's matrix
   const uint32_t rowb = static_cast<uint32_t>(Kd * BITS / 8);
-  const int64_t kpad = (Kd + 64 * CPC - 1) / (64 * CPC) * (64 * CPC);
-  const int steps = static_cast<int>(kpad / (64 * CPC));
-  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (MOE_T / 64) + wave) * RPW;
-  const int64_t spr = SM == SM_ROW ? 1 : Kd / a.bs;  // scales per row
-  const uint8_t* W = fc2 ? a.fc2 : a.fc1;
-  const float* S = fc2 ? a.s2 : a.s1;
+  const uint32_t chunks = rowb / 16;
+  const int steps = static_cast<int>((chunks + 63) / 64);
+  const int s0 = fc2 ? kseg * a.seg : 0;
+  const int nst = fc2 ? min(a.seg, steps - s0) : steps;  // steps of this segment
+  const int64_t k_lo = static_cast<int64_t>(s0) * 64 * CPC;
+  const int64_t kpad = static_cast<int64_t>(nst) * 64 * CPC;
+  const int64_t kpad_lds = kpad / CPC * (CPC + 4);
+  const uint32_t spr = SM == SM_ROW ? 1u : static_cast<uint32_t>(Kd >> a.lbs);  // scales per row
+  const int row_base = (tile * 4 + wave) * (RPW * gpw);
+  const int E = static_cast<int>(a.E);
+  const bool combine = a.k * ks > 1;
 
-  // FC1: one (token, slot) per blockIdx.y; FC2: one token, every slot
-  const int64_t p = blockIdx.y;
-  const int nslots = fc2 ? a.k : 1;
-  float yacc[RPW];
-#pragma unroll
-  for (int r = 0; r < RPW; ++r) yacc[r] = 0.f;
-
-  for (int sl = 0; sl < nslots; ++sl) {
-    const int64_t pair = fc2 ? p * a.k + sl : p;
-    const int e = min(max(a.sel[pair], 0), static_cast<int>(a.E) - 1);  // an index out of range can never be read
-    const float wgt = fc2 ? a.wts[pair] : 1.f;
-    // stage the activation vector (zero-padded to whole steps)
-    const float* src = fc2 ? a.h + pair * a.I : a.x + (pair / a.k) * a.H;
-    if (sl > 0) __syncthreads();  // every wave is done with the previous vector
-    for (int64_t i = tid; i < kpad; i += MOE_T) xs[i] = i < Kd ? src[i] : 0.f;
+  int e;
+  float wgt = 1.f;
+  if constexpr (!fc2) {
+    float* lr = xs + kpad_lds;
+    int* fl = reinterpret_cast<int*>(lr + E);
+    int* sl = fl + E;
+    const float* lsrc = a.router + t * a.E;
+    for (int i = tid; i < E; i += MOE_T) lr[i] = lsrc[i];
+    stage_vec<CPC>(xs, a.x + t * a.H, Kd, kpad);
+    if (a.clear)
+      for (int64_t i = static_cast<int64_t>(blockIdx.x) * MOE_T + tid; i < a.T * tiles2;
+           i += static_cast<int64_t>(gridDim.x) * MOE_T)
+        a.cnt[i] = 0u;
     __syncthreads();
+    route_slot(E, a.k, slot, lr, fl, sl, &s_e, &s_w);
+    e = s_e;
+    if (tile == 0 && tid == 0) {
+      a.sel[pair] = s_e;
+      a.wts[pair] = s_w;
+    }
+  } else {
+    e = min(max(a.sel[pair], 0), E - 1);  // an index out of range can never be read
+    wgt = a.wts[pair];
+  }
 
-    const uint8_t* We = W + static_cast<int64_t>(e) * Nd * rowb;
-    const float* Se = S + static_cast<int64_t>(e) * Nd * spr;
-    const rsrc_t rW = mk_rsrc(We, static_cast<uint32_t>(Nd) * rowb);
-    float acc[RPW];
+  const uint8_t* We = (fc2 ? a.fc2 : a.fc1) + static_cast<int64_t>(e) * Nd * rowb;
+  const float* Se = (fc2 ? a.s2 : a.s1) + static_cast<int64_t>(e) * Nd * spr;
+  const rsrc_t rW = mk_rsrc(We, static_cast<uint32_t>(Nd) * rowb);
+  const rsrc_t rS = mk_rsrc(Se, static_cast<uint32_t>(Nd) * spr * 4u);
+  const int myrow = row8(lane);
+
+  struct Buf {
+    u32x4 w[RPW];
+    float s[RPW][NS];
+    float rs;  // row scale of row8(lane) (block_size 0)
+  };
+  // Loads of unit (g, s): rows are wave-uniform, so each row's offset is a
+  // scalar operand (clamped to the last row: rows past the end read real
+  // memory and are never written); the lane's chunk is the vector offset,
+  // out of range past the row end or past the wave's last group.
+  auto issue = [&](Buf& b, int g, int s) {
+    const uint32_t c = static_cast<uint32_t>(s) * 64u + static_cast<uint32_t>(lane);
+    const bool in = g < gpw && c < chunks;
+    const uint32_t voff = in ? c * 16u : 0x80000000u;
+    const int row0 = row_base + g * RPW;
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = 0.f;
-    auto ld = [&](u32x4(&w)[RPW], int s) {
-      const uint32_t c = static_cast<uint32_t>(s * 64 + lane);  // chunk of the row
-      const bool in = static_cast<int64_t>(c) * CPC < Kd;
+    for (int r = 0; r < RPW; ++r)
+      b.w[r] = bld16_nt(rW, voff, static_cast<uint32_t>(min(row0 + r, Nd - 1)) * rowb);
+    if constexpr (SM != SM_ROW) {
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) {
-        const int64_t row = row0 + r;
-        const uint32_t off = (in && row < Nd) ? static_cast<uint32_t>(row) * rowb + c * 16u : 0x80000000u;
-        w[r] = bld16_nt(rW, off, 0);
+      for (int q = 0; q < NS; ++q) {
+        const uint32_t so = in ? ((c * CPC + q * (CPC / NS)) >> a.lbs) * 4u : 0x80000000u;
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+          b.s[r][q] = bld_f32(rS, so, static_cast<uint32_t>(min(row0 + r, Nd - 1)) * spr * 4u);
       }
-    };
-    u32x4 wb[2][RPW];
-    ld(wb[0], 0);
-    for (int s = 0; s < steps; ++s) {
-      if (s + 1 < steps) ld(wb[(s + 1) & 1], s + 1);
-      const int64_t k0 = (static_cast<int64_t>(s) * 64 + lane) * CPC;
-      float xv[CPC];
+    } else {
+      b.rs = bld_f32(rS, g < gpw ? static_cast<uint32_t>(min(row0 + myrow, Nd - 1)) * 4u : 0x80000000u, 0);
+    }
+  };
+
+  Buf buf[2];
+  issue(buf[0], 0, s0);
+  if constexpr (fc2) {
+    // this segment of h, zero-padded to whole steps, staged while unit 0 loads
+    stage_vec<CPC>(xs, a.h + pair * a.I + k_lo, min(Kd - k_lo, kpad), kpad);
+    __syncthreads();
+  }
+
+  float acc[RPW];
 #pragma unroll
-      for (int q = 0; q < CPC / 4; ++q) {
-        const float4 v = *reinterpret_cast<const float4*>(xs + k0 + 4 * q);
+  for (int r = 0; r < RPW; ++r) acc[r] = 0.f;
+
+  auto consume = [&](const Buf& b, int g, int s) {
+    const int sl = s - s0;  // step within the segment
+    const float* xq = xs + (static_cast<int64_t>(sl) * 64 + lane) * (CPC + 4);
+    float part[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) part[r] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      float xv[CPD];
+#pragma unroll
+      for (int q = 0; q < CPD / 4; ++q) {
+        const float4 v = *reinterpret_cast<const float4*>(xq + d * CPD + 4 * q);
         xv[4 * q] = v.x;
         xv[4 * q + 1] = v.y;
         xv[4 * q + 2] = v.z;
         xv[4 * q + 3] = v.w;
       }
-      constexpr int G = SM == SM_HALF ? 2 : 1;  // scale groups per chunk
-      const bool in = k0 < Kd;
 #pragma unroll
       for (int r = 0; r < RPW; ++r) {
-        const u32x4 w = wb[s & 1][r];
-#pragma unroll
-        for (int gi = 0; gi < G; ++gi) {
-          if constexpr (SM == SM_ROW) {
-#pragma unroll
-            for (int d = 0; d < 4; ++d) acc[r] = dword_dot<BITS>(w[d], xv + d * CPD, acc[r]);
-          } else {
-            float part = 0.f;
-#pragma unroll
-            for (int d = gi * 4 / G; d < (gi + 1) * 4 / G; ++d) part = dword_dot<BITS>(w[d], xv + d * CPD, part);
-            const int64_t row = row0 + r;
-            const float sc = (in && row < Nd) ? Se[row * spr + (k0 + gi * CPC / G) / a.bs] : 0.f;
-            acc[r] = __builtin_fmaf(sc, part, acc[r]);
-          }
-        }
-      }
-    }
-    // wave sums; row scale for per-row scales
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      float v = wave_sum(acc[r]);
-      const int64_t row = row0 + r;
-      if constexpr (SM == SM_ROW) v *= row < Nd ? Se[row] : 0.f;
-      acc[r] = v;
-    }
-    if constexpr (ST == ST_FC2) {
-#pragma unroll
-      for (int r = 0; r < RPW; ++r) yacc[r] = __builtin_fmaf(wgt, acc[r], yacc[r]);
-    } else {
-      // FC1 epilogue: activation, h[pair][j]
-      float* hp = a.h + pair * a.I;
-      if (lane == 0) {
-        if constexpr (ST == ST_FC1_SWIGLU) {
-#pragma unroll
-          for (int r = 0; r + 1 < RPW; r += 2) {
-            const int64_t j = (row0 + r) / 2;
-            if (row0 + r + 1 < Nd) hp[j] = swiglu(acc[r], acc[r + 1], a);
-          }
+        if constexpr (SM == SM_ROW) {
+          acc[r] = dword_dot<BITS>(b.w[r][d], xv, acc[r]);
         } else {
-#pragma unroll
-          for (int r = 0; r < RPW; ++r)
-            if (row0 + r < Nd) hp[row0 + r] = fmaxf(acc[r], 0.f);
+          part[r] = dword_dot<BITS>(b.w[r][d], xv, part[r]);
+          if (NS == 2 && d == 1) {  // first of two scale blocks complete
+            acc[r] = __builtin_fmaf(b.s[r][0], part[r], acc[r]);
+            part[r] = 0.f;
+          }
         }
       }
     }
-  }
-  if constexpr (ST == ST_FC2) {
-    if (lane == 0) {
+    if constexpr (SM != SM_ROW) {
 #pragma unroll
-      for (int r = 0; r < RPW; ++r)
-        if (row0 + r < Nd) a.y[p * a.H + row0 + r] = yacc[r];
+      for (int r = 0; r < RPW; ++r) acc[r] = __builtin_fmaf(b.s[r][NS - 1], part[r], acc[r]);
+    }
+    if (sl == nst - 1) {  // the group is complete: reduce, scale, write
+      float v = reduce8(acc, lane);
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) acc[r] = 0.f;
+      if constexpr (SM == SM_ROW) v *= b.rs;
+      const int row = row_base + g * RPW + myrow;
+      if constexpr (ST == ST_FC1_SWIGLU) {
+        const float lin = __shfl_xor(v, 32, 64);  // row + 1
+        if ((lane & 39) == 0 && row + 1 < Nd) a.h[pair * a.I + row / 2] = swiglu(v, lin, a);
+      } else if constexpr (ST == ST_FC1_RELU) {
+        if ((lane & 7) == 0 && row < Nd) a.h[pair * a.I + row] = fmaxf(v, 0.f);
+      } else {
+        if ((lane & 7) == 0 && row < Nd) {
+          if (!combine)
+            a.y[t * a.H + row] = wgt * v;
+          else  // device-coherent store: read back by another workgroup
+            __hip_atomic_store(a.yp + (pair * ks + kseg) * a.H + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+  };
+
+  // units in (group, step) order, two per trip so the buffers are named
+  // statically; (g, s) past the wave's last group load nothing
+  int g = 0, s = s0;
+  auto next = [&](int& gg, int& ss) {
+    if (++ss == s0 + nst) {
+      ss = s0;
+      ++gg;
+    }
+  };
+  // (the scheduling barriers keep each unit's loads ahead of the previous
+  // unit's arithmetic: the memory counter retires in issue order)
+  while (g < gpw) {
+    int g1 = g, s1 = s;
+    next(g1, s1);
+    issue(buf[1], g1, s1);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(buf[0], g, s);
+    int g2 = g1, s2 = s1;
+    next(g2, s2);
+    issue(buf[0], g2, s2);
+    __builtin_amdgcn_sched_barrier(0);
+    if (g1 < gpw) consume(buf[1], g1, s1);
+    g = g2;
+    s = s2;
+  }
+
+  if constexpr (fc2) {
+    if (combine) {
+      // The partials went out as device-coherent stores; once every one of
+      // them has completed (s_waitcnt 0 in each thread, then the barrier) the
+      // arrival is counted, and the last of the token's k * ks workgroups on
+      // this row tile reads them back with device-coherent loads and sums
+      // them. No cache-wide write-back or invalidation is needed.
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tid == 0)
+        s_last = __hip_atomic_fetch_add(a.cnt + t * tiles2 + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 static_cast<uint32_t>(a.k * ks - 1);
+      __syncthreads();
+      if (s_last) {
+        const int rows = 4 * RPW * gpw;
+        for (int i = tid; i < rows; i += MOE_T) {
+          const int row = tile * rows + i;
+          if (row < Nd) {
+            float y = 0.f;
+            for (int s = 0; s < a.k; ++s) {
+              const float* p = a.yp + (t * a.k + s) * ks * a.H + row;
+              float v = 0.f;
+              for (int q = 0; q < ks; ++q)
+                v += __hip_atomic_load(p + static_cast<int64_t>(q) * a.H, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              y = __builtin_fmaf(a.wts[t * a.k + s], v, y);
+            }
+            a.y[t * a.H + row] = y;
+          }
+        }
+      }
     }
   }
 }
-
 // ---------------------------------------------------------------------------
 // scalar fallback (any shape): one thread per output element
 
@@ -309,13 +546,20 @@ __global__ __launch_bounds__(MOE_T) void k_moe_zero(float* y, int64_t n) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <int BITS, int SM, int ST, int RPW>
-hipError_t launch_rows(const MoeArgs& a, hipStream_t st) {
+// Floats of LDS for an activation vector of kd codes (whole steps, padded
+// chunk layout).
+int64_t moe_kpad(int64_t kd, int bits) {
+  const int64_t cpc = 128 / bits, per_step = 64 * cpc;
+  return (kd + per_step - 1) / per_step * 64 * (cpc + 4);
+}
+
+template <int BITS, int SM, int ST>
+hipError_t launch_gemv(const MoeArgs& a, int gpw, hipStream_t st) {
   const bool fc2 = ST == ST_FC2;
-  const int64_t Kd = fc2 ? a.I : a.H, Nd = fc2 ? a.H : a.F1;
-  const int64_t kpad = (Kd + 64 * (128 / BITS) - 1) / (64 * (128 / BITS)) * (64 * (128 / BITS));
-  const size_t lds = static_cast<size_t>(kpad) * sizeof(float);
-  auto kern = k_moe_rows<BITS, SM, ST, RPW>;
+  const int64_t Nd = fc2 ? a.H : a.F1;
+  const int64_t per_step_lds = 64 * (128 / BITS + 4);
+  const size_t lds = static_cast<size_t>(fc2 ? a.seg * per_step_lds : moe_kpad(a.H, BITS) + 2 * a.E + MOE_MAX_K) * 4;
+  auto kern = k_moe_gemv<BITS, SM, ST>;
   if (lds > 64 * 1024) {
     static bool raised = false;  // per instantiation
     if (!raised) {
@@ -325,54 +569,62 @@ hipError_t launch_rows(const MoeArgs& a, hipStream_t st) {
       raised = true;
     }
   }
-  const int64_t rows_per_wg = (MOE_T / 64) * RPW;
-  const dim3 grid(static_cast<uint32_t>((Nd + rows_per_wg - 1) / rows_per_wg),
-                  static_cast<uint32_t>(fc2 ? a.T : a.T * a.k));
-  hipLaunchKernelGGL(kern, grid, dim3(MOE_T), lds, st, a);
+  const int64_t tiles = (Nd + 32 * gpw - 1) / (32 * gpw);
+  const int64_t blocks = a.T * a.k * tiles * (fc2 ? a.ks : 1);
+  hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(blocks)), dim3(MOE_T), lds, st, a, gpw, static_cast<int>(tiles),
+                     static_cast<int>(moe_tiles2(a.H)));
   return hipGetLastError();
 }
 
 template <int BITS, int SM>
-hipError_t launch_fast(const MoeArgs& a, hipStream_t st) {
-  hipError_t e = a.act == XRMM_ACT_SWIGLU_CODE ? launch_rows<BITS, SM, ST_FC1_SWIGLU, 16>(a, st)
-                                               : launch_rows<BITS, SM, ST_FC1_RELU, 16>(a, st);
+hipError_t launch_fast(const MoeArgs& args, hipStream_t st) {
+  MoeArgs a = args;
+  const int64_t steps2 = (a.I * BITS / 8 / 16 + 63) / 64;
+  const int64_t ks0 = moe_fc2_segments_max(a.T, a.k, a.H, steps2, XRMM_MOE_FC2_WGS);
+  a.seg = static_cast<int>((steps2 + ks0 - 1) / ks0);
+  a.ks = static_cast<int>((steps2 + a.seg - 1) / a.seg);
+  a.clear = a.k * a.ks > 1;
+  a.lbs = a.bs ? __builtin_ctz(static_cast<unsigned>(a.bs)) : 0;
+  // FC1 row groups per wave: enough rows per workgroup that the launch stays
+  // within one resident round
+  const int64_t tiles32 = a.T * a.k * ((a.F1 + 31) / 32);
+  const int gpw1 = static_cast<int>(std::min<int64_t>(16, std::max<int64_t>(1, (tiles32 + XRMM_MOE_FC1_WGS - 1) / XRMM_MOE_FC1_WGS)));
+  hipError_t e = a.act == XRMM_ACT_SWIGLU_CODE ? launch_gemv<BITS, SM, ST_FC1_SWIGLU>(a, gpw1, st)
+                                               : launch_gemv<BITS, SM, ST_FC1_RELU>(a, gpw1, st);
   if (e != hipSuccess) return e;
-  return launch_rows<BITS, SM, ST_FC2, 4>(a, st);
+  return launch_gemv<BITS, SM, ST_FC2>(a, 1, st);
 }
 
 }  // namespace
 
 bool moe_fast_ok(const MoeArgs& a) {
-  // whole 16-byte chunks per row, aligned tensors, activation vectors within LDS
+  // whole 16-byte chunks per row, aligned tensors, vectors within LDS
   if ((a.H * a.bits / 8) % 16 != 0 || (a.I * a.bits / 8) % 16 != 0) return false;
   if (!aligned16(a.x) || !aligned16(a.fc1) || !aligned16(a.fc2) || !aligned16(a.h)) return false;
-  const int64_t cpc = 128 / a.bits;
-  for (int64_t kd : {a.H, a.I}) {
-    const int64_t kpad = (kd + 64 * cpc - 1) / (64 * cpc) * (64 * cpc);
-    if (kpad * 4 > kMoeMaxLds) return false;
-  }
+  if ((moe_kpad(a.H, a.bits) + 2 * a.E + MOE_MAX_K) * 4 > kMoeMaxLds || moe_kpad(a.I, a.bits) * 4 > kMoeMaxLds)
+    return false;
+  if (a.k > MOE_MAX_K || a.E > 4096) return false;
   if (a.act == XRMM_ACT_SWIGLU_CODE && a.F1 % 2 != 0) return false;
-  // one expert's matrix within a 32-bit buffer range
+  // each expert's code and scale matrices within a 32-bit buffer range
   const int64_t lim = int64_t(1) << 31;
+  const int64_t spr1 = a.bs ? a.H / a.bs : 1, spr2 = a.bs ? a.I / a.bs : 1;
   if (a.F1 * a.H * a.bits / 8 >= lim || a.H * a.I * a.bits / 8 >= lim) return false;
-  // block scales: a whole number of blocks per 16-byte chunk, or two per chunk
-  if (a.bs != 0 && a.bs < cpc / 2) return false;
-  return a.T * a.k <= 65535 && a.T <= 65535;
+  if (a.F1 * spr1 * 4 >= lim || a.H * spr2 * 4 >= lim) return false;
+  // block scales: whole blocks per 16-byte chunk, or two blocks per chunk
+  if (a.bs != 0 && a.bs < 64 / a.bits) return false;
+  return a.T * a.k * ((a.F1 + 31) / 32) < (int64_t(1) << 31) && a.T * a.k * moe_tiles2(a.H) * 1024 < (int64_t(1) << 31);
 }
 
 const char* moe_kernel_name(const MoeArgs& a) { return moe_fast_ok(a) ? "qmoe_rows" : "qmoe_scalar"; }
 
 hipError_t launch_qmoe(const MoeArgs& a, hipStream_t st) {
   if (a.T == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_moe_route, dim3(static_cast<uint32_t>((a.T + 3) / 4)), dim3(MOE_T), 0, st, a.router, a.sel, a.wts,
-                     static_cast<int>(a.T), static_cast<int>(a.E), a.k);
-  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   if (a.I == 0) {  // no intermediate width: every expert contributes zero
     hipLaunchKernelGGL(k_moe_zero, dim3(static_cast<uint32_t>((a.T * a.H + MOE_T - 1) / MOE_T)), dim3(MOE_T), 0, st, a.y,
                        a.T * a.H);
     return hipGetLastError();
   }
-  if (moe_fast_ok(a)) {
+  if (moe_fast_ok(a)) {  // routing runs inside the FC1 launch
     const int cpc = 128 / a.bits;
     const int sm = a.bs == 0 ? SM_ROW : a.bs >= cpc ? SM_CHUNK : SM_HALF;
     if (a.bits == 4) {
@@ -381,9 +633,11 @@ hipError_t launch_qmoe(const MoeArgs& a, hipStream_t st) {
       return launch_fast<4, SM_HALF>(a, st);
     }
     if (sm == SM_ROW) return launch_fast<8, SM_ROW>(a, st);
-    if (sm == SM_CHUNK) return launch_fast<8, SM_CHUNK>(a, st);
-    return launch_fast<8, SM_HALF>(a, st);
+    return launch_fast<8, SM_CHUNK>(a, st);
   }
+  hipLaunchKernelGGL(k_moe_route, dim3(static_cast<uint32_t>((a.T + 3) / 4)), dim3(MOE_T), 0, st, a.router, a.sel, a.wts,
+                     static_cast<int>(a.T), static_cast<int>(a.E), a.k);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   hipLaunchKernelGGL(k_moe_fc1_scalar, dim3(static_cast<uint32_t>((a.T * a.k * a.I + MOE_T - 1) / MOE_T)), dim3(MOE_T), 0,
                      st, a);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;

@@ -210,15 +210,19 @@ def qmoe(x, router, fc1, fc1_scales, fc2, fc2_scales, *, k=1, activation="relu",
         if tuple(sc.shape) != want:
             raise nat.XrmmInvalid("Invalid quantized expert scales")
     y = torch.empty_like(x)
-    need = nat.lib().xrmm_qmoe_workspace_bytes(T, int(k), inter)
     if workspace is None:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+        workspace = torch.empty(qmoe_workspace_bytes(T, k, H, inter), dtype=torch.uint8, device=x.device)
     nat.check(nat.lib().xrmm_qmoe(
         _ptr(x), _ptr(router), _ptr(fc1), _ptr(fc1_scales), _ptr(fc2), _ptr(fc2_scales), _ptr(y), _ptr(workspace),
         workspace.numel(), T, H, E, F1, int(k), int(expert_weight_bits), int(block_size), act, int(swiglu_fusion),
         float(activation_alpha), float(activation_beta), float(swiglu_limit or 0.0), int(swiglu_limit is not None),
         _stream(stream)))
     return y
+
+
+def qmoe_workspace_bytes(T, k, hidden, inter) -> int:
+    """Bytes of device workspace ``qmoe`` needs (routing table, h, FC2 partials)."""
+    return max(int(nat.lib().xrmm_qmoe_workspace_bytes(int(T), int(k), int(hidden), int(inter))), 1)
 
 
 def qmoe_kernel(T, H, E, F1, k=1, bits=4, block_size=0, activation="relu", swiglu_fusion=0) -> str:
