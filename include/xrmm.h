@@ -1,4 +1,5 @@
-/* xrmm: MI355X (gfx950) MatMulNBits / MatMulNBitsQkv / MatMulNBitsMlp, and QMoE.
+/* xrmm: MI355X (gfx950) MatMulNBits / MatMulNBitsQkv / MatMulNBitsMlp, QMoE,
+ * GatherBlockQuantized and MatMulBnb4.
  *
  * C ABI of libxrmm.so. Plain pointers and sizes only. Every entry point
  * returns XRMM_OK or an error class and leaves a thread-local message for
@@ -259,6 +260,39 @@ int xrmm_qmoe(const void* input, const void* router, const void* fc1, const void
  * or "qmoe_scalar"), NULL for an invalid geometry. No device work. */
 const char* xrmm_qmoe_kernel(int64_t tokens, int64_t hidden, int64_t experts, int64_t fc1_rows, int32_t k, int32_t bits,
                              int32_t block_size, int32_t activation, int32_t swiglu_fusion);
+
+/* ---------------------------------------------------------------------------
+ * com.microsoft.GatherBlockQuantized, opcode 1031 (gatherQuant,
+ * kernels/_shared/extended/shaders/complex_kernel.glsl:85; planner
+ * complex_plan.cpp:129). data [rows, packed_cols] uint8 (codes low-first),
+ * indices [n_indices] (XRMM_I32 / XRMM_U32 read as int32, or XRMM_I64
+ * saturated to int32, as controlIndex does), float32 scales [rows, blocks]
+ * with blocks = ceil(width / block_size), width = packed_cols * 8 / bits,
+ * optional packed zero points [rows, ceil(blocks * bits / 8)] (NULL: the
+ * midpoint 2^(bits-1)); output float32 [n_indices, width]. bits 4 or 8,
+ * block_size a power of two >= 16. An index outside [0, rows) leaves its
+ * output row zero and, when `status` (a device uint32, caller-zeroed) is not
+ * NULL, raises it to 55 with an atomic max: the code the reference's run
+ * fails with ("GPU operator contract validation failed: code 55",
+ * vulkan.cpp:115). Enqueues on `stream` and returns. */
+int xrmm_gather_block_quantized(const void* data, const void* indices, int32_t indices_dtype, const void* scales,
+                                const void* zero_points, void* output, void* status, int64_t rows,
+                                int64_t packed_cols, int64_t n_indices, int32_t bits, int32_t block_size,
+                                void* stream);
+
+/* com.microsoft.MatMulBnb4, opcode 1026 (bnbWeight complex_kernel.glsl:82, the
+ * 1026 branch of packedMatmul :83; planner complex_plan.cpp:117-120).
+ * A [M, K] and absmax [ceil(N*K / block_size)] in `dtype` (XRMM_F32 or
+ * XRMM_F16), B the flat [N, K] (trans_b != 0, the default) or [K, N] weight
+ * as ceil(N*K / 2) bytes, two codes per byte with the even flat index in the
+ * high nibble; quant_type 1 = NF4, 0 = FP4. Y [M, N] in `dtype`. */
+int xrmm_matmul_bnb4(const void* A, const void* B, const void* absmax, void* Y, int64_t M, int64_t K, int64_t N,
+                     int32_t block_size, int32_t quant_type, int32_t trans_b, int32_t dtype, void* stream);
+
+/* Kernel family xrmm_matmul_bnb4 picks ("bnb4_gemv" or "bnb4_scalar"), NULL
+ * for an invalid geometry. No device work. */
+const char* xrmm_matmul_bnb4_kernel(int64_t M, int64_t K, int64_t N, int32_t block_size, int32_t quant_type,
+                                    int32_t trans_b, int32_t dtype);
 
 #ifdef __cplusplus
 }

@@ -60,6 +60,10 @@ def _sig(lib):
     s("xrmm_qmoe", ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
       _i32, _i32, _i32, _f32, _f32, _f32, _i32, _vp)
     s("xrmm_qmoe_kernel", ctypes.c_char_p, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32)
+    s("xrmm_gather_block_quantized", ctypes.c_int, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32,
+      _vp)
+    s("xrmm_matmul_bnb4", ctypes.c_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _vp)
+    s("xrmm_matmul_bnb4_kernel", ctypes.c_char_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32)
 
 
 def lib():

@@ -37,6 +37,7 @@ UNITS = [
     ("xrmm_gemm_zp.hip", ["-DXRMM_ZPK=1"], "gemm_zp1.o"),
     ("xrmm_gemm_zp.hip", ["-DXRMM_ZPK=2"], "gemm_zp2.o"),
     ("xrmm_moe.hip", [], "moe.o"),
+    ("xrmm_quant.hip", [], "quant.o"),
     ("xrmm_api.cpp", [], "api.o"),
     ("xrmm_operator.cpp", [], "operator.o"),
 ]

@@ -10,6 +10,7 @@
 #include "../../include/xrmm.h"
 #include "xrmm_internal.h"
 #include "xrmm_moe.h"
+#include "xrmm_quant.h"
 
 namespace {
 
@@ -286,4 +287,90 @@ const char* xrmm_qmoe_kernel(int64_t tokens, int64_t hidden, int64_t experts, in
   a.fc1 = a.fc2 = probe;
   a.h = reinterpret_cast<float*>(const_cast<uint8_t*>(probe));
   return xrmm::moe_kernel_name(a);
+}
+
+// ---------------------------------------------------------------------------
+// com.microsoft.GatherBlockQuantized (opcode 1031), com.microsoft.MatMulBnb4 (1026)
+
+int xrmm_gather_block_quantized(const void* data, const void* indices, int32_t indices_dtype, const void* scales,
+                                const void* zero_points, void* output, void* status, int64_t rows,
+                                int64_t packed_cols, int64_t n_indices, int32_t bits, int32_t block_size,
+                                void* stream) {
+  // complex_plan.cpp:129
+  if ((bits != 4 && bits != 8) || block_size < 16 || (block_size & (block_size - 1)) != 0)
+    return fail(XRMM_EINVAL, "Unsupported GatherBlockQuantized geometry");
+  if (rows < 0 || packed_cols < 0 || n_indices < 0) return fail(XRMM_EINVAL, "Unsupported GatherBlockQuantized geometry");
+  if (indices_dtype != XRMM_I32 && indices_dtype != XRMM_U32 && indices_dtype != XRMM_I64)
+    return fail(XRMM_EINVAL, "Logical dtype outside frozen contract: indicesT");
+  xrmm::GbqArgs a{};
+  a.width = packed_cols * (8 / bits);
+  a.blocks = (a.width + block_size - 1) / block_size;
+  a.zpcols = (a.blocks * bits + 7) / 8;
+  if (n_indices > 0 && a.width > 0 && (!data || !indices || !scales || !output))
+    return fail(XRMM_EINVAL, "null tensor pointer");
+  if (n_indices * a.width >= (int64_t(1) << 40)) return fail(XRMM_EINVAL, "GatherBlockQuantized output too large");
+  a.data = static_cast<const uint8_t*>(data);
+  a.idx = indices;
+  a.idx64 = indices_dtype == XRMM_I64;
+  a.scales = static_cast<const float*>(scales);
+  a.zp = static_cast<const uint8_t*>(zero_points);
+  a.out = static_cast<float*>(output);
+  a.status = static_cast<uint32_t*>(status);
+  a.rows = rows;
+  a.pcols = packed_cols;
+  a.n = n_indices;
+  a.bits = bits;
+  a.bs = block_size;
+  const hipError_t e = xrmm::launch_gbq(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return dev_fail(e, "GatherBlockQuantized launch");
+  return ok();
+}
+
+namespace {
+
+int bnb4_geometry(xrmm::Bnb4Args& a, int64_t M, int64_t K, int64_t N, int32_t block_size, int32_t quant_type,
+                  int32_t trans_b, int32_t dtype) {
+  // complex_plan.cpp:117-120
+  if (!t1_ok(dtype)) return fail(XRMM_EINVAL, "Logical dtype outside frozen contract: aT");
+  if (K <= 0 || block_size <= 0) return fail(XRMM_EINVAL, "Invalid packed matmul geometry");
+  if (N <= 0) return fail(XRMM_EINVAL, "Packed matmul N required");
+  if (M < 0) return fail(XRMM_EINVAL, "Invalid packed matmul geometry");
+  if (quant_type != 0 && quant_type != 1) return fail(XRMM_EINVAL, "MatMulBnb4 quant_type must be 0 (FP4) or 1 (NF4)");
+  if (N * K >= (int64_t(1) << 40)) return fail(XRMM_EINVAL, "MatMulBnb4 weight too large");
+  a = xrmm::Bnb4Args{};
+  a.M = M;
+  a.K = K;
+  a.N = N;
+  a.bs = block_size;
+  a.qt = quant_type;
+  a.tb = trans_b != 0;
+  a.f16 = dtype == XRMM_F16;
+  return XRMM_OK;
+}
+
+}  // namespace
+
+int xrmm_matmul_bnb4(const void* A, const void* B, const void* absmax, void* Y, int64_t M, int64_t K, int64_t N,
+                     int32_t block_size, int32_t quant_type, int32_t trans_b, int32_t dtype, void* stream) {
+  xrmm::Bnb4Args a;
+  if (int rc = bnb4_geometry(a, M, K, N, block_size, quant_type, trans_b, dtype)) return rc;
+  if (M > 0 && (!A || !B || !absmax || !Y)) return fail(XRMM_EINVAL, "null tensor pointer");
+  a.A = A;
+  a.B = static_cast<const uint8_t*>(B);
+  a.absmax = absmax;
+  a.Y = Y;
+  const hipError_t e = xrmm::launch_bnb4(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return dev_fail(e, "MatMulBnb4 launch");
+  return ok();
+}
+
+const char* xrmm_matmul_bnb4_kernel(int64_t M, int64_t K, int64_t N, int32_t block_size, int32_t quant_type,
+                                    int32_t trans_b, int32_t dtype) {
+  xrmm::Bnb4Args a;
+  if (bnb4_geometry(a, M, K, N, block_size, quant_type, trans_b, dtype)) return nullptr;
+  static const uint8_t probe[16] __attribute__((aligned(16))) = {};
+  a.A = probe;
+  a.B = probe;
+  ok();
+  return xrmm::bnb4_fast_ok(a) ? "bnb4_gemv" : "bnb4_scalar";
 }

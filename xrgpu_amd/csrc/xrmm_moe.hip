@@ -149,25 +149,6 @@ __device__ __forceinline__ float dword_dot(uint32_t w, const float* x, float acc
   }
 }
 
-// Wave sums of eight per-lane values in 10 exchanges instead of 48: each
-// exchange over lane bit 5, 4 and 3 halves the values a lane keeps, then
-// bits 2..0 finish the sum. Lane l returns the sum of row
-// row8(l) = 4*bit3 + 2*bit4 + bit5.
-__device__ __forceinline__ int row8(int lane) { return ((lane >> 3) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 5) & 1); }
-
-__device__ __forceinline__ float reduce8(const float (&v)[8], int lane) {
-  float a4[4], a2[2];
-  const bool h5 = (lane & 32) != 0, h4 = (lane & 16) != 0, h3 = (lane & 8) != 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) a4[i] = (h5 ? v[2 * i + 1] : v[2 * i]) + __shfl_xor(h5 ? v[2 * i] : v[2 * i + 1], 32, 64);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) a2[i] = (h4 ? a4[2 * i + 1] : a4[2 * i]) + __shfl_xor(h4 ? a4[2 * i] : a4[2 * i + 1], 16, 64);
-  float a1 = (h3 ? a2[1] : a2[0]) + __shfl_xor(h3 ? a2[0] : a2[1], 8, 64);
-  a1 += __shfl_xor(a1, 4, 64);
-  a1 += __shfl_xor(a1, 2, 64);
-  return a1 + __shfl_xor(a1, 1, 64);
-}
-
 __device__ __forceinline__ float bld_f32(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, bld_u32(r, voff, soff));
 }

@@ -1,0 +1,38 @@
+// Internal interface of the GatherBlockQuantized and MatMulBnb4 paths
+// (xrmm_quant.hip): argument blocks, launches and kernel choice.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace xrmm {
+
+constexpr uint32_t kGbqIndexError = 55;  // the shader's failure code for an out-of-range index
+
+struct GbqArgs {
+  const uint8_t* data;  // [rows, pcols] packed codes, low-first
+  const void* idx;      // [n] int32 (or uint32 read as int32) / int64
+  int idx64;
+  const float* scales;  // [rows, blocks]
+  const uint8_t* zp;    // [rows, zpcols] packed zero points, or null (midpoint)
+  float* out;           // [n, width]
+  uint32_t* status;     // device word receiving kGbqIndexError (max), or null
+  int64_t rows, pcols, n, width, blocks, zpcols;
+  int bits, bs;
+};
+
+bool gbq_fast_ok(const GbqArgs& a);
+hipError_t launch_gbq(const GbqArgs& a, hipStream_t st);
+
+struct Bnb4Args {
+  const void* A;       // [M, K] float32 / float16
+  const uint8_t* B;    // flat [N * K] codes, two per byte, even index in the high nibble
+  const void* absmax;  // [ceil(N * K / bs)] in A's dtype
+  void* Y;             // [M, N] in A's dtype
+  int64_t M, K, N;
+  int bs, qt, tb, f16;
+};
+
+bool bnb4_fast_ok(const Bnb4Args& a);
+hipError_t launch_bnb4(const Bnb4Args& a, hipStream_t st);
+
+}  // namespace xrmm

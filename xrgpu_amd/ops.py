@@ -228,3 +228,77 @@ def qmoe_workspace_bytes(T, k, hidden, inter) -> int:
 def qmoe_kernel(T, H, E, F1, k=1, bits=4, block_size=0, activation="relu", swiglu_fusion=0) -> str:
     r = nat.lib().xrmm_qmoe_kernel(T, H, E, F1, k, bits, block_size, nat.ACT[activation], swiglu_fusion)
     return r.decode() if r else ""
+
+
+_IDX = {torch.int32: nat.I32, torch.int64: nat.I64}
+
+
+def gather_block_quantized(data, indices, scales, zero_points=None, *, bits=4, block_size=128, status=None,
+                           check=True, stream=None):
+    """com.microsoft.GatherBlockQuantized: float32 ``[len(indices), width]``.
+
+    data ``[rows, packed_cols]`` uint8, indices int32/int64 ``[n]``, float32
+    scales ``[rows, blocks]``, optional packed uint8 zero points. An index out
+    of range leaves its row zero and raises the device word ``status`` (uint32,
+    allocated here when not given) to 55; with ``check`` the call waits for the
+    stream and raises ``XrmmError`` ("GPU operator contract validation failed:
+    code 55") as the reference's run does.
+    """
+    _check_dev(data, indices, scales, zero_points, status)
+    if data.dtype != torch.uint8 or (zero_points is not None and zero_points.dtype != torch.uint8):
+        raise nat.XrmmInvalid("Logical dtype outside frozen contract: dataT")
+    if scales.dtype != torch.float32:
+        raise nat.XrmmInvalid("Logical dtype outside frozen contract: scalesT")
+    if indices.dtype not in _IDX:
+        raise nat.XrmmInvalid("Logical dtype outside frozen contract: indicesT")
+    if data.dim() != 2 or indices.dim() != 1:
+        raise nat.XrmmInvalid("Unsupported GatherBlockQuantized geometry")
+    rows, pcols = int(data.shape[0]), int(data.shape[1])
+    width = pcols * (8 // int(bits)) if bits in (4, 8) else 0
+    blocks = (width + block_size - 1) // block_size if block_size > 0 else 0
+    if tuple(scales.shape) != (rows, blocks):
+        raise nat.XrmmInvalid("Unsupported GatherBlockQuantized geometry")
+    if zero_points is not None and tuple(zero_points.shape) != (rows, (blocks * bits + 7) // 8):
+        raise nat.XrmmInvalid("Unsupported GatherBlockQuantized geometry")
+    data, indices, scales = data.contiguous(), indices.contiguous(), scales.contiguous()
+    out = torch.empty((int(indices.shape[0]), width), dtype=torch.float32, device=data.device)
+    if status is None:
+        status = torch.zeros(1, dtype=torch.int32, device=data.device)
+    nat.check(nat.lib().xrmm_gather_block_quantized(
+        _ptr(data), _ptr(indices), _IDX[indices.dtype], _ptr(scales), _ptr(zero_points), _ptr(out), _ptr(status),
+        rows, pcols, int(indices.shape[0]), int(bits), int(block_size), _stream(stream)))
+    if check:
+        code = int(status.item())
+        if code:
+            raise nat.XrmmError(f"GPU operator contract validation failed: code {code}")
+    return out
+
+
+def matmul_bnb4(A, B, absmax, *, K, N, block_size=32, quant_type=1, trans_b=1, out=None, stream=None):
+    """com.microsoft.MatMulBnb4: ``Y = A @ dequant(B)`` in A's dtype, ``[M, N]``.
+
+    A ``[M, K]`` float32/float16, B uint8 ``ceil(N*K/2)`` bytes (even flat index
+    in the high nibble), absmax ``ceil(N*K/block_size)`` in A's dtype.
+    """
+    _check_dev(A, B, absmax, out)
+    if A.dtype not in _T1 or absmax.dtype != A.dtype:
+        raise nat.XrmmInvalid("Logical dtype outside frozen contract: aT")
+    if B.dtype != torch.uint8:
+        raise nat.XrmmInvalid("Logical dtype outside frozen contract: bT")
+    if A.dim() != 2 or int(A.shape[1]) != K:
+        raise nat.XrmmInvalid("Invalid packed matmul geometry")
+    if B.numel() < (N * K + 1) // 2 or absmax.numel() < (N * K + block_size - 1) // max(block_size, 1):
+        raise nat.XrmmInvalid("Invalid packed matmul geometry")
+    A, B, absmax = A.contiguous(), B.contiguous(), absmax.contiguous()
+    M = int(A.shape[0])
+    Y = out if out is not None else torch.empty((M, N), dtype=A.dtype, device=A.device)
+    nat.check(nat.lib().xrmm_matmul_bnb4(_ptr(A), _ptr(B), _ptr(absmax), _ptr(Y), M, K, N, int(block_size),
+                                         int(quant_type), int(trans_b), _T1[A.dtype], _stream(stream)))
+    return Y
+
+
+def bnb4_kernel(M, K, N, block_size=32, quant_type=1, trans_b=1, dtype=torch.float16) -> str:
+    r = nat.lib().xrmm_matmul_bnb4_kernel(M, K, N, block_size, quant_type, trans_b, _T1[dtype])
+    if r is None:
+        raise nat.XrmmInvalid(nat.last_error())
+    return r.decode()
