@@ -28,7 +28,13 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
 FP16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, published
 PROFILES = os.path.join(ROOT, "profiles")
-SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048": 4, "qmoe_mixtral_t1": 6}
+SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048": 4, "qmoe_mixtral_t1": 6,
+         "bnb4_nf4_m1": 7, "gbq_embed_t2048": 8}
+# com.microsoft.MatMulBnb4 decode: the FFN up-projection shape in NF4, blocks of 64
+BNB4 = dict(M=1, K=4096, N=14336, bs=64)
+# com.microsoft.GatherBlockQuantized: a 128256 x 4096 4-bit embedding table
+# (blocks of 32, float32 scales) gathered for 2048 tokens
+GBQ = dict(rows=128256, width=4096, bs=32, n=2048)
 # com.microsoft.QMoE decode, Mixtral-8x7B expert geometry: T=1, H=4096, I=14336,
 # E=8, k=2, 4-bit codes, float32 scales per block of 64, interleaved SwiGLU
 QMOE = dict(T=1, H=4096, I=14336, E=8, k=2, bits=4, bs=64)
@@ -101,6 +107,19 @@ def make_replicas(torch, name, R, dev, seed):
                 fc2=torch.randint(0, 256, (E, H, I * bits // 8), dtype=torch.uint8, device=dev, generator=g),
                 s2=torch.rand((E, H, I // bs), device=dev, generator=g) * 0.019 + 0.001))
         return dict(A=x, routers=routers, reps=reps)
+    if name == "bnb4_nf4_m1":
+        q = BNB4
+        A = torch.randn((q["M"], q["K"]), device=dev, generator=g).half()
+        for _ in range(R):
+            reps.append(dict(B=torch.randint(0, 256, (q["N"] * q["K"] // 2,), dtype=torch.uint8, device=dev, generator=g),
+                             S=(torch.rand(q["N"] * q["K"] // q["bs"], device=dev, generator=g) + 0.05).half()))
+        return dict(A=A, reps=reps)
+    if name == "gbq_embed_t2048":
+        q = GBQ
+        data = torch.randint(0, 256, (q["rows"], q["width"] // 2), dtype=torch.uint8, device=dev, generator=g)
+        scales = torch.rand((q["rows"], q["width"] // q["bs"]), device=dev, generator=g) * 0.02
+        idx = [torch.randint(0, q["rows"], (q["n"],), dtype=torch.int32, device=dev, generator=g) for _ in range(R)]
+        return dict(A=data, scales=scales, reps=idx)
     if name == "mlp_swiglu_m16":
         K, N, bs = 4096, 14336, 32
         A = torch.randn((16, K), device=dev, generator=g).half()
@@ -149,6 +168,15 @@ def step_fn(ops, name, w):
                             activation="swiglu", swiglu_fusion=1, expert_weight_bits=q["bits"], block_size=q["bs"],
                             workspace=ws)
         return f
+    if name == "bnb4_nf4_m1":
+        q = BNB4
+        Y = torch.empty((q["M"], q["N"]), dtype=torch.float16, device=A.device)
+        return lambda i: ops.matmul_bnb4(A, reps[i % len(reps)]["B"], reps[i % len(reps)]["S"], K=q["K"], N=q["N"],
+                                         block_size=q["bs"], quant_type=1, out=Y)
+    if name == "gbq_embed_t2048":
+        status = torch.zeros(1, dtype=torch.int32, device=A.device)
+        return lambda i: ops.gather_block_quantized(A, reps[i % len(reps)], w["scales"], bits=4, block_size=GBQ["bs"],
+                                                    status=status, check=False)
     raise KeyError(name)
 
 
@@ -280,11 +308,12 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     results = {}
-    names = ["decode_up_m1", "prefill_m2048", "qkv_gqa_m4", "mlp_swiglu_m16", "qmoe_mixtral_t1"]
+    names = ["decode_up_m1", "prefill_m2048", "qkv_gqa_m4", "mlp_swiglu_m16", "qmoe_mixtral_t1", "bnb4_nf4_m1",
+             "gbq_embed_t2048"]
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
     for name in names:
-        R = {"prefill_m2048": 2, "qmoe_mixtral_t1": 2}.get(name, args.replicas)
+        R = {"prefill_m2048": 2, "qmoe_mixtral_t1": 2, "gbq_embed_t2048": 8}.get(name, args.replicas)
         w = make_replicas(torch, name, R, dev, seed=SEEDS[name])
         fn = step_fn(ops, name, w)
         steps = args.steps if name != "prefill_m2048" else max(10, args.steps // 10)
@@ -355,6 +384,22 @@ def main():
             "us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
             "bytes_per_launch": nbytes, "kernel": ops.qmoe_kernel(q["T"], q["H"], q["E"], 2 * q["I"], q["k"], q["bits"],
                                                                    q["bs"], "swiglu", 1)}
+    if "bnb4_nf4_m1" in results:
+        r, q = results["bnb4_nf4_m1"], BNB4
+        nbytes = q["N"] * q["K"] // 2 + q["N"] * q["K"] // q["bs"] * 2 + q["M"] * (q["K"] + q["N"]) * 2
+        gbs = nbytes / (r["ms"] * 1e-3) / 1e9
+        out["bnb4_nf4_m1"] = {
+            "workload": "MatMulBnb4 fp16 M=1 K=4096 N=14336 NF4 block_size=64 (codes + fp16 absmax)",
+            "us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": nbytes, "kernel": ops.bnb4_kernel(q["M"], q["K"], q["N"], q["bs"], 1, 1)}
+    if "gbq_embed_t2048" in results:
+        r, q = results["gbq_embed_t2048"], GBQ
+        nbytes = q["n"] * (q["width"] // 2 + q["width"] // q["bs"] * 4 + q["width"] * 4 + 4)
+        gbs = nbytes / (r["ms"] * 1e-3) / 1e9
+        out["gbq_embed_t2048"] = {
+            "workload": "GatherBlockQuantized 2048 rows of a 128256 x 4096 4-bit table, block_size=32, fp32 out",
+            "us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": nbytes}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

@@ -139,6 +139,10 @@ __global__ __launch_bounds__(QT) void k_bnb4_scalar(Bnb4Args a) {
   static_cast<T*>(a.Y)[i] = static_cast<T>(sum);
 }
 
+#ifndef XRMM_BNB_PIN
+#define XRMM_BNB_PIN 2  // columns whose table lookups may be in flight together
+#endif
+
 constexpr int BNB_RPW = 8;  // output columns per wave
 constexpr int BNB_CPC = 32;  // codes per 16-byte chunk
 
@@ -162,17 +166,7 @@ __global__ __launch_bounds__(QT) void k_bnb4_gemv(Bnb4Args a, int ctiles) {
   const int per_row = steps * 64 * (BNB_CPC + 4);
   float* tbl = xs + MR * per_row;
   const float* book = a.qt == 1 ? kNF4 : kFP4;
-  if (tid < 16) tbl[tid] = book[tid];
-  // A rows -> LDS (float32, zero past K and past M)
   const T* A = static_cast<const T*>(a.A);
-  for (int m = 0; m < MR; ++m) {
-    const bool live = m0 + m < a.M;
-    for (int64_t i = tid; i < static_cast<int64_t>(steps) * 64 * BNB_CPC; i += QT) {
-      const float v = live && i < K ? static_cast<float>(A[(m0 + m) * a.K + i]) : 0.f;
-      xs[m * per_row + (i / BNB_CPC) * (BNB_CPC + 4) + i % BNB_CPC] = v;
-    }
-  }
-  __syncthreads();
 
   const int n0 = (ctile * 4 + wave) * BNB_RPW;
   const uint32_t apc = static_cast<uint32_t>(K / a.bs);  // absmax blocks per column
@@ -244,12 +238,16 @@ __global__ __launch_bounds__(QT) void k_bnb4_gemv(Bnb4Args a, int ctiles) {
             part[m][r] = 0.f;
           }
         }
-        // one column's eight lookups and products at a time: the empty asm
-        // makes the partial sums live here, so the products cannot sink past
-        // later lookups and the table reads in flight (and their registers)
-        // stay bounded
+        // XRMM_BNB_PIN columns' lookups and products at a time: the empty asm
+        // makes their partial sums live here, so the products cannot sink
+        // past later lookups and the table reads in flight (and their
+        // registers) stay bounded
+        if ((r + 1) % XRMM_BNB_PIN == 0) {
 #pragma unroll
-        for (int m = 0; m < MR; ++m) asm volatile("" : "+v"(part[m][r]));
+          for (int rr = r + 1 - XRMM_BNB_PIN; rr <= r; ++rr)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) asm volatile("" : "+v"(part[m][rr]));
+        }
       }
     }
 #pragma unroll
@@ -259,7 +257,53 @@ __global__ __launch_bounds__(QT) void k_bnb4_gemv(Bnb4Args a, int ctiles) {
   };
 
   Buf buf[2];
-  issue(buf[0], 0);
+  issue(buf[0], 0);  // the first codes are in flight while A is staged
+
+  // table and A rows -> LDS (float32, zero past K and past M): loads of four
+  // 8-element pieces per thread in flight before their stores
+  if (tid < 16) tbl[tid] = book[tid];
+  {
+    const int per_piece = 8, pieces = steps * 64 * BNB_CPC / per_piece;
+    for (int m = 0; m < MR; ++m) {
+      const bool live = m0 + m < a.M;
+      const T* src = A + (m0 + m) * a.K;
+      for (int p0 = 0; p0 < pieces; p0 += 4 * QT) {
+        float v[4][per_piece];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int piece = p0 + j * QT + tid;
+          const int k0 = piece * per_piece;
+          if (live && k0 < K) {  // K is a multiple of 32: whole pieces
+            if constexpr (sizeof(T) == 4) {
+              const float4 u = *reinterpret_cast<const float4*>(src + k0);
+              const float4 w = *reinterpret_cast<const float4*>(src + k0 + 4);
+              v[j][0] = u.x; v[j][1] = u.y; v[j][2] = u.z; v[j][3] = u.w;
+              v[j][4] = w.x; v[j][5] = w.y; v[j][6] = w.z; v[j][7] = w.w;
+            } else {
+              const f16x8 h = *reinterpret_cast<const f16x8*>(src + k0);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) v[j][e] = static_cast<float>(h[e]);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[j][e] = 0.f;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int piece = p0 + j * QT + tid;
+          if (piece < pieces) {
+            const int k0 = piece * per_piece;  // 8 floats inside one 32-code chunk
+            float* dst = xs + m * per_row + (k0 / BNB_CPC) * (BNB_CPC + 4) + k0 % BNB_CPC;
+            *reinterpret_cast<float4*>(dst) = float4{v[j][0], v[j][1], v[j][2], v[j][3]};
+            *reinterpret_cast<float4*>(dst + 4) = float4{v[j][4], v[j][5], v[j][6], v[j][7]};
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+
   for (int s = 0; s < steps; s += 2) {
     issue(buf[1], s + 1);
     __builtin_amdgcn_sched_barrier(0);
