@@ -146,3 +146,70 @@ def test_host_forced_timeout_poisons_until_close(gpu):
         o.run()
     o.close()
     assert o.info()["closed"] is True
+
+
+BNB, QMOE, GBQ = "com.microsoft.MatMulBnb4", "com.microsoft.QMoE", "com.microsoft.GatherBlockQuantized"
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_bnb4_lifecycle(gpu, dtype):
+    from oracle import quant as Q
+    rng = np.random.default_rng(5)
+    M, K, N, bs = 2, 512, 96, 64
+    ins = dict(aT=rng.standard_normal((M, K)).astype(dtype), bT=rng.integers(0, 256, N * K // 2, dtype=np.uint8),
+               absmaxT=rng.uniform(0.1, 1.0, N * K // bs).astype(dtype))
+    with op.Operator.prepare("", request(BNB, ins, {"K": K, "N": N, "block_size": bs, "quant_type": 0})) as o:
+        o.run()
+        (y,) = o.read_outputs()
+        assert o.info()["kernel"] == "bnb4_gemv"
+    ref = Q.matmul_bnb4(ins["aT"], ins["bT"], ins["absmaxT"], K=K, N=N, block_size=bs, quant_type=0)
+    ok, err, lim = O.tolerance_ok(y.data, ref, dtype)
+    assert ok, (err, lim)
+
+
+def test_qmoe_lifecycle(gpu):
+    from oracle import moe as QM
+    rng = np.random.default_rng(6)
+    T_, H, I, E = 3, 256, 128, 4
+    ins = dict(inputT=rng.standard_normal((1, T_, H)).astype(np.float32),
+               routerT=rng.standard_normal((T_, E)).astype(np.float32),
+               fc1T=rng.integers(0, 256, (E, 2 * I, H // 2), dtype=np.uint8),
+               fc1ScalesT=rng.uniform(0.01, 0.05, (E, 2 * I, H // 32)).astype(np.float32),
+               fc2T=rng.integers(0, 256, (E, H, I // 2), dtype=np.uint8),
+               fc2ScalesT=rng.uniform(0.01, 0.05, (E, H, I // 32)).astype(np.float32))
+    attrs = {"k": 2, "activation_type": "swiglu", "swiglu_fusion": 1, "block_size": 32, "activation_alpha": 1.702,
+             "activation_beta": 1.0, "swiglu_limit": 7.0}
+    with op.Operator.prepare("", request(QMOE, ins, attrs)) as o:
+        o.run()
+        o.run()
+        (y,) = o.read_outputs()
+        info = o.info()
+    assert info["kernel"] == "qmoe_rows" and info["dispatch_count"] == 1
+    ref = QM.qmoe(ins["inputT"], ins["routerT"], ins["fc1T"], ins["fc1ScalesT"], ins["fc2T"], ins["fc2ScalesT"], k=2,
+                  activation="swiglu", swiglu_fusion=1, bits=4, block_size=32, alpha=1.702, beta=1.0, swiglu_limit=7.0)
+    assert y.data.shape == (1, T_, H)
+    ok, err, lim = O.tolerance_ok(y.data, ref, np.float32)
+    assert ok, (err, lim)
+
+
+def test_gbq_lifecycle_and_index_failure(gpu):
+    from oracle import quant as Q
+    rng = np.random.default_rng(8)
+    rows, pcols, bs = 40, 64, 32
+    data = rng.integers(0, 256, (rows, pcols), dtype=np.uint8)
+    scales = rng.uniform(-1, 1, (rows, pcols * 2 // bs)).astype(np.float32)
+    zps = rng.integers(0, 256, (rows, pcols * 2 // bs // 2), dtype=np.uint8)
+    idx = np.array([3, 39, 0, 3], np.int64)
+    ins = dict(dataT=data, indicesT=idx, scalesT=scales, zeroPointsT=zps)
+    with op.Operator.prepare("", request(GBQ, ins, {"bits": 4, "block_size": bs})) as o:
+        o.run()
+        (y,) = o.read_outputs()
+        assert o.info()["kernel"] == "gbq_words"
+    assert np.array_equal(y.data, Q.gather_block_quantized(data, idx, scales, zps, bits=4, block_size=bs))
+    bad = dict(ins, indicesT=np.array([1, rows], np.int64))
+    o = op.Operator.prepare("", request(GBQ, bad, {"bits": 4, "block_size": bs}))
+    with pytest.raises(op.XrmmError, match="GPU operator contract validation failed: code 55"):
+        o.run()
+    with pytest.raises(op.XrmmError, match="failed and must be closed"):
+        o.run()
+    o.close()

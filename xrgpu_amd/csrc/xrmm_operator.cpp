@@ -1,12 +1,13 @@
 // Request-level lifecycle of libxrmm: plan / prepare / run / read_outputs /
-// info / close for the three MatMulNBits-family operators.
+// info / close for the three MatMulNBits-family operators and for
+// com.microsoft.QMoE (1030), GatherBlockQuantized (1031) and MatMulBnb4 (1026).
 //
 // Behaviour follows xrgpu::operators::extended:
 //  * plan():   contract validation (kernels/_shared/extended/contracts.cpp:14,
-//              rows contract_data.h:722-751), args-over-attrs merging
-//              (planner.cpp:67-85), attribute defaults and output shapes of the
-//              complex planner (complex_plan.cpp:117-120), requested-output
-//              checks (planner.cpp:86-93);
+//              rows contract_data.h:659-663,718-751,821-827), args-over-attrs
+//              merging (planner.cpp:67-85), attribute defaults, checks and
+//              output shapes of the complex planner (complex_plan.cpp:117-129),
+//              requested-output checks (planner.cpp:86-93);
 //  * prepare(): input byte-count and memory-limit checks (planner.cpp:32-49),
 //              then one device arena holding every input and output;
 //  * run():    launch on the operator's own stream and wait with a time-out;
@@ -38,6 +39,8 @@
 
 #include "../../include/xrmm.h"
 #include "xrmm_internal.h"
+#include "xrmm_moe.h"
+#include "xrmm_quant.h"
 
 namespace {
 
@@ -98,6 +101,11 @@ struct Port {
 constexpr uint32_t kT1 = (1u << XRMM_F32) | (1u << XRMM_F16);
 constexpr uint32_t kU8 = 1u << XRMM_U8;
 constexpr uint32_t kT3 = kT1 | kU8;  // float zero points (reference) or packed uint8 (extension)
+constexpr uint32_t kF32 = 1u << XRMM_F32;
+// int64 indices (the reference contract) and int32 / uint32 (read as int32 by controlIndex)
+constexpr uint32_t kIdx = (1u << XRMM_I64) | (1u << XRMM_I32) | (1u << XRMM_U32);
+// operators outside the MatMulNBits family (xrmm::Op covers that family)
+constexpr int OP_BNB4 = 10, OP_QMOE = 11, OP_GBQ = 12;
 
 struct OpContract {
   const char* operation;
@@ -125,6 +133,17 @@ const std::vector<OpContract>& contracts() {
         {"qZeroPointsT", "T3", kT3, 2, true}, {"kZeroPointsT", "T3", kT3, 2, true}, {"vZeroPointsT", "T3", kT3, 2, true}},
        {{"qT", "T1", kT1, -1, false}, {"kT", "T1", kT1, -1, false}, {"vT", "T1", kT1, -1, false},
         {"residualT", "T1", kT1, -1, true}}},
+      {"com.microsoft.MatMulBnb4", OP_BNB4,
+       {{"aT", "T1", kT1, 2, false}, {"bT", "T2", kU8, 1, false}, {"absmaxT", "T1", kT1, 1, false}},
+       {{"yT", "T1", kT1, 2, false}}},
+      {"com.microsoft.QMoE", OP_QMOE,
+       {{"inputT", "T", kF32, -1, false}, {"routerT", "T", kF32, 2, false}, {"fc1T", "T1", kU8, 3, false},
+        {"fc1ScalesT", "T2", kF32, -1, false}, {"fc2T", "T1", kU8, 3, false}, {"fc2ScalesT", "T2", kF32, -1, false}},
+       {{"outputT", "T", kF32, -1, false}}},
+      {"com.microsoft.GatherBlockQuantized", OP_GBQ,
+       {{"dataT", "T1", kU8, 2, false}, {"indicesT", "Tind", kIdx, 1, false}, {"scalesT", "T2", kF32, 2, false},
+        {"zeroPointsT", "T1", kU8, 2, true}},
+       {{"outputT", "T2", kF32, 2, false}}},
   };
   return c;
 }
@@ -224,6 +243,16 @@ struct Plan {
   int64_t K = 0, N = 0, Nq = 0, Nkv = 0, M = 0;
   int32_t bits = 4, block_size = 32, act = 2, dtype = XRMM_F32, zp_dtype = XRMM_UNSPECIFIED;
   float eps = 1e-5f;
+  // MatMulBnb4
+  int32_t quant_type = 1, trans_b = 1;
+  // QMoE
+  int64_t T = 0, H = 0, E = 0, F1 = 0, I = 0;
+  int32_t k = 1, fusion = 0, has_limit = 0;
+  float alpha = 1.f, beta = 0.f, limit = 0.f;
+  // GatherBlockQuantized
+  int64_t rows = 0, pcols = 0, n_idx = 0;
+  int32_t idx_dtype = XRMM_I64;
+  std::map<std::string, std::vector<int64_t>> out_shape;  // planned output shapes by port
 
   const Tensor* get(const char* n) const {
     auto it = in.find(n);
@@ -244,6 +273,133 @@ void expect_shape(const Tensor* t, const std::vector<int64_t>& want) {
     o << "]";
     throw Invalid(o.str());
   }
+}
+
+// Planned outputs in contract order from p.out_shape (optional ones only when
+// requested), then the requested-output checks that select storage dtypes
+// (planner.cpp:86-93). Output dtypes follow their type variable.
+void finish_outputs(Plan& p, const xrmm_request* q) {
+  const OpContract& c = *p.contract;
+  if (q->n_requested_outputs < 0 || (q->n_requested_outputs > 0 && !q->requested_outputs)) throw Invalid("Invalid requested-output list");
+  std::vector<Tensor> requested;
+  for (int32_t i = 0; i < q->n_requested_outputs; ++i) requested.push_back(from_c(q->requested_outputs[i], false));
+  for (const auto& pt : c.outputs) {
+    const bool asked = std::any_of(requested.begin(), requested.end(), [&](const Tensor& t) { return t.name == pt.name; });
+    if ((pt.optional && !asked) || (!requested.empty() && !asked)) continue;
+    Tensor t;
+    t.name = pt.name;
+    t.dtype = t.storage = p.dtype;
+    t.shape = p.out_shape.at(pt.name);
+    p.outputs.push_back(t);
+  }
+  for (const auto& pt : c.outputs)
+    if (!pt.optional && std::none_of(p.outputs.begin(), p.outputs.end(), [&](const Tensor& t) { return t.name == pt.name; }))
+      throw Invalid(std::string("Missing required frozen-contract output: ") + pt.name);
+  if (!requested.empty()) {
+    check(requested.size() == p.outputs.size(), "Requested output count differs from plan");
+    for (size_t i = 0; i < p.outputs.size(); ++i) {
+      const Tensor& w = requested[i];
+      Tensor& t = p.outputs[i];
+      check(w.name == t.name && w.dtype == t.dtype, "Requested output name/type differs from plan");
+      check(w.shape.size() == t.shape.size(), "Requested output rank differs from plan");
+      check(w.shape == t.shape, "Requested output shape differs from plan");
+      t.storage = w.storage;
+    }
+  }
+}
+
+// MatMulBnb4 (complex_plan.cpp:117-120): K defaults to A's last dimension,
+// N required, block_size 32, quant_type 1 (NF4), transB 1.
+void plan_bnb4(Plan& p, const Attrs& a) {
+  const Tensor& A = p.in.at("aT");
+  p.dtype = A.dtype;
+  p.K = attr_int(a, "K", A.shape.back());
+  p.N = attr_int(a, "N", 0);
+  p.block_size = int32_t(attr_int(a, "block_size", 32));
+  p.quant_type = int32_t(attr_int(a, "quant_type", 1));
+  p.trans_b = int32_t(attr_int(a, "transB", 1));
+  check(p.K > 0 && p.block_size > 0, "Invalid packed matmul geometry");
+  check(p.N > 0, "Packed matmul N required");
+  check(p.quant_type == 0 || p.quant_type == 1, "MatMulBnb4 quant_type must be 0 (FP4) or 1 (NF4)");
+  check(A.shape.back() == p.K, "aT's last dimension must equal K");
+  p.M = A.shape[0];
+  check(int64_t(numel(p.in.at("bT").shape)) >= (p.N * p.K + 1) / 2, "bT holds fewer than N*K codes");
+  check(int64_t(numel(p.in.at("absmaxT").shape)) >= (p.N * p.K + p.block_size - 1) / p.block_size,
+        "absmaxT holds fewer than ceil(N*K/block_size) scales");
+  p.out_shape["yT"] = {p.M, p.N};
+}
+
+// QMoE (complex_plan.cpp:121-128), with the reference's messages.
+void plan_qmoe(Plan& p, const Attrs& a) {
+  const Tensor& x = p.in.at("inputT");
+  const Tensor& router = p.in.at("routerT");
+  const Tensor& fc1 = p.in.at("fc1T");
+  const Tensor& fc2 = p.in.at("fc2T");
+  const Tensor& s1 = p.in.at("fc1ScalesT");
+  const Tensor& s2 = p.in.at("fc2ScalesT");
+  p.dtype = x.dtype;
+  p.k = int32_t(attr_int(a, "k", 1));
+  const int64_t sparse = attr_int(a, "use_sparse_mixer", 0);
+  p.fusion = int32_t(attr_int(a, "swiglu_fusion", 0));
+  p.bits = int32_t(attr_int(a, "expert_weight_bits", 4));
+  p.block_size = int32_t(attr_int(a, "block_size", 0));
+  const int64_t prepacked = attr_int(a, "weights_prepacked", -1);
+  p.act = activation_code(attr_str(a, "activation_type", "relu"));
+  p.alpha = float(attr_num(a, "activation_alpha", 1));
+  p.beta = float(attr_num(a, "activation_beta", 0));
+  p.limit = float(attr_num(a, "swiglu_limit", 0));
+  p.has_limit = a.count("swiglu_limit") ? 1 : 0;
+  p.H = x.shape.empty() ? 0 : x.shape.back();
+  p.E = router.shape[1];
+  p.F1 = fc1.shape[1];
+  const int64_t fusion = p.act == 6 && p.fusion ? 2 : 1;
+  p.I = p.F1 / fusion;
+  check((x.shape.size() == 2 || x.shape.size() == 3) && p.H > 0 && p.k >= 1 && p.k <= p.E && sparse == 0,
+        "Invalid MoE input or routing geometry");
+  p.T = int64_t(numel(x.shape) / uint64_t(p.H));
+  check(router.shape[0] == p.T && fc1.shape[0] == p.E && fc2.shape[0] == p.E && fc2.shape[1] == p.H &&
+            p.F1 % fusion == 0,
+        "Invalid MoE weight geometry");
+  check((p.bits == 4 || p.bits == 8) && (prepacked == -1 || prepacked == 0) && attr_str(a, "quant_type", "int") == "int",
+        "Unsupported QMoE integer layout");
+  check((p.act == 1 && p.fusion == 0) || (p.act == 6 && p.fusion == 1), "Invalid quantized SwiGLU fusion");
+  check(fc1.shape[2] * (8 / p.bits) == p.H && fc2.shape[2] * (8 / p.bits) == p.I, "Invalid packed expert projection");
+  const int32_t bs = p.block_size;
+  check(bs == 0 || (bs >= 16 && (bs & (bs - 1)) == 0 && p.H % bs == 0 && p.I % bs == 0),
+        "Invalid quantized expert block size");
+  for (const Tensor* sc : {&s1, &s2}) {
+    const Tensor& w = sc == &s1 ? fc1 : fc2;
+    const int64_t cols = sc == &s1 ? p.H : p.I;
+    check(int(sc->shape.size()) == (bs ? 3 : 2) && sc->shape[0] == p.E && sc->shape[1] == w.shape[1] &&
+              (!bs || sc->shape[2] == cols / bs),
+          "Invalid quantized expert scales");
+  }
+  p.out_shape["outputT"] = x.shape;
+}
+
+// GatherBlockQuantized (complex_plan.cpp:129): bits 4 / 8, block_size a power
+// of two >= 16, gather_axis 0, quantize_axis 1; output [indices, width] in the
+// scales' dtype.
+void plan_gbq(Plan& p, const Attrs& a, const std::map<std::string, int32_t>& vars) {
+  const Tensor& data = p.in.at("dataT");
+  const Tensor& idx = p.in.at("indicesT");
+  const Tensor& sc = p.in.at("scalesT");
+  p.bits = int32_t(attr_int(a, "bits", 4));
+  p.block_size = int32_t(attr_int(a, "block_size", 128));
+  const int64_t gather_axis = attr_int(a, "gather_axis", 0), quantize_axis = attr_int(a, "quantize_axis", 1);
+  const int32_t bs = p.block_size;
+  check((p.bits == 4 || p.bits == 8) && bs >= 16 && (bs & (bs - 1)) == 0 && gather_axis == 0 && quantize_axis == 1,
+        "Unsupported GatherBlockQuantized geometry");
+  p.dtype = sc.dtype;
+  p.idx_dtype = idx.dtype;
+  p.rows = data.shape[0];
+  p.pcols = data.shape[1];
+  p.n_idx = idx.shape[0];
+  const int64_t width = p.pcols * (8 / p.bits), blocks = (width + bs - 1) / bs;
+  expect_shape(&sc, {p.rows, blocks});
+  expect_shape(p.get("zeroPointsT"), {p.rows, (blocks * p.bits + 7) / 8});
+  (void)vars;
+  p.out_shape["outputT"] = {p.n_idx, width};
 }
 
 Plan make_plan(const xrmm_request* q) {
@@ -280,8 +436,16 @@ Plan make_plan(const xrmm_request* q) {
   for (const auto& pt : c.inputs)
     if (!pt.optional && !p.in.count(pt.name)) throw Invalid(std::string("Missing required frozen-contract input: ") + pt.name);
 
-  // ---- attributes (complex_plan.cpp:118)
   const Attrs a = merged_attrs(*q);
+  if (c.op == OP_BNB4 || c.op == OP_QMOE || c.op == OP_GBQ) {
+    if (c.op == OP_BNB4) plan_bnb4(p, a);
+    if (c.op == OP_QMOE) plan_qmoe(p, a);
+    if (c.op == OP_GBQ) plan_gbq(p, a, vars);
+    finish_outputs(p, q);
+    return p;
+  }
+
+  // ---- attributes (complex_plan.cpp:118)
   const Tensor& A = p.in.at("aT");
   check(!A.shape.empty(), "Rank-one or greater tensor required");
   p.dtype = A.dtype;
@@ -331,40 +495,16 @@ Plan make_plan(const xrmm_request* q) {
   p.zp_dtype = zp == vars.end() ? XRMM_UNSPECIFIED : zp->second;
 
   // ---- outputs (complex_plan.cpp:66-72,119)
-  if (q->n_requested_outputs < 0 || (q->n_requested_outputs > 0 && !q->requested_outputs)) throw Invalid("Invalid requested-output list");
-  std::vector<Tensor> requested;
-  for (int32_t i = 0; i < q->n_requested_outputs; ++i) requested.push_back(from_c(q->requested_outputs[i], false));
   auto last = [&](int64_t n) {
-    auto s = A.shape;
-    s.back() = n;
-    return s;
+    auto sh = A.shape;
+    sh.back() = n;
+    return sh;
   };
   for (const auto& pt : c.outputs) {
-    const bool asked = std::any_of(requested.begin(), requested.end(), [&](const Tensor& t) { return t.name == pt.name; });
-    if ((pt.optional && !asked) || (!requested.empty() && !asked)) continue;
-    Tensor t;
-    t.name = pt.name;
-    t.dtype = t.storage = p.dtype;
     const std::string nm = pt.name;
-    t.shape = nm == "residualT" ? A.shape : nm == "qT" ? last(p.Nq) : (nm == "kT" || nm == "vT") ? last(p.Nkv) : last(p.N);
-    p.outputs.push_back(t);
+    p.out_shape[nm] = nm == "residualT" ? A.shape : nm == "qT" ? last(p.Nq) : (nm == "kT" || nm == "vT") ? last(p.Nkv) : last(p.N);
   }
-  for (const auto& pt : c.outputs)
-    if (!pt.optional && std::none_of(p.outputs.begin(), p.outputs.end(), [&](const Tensor& t) { return t.name == pt.name; }))
-      throw Invalid(std::string("Missing required frozen-contract output: ") + pt.name);
-
-  // ---- requested outputs select storage (planner.cpp:86-93)
-  if (!requested.empty()) {
-    check(requested.size() == p.outputs.size(), "Requested output count differs from plan");
-    for (size_t i = 0; i < p.outputs.size(); ++i) {
-      const Tensor& w = requested[i];
-      Tensor& t = p.outputs[i];
-      check(w.name == t.name && w.dtype == t.dtype, "Requested output name/type differs from plan");
-      check(w.shape.size() == t.shape.size(), "Requested output rank differs from plan");
-      check(w.shape == t.shape, "Requested output shape differs from plan");
-      t.storage = w.storage;
-    }
-  }
+  finish_outputs(p, q);
   return p;
 }
 
@@ -437,6 +577,8 @@ struct xrmm_op {
   uint64_t arena_bytes = 0;
   std::map<std::string, void*> in_dev;  // device copies of present inputs
   std::vector<void*> out_dev;           // device outputs in plan order
+  void* workspace = nullptr;            // QMoE workspace / GatherBlockQuantized status word
+  uint64_t workspace_bytes = 0;
   bool closed = false, executed = false, poisoned = false, has_gpu = false;
   double execution_ms = 0, gpu_ms = 0;
   std::string kernel, device_name, info_json;
@@ -476,6 +618,21 @@ struct xrmm_op {
     void* s = stream;
     const int32_t zd = p.zp_dtype;
     switch (p.contract->op) {
+      case OP_BNB4:
+        return xrmm_matmul_bnb4(dptr("aT"), dptr("bT"), dptr("absmaxT"), optr("yT"), p.M, p.K, p.N, p.block_size,
+                                p.quant_type, p.trans_b, p.dtype, s);
+      case OP_QMOE:
+        return xrmm_qmoe(dptr("inputT"), dptr("routerT"), dptr("fc1T"), dptr("fc1ScalesT"), dptr("fc2T"),
+                         dptr("fc2ScalesT"), optr("outputT"), workspace, int64_t(workspace_bytes), p.T, p.H, p.E, p.F1,
+                         p.k, p.bits, p.block_size, p.act, p.fusion, p.alpha, p.beta, p.limit, p.has_limit, s);
+      case OP_GBQ: {
+        // the status word starts at zero for every run (the kernels only raise it)
+        const hipError_t e = hipMemsetAsync(workspace, 0, 4, stream);
+        if (e != hipSuccess) return xrmm::set_status(XRMM_EDEVICE, std::string("hipMemsetAsync: ") + hipGetErrorString(e));
+        return xrmm_gather_block_quantized(dptr("dataT"), dptr("indicesT"), p.idx_dtype, dptr("scalesT"),
+                                           dptr("zeroPointsT"), optr("outputT"), workspace, p.rows, p.pcols, p.n_idx,
+                                           p.bits, p.block_size, s);
+      }
       case xrmm::OP_MATMUL:
         return xrmm_matmul_nbits(dptr("aT"), dptr("bT"), dptr("scalesT"), dptr("zeroPointsT"), dptr("zeroPointsT") ? zd : XRMM_UNSPECIFIED,
                                  dptr("biasT"), optr("yT"), p.M, p.K, p.N, p.bits, p.block_size, p.dtype, s);
@@ -565,6 +722,10 @@ int xrmm_prepare(const xrmm_request* request, const xrmm_options* options, xrmm_
       total += align256(n * dtype_bytes(t.dtype));
     }
     for (const Tensor& t : p.outputs) total += align256(numel(t.shape) * dtype_bytes(t.dtype));
+    uint64_t ws = 0;
+    if (p.contract->op == OP_QMOE) ws = uint64_t(xrmm_qmoe_workspace_bytes(p.T, p.k, p.H, p.I));
+    if (p.contract->op == OP_GBQ) ws = 4;
+    total += align256(ws);
     if (total > o.memory_limit_bytes) throw Invalid("Extended heap memory limit exceeded");
 
     hip_check(hipGetDevice(&op->device), "hipGetDevice");
@@ -600,10 +761,26 @@ int xrmm_prepare(const xrmm_request* request, const xrmm_options* options, xrmm_
       op->out_dev.push_back(op->arena + off);
       off += align256(numel(t.shape) * dtype_bytes(t.dtype));
     }
+    op->workspace = ws ? op->arena + off : nullptr;
+    op->workspace_bytes = ws;
     const int32_t zk = p.zp_dtype;
     const int code = p.contract->op;
-    const int64_t n0 = code == xrmm::OP_QKV ? p.Nq : p.N;
-    const char* k = xrmm_select_kernel(code, p.M, p.K, n0, p.bits, p.block_size, p.dtype, zk);
+    const char* k = nullptr;
+    if (code == OP_BNB4) {
+      k = xrmm_matmul_bnb4_kernel(p.M, p.K, p.N, p.block_size, p.quant_type, p.trans_b, p.dtype);
+    } else if (code == OP_QMOE) {
+      k = xrmm_qmoe_kernel(p.T, p.H, p.E, p.F1, p.k, p.bits, p.block_size, p.act, p.fusion);
+    } else if (code == OP_GBQ) {
+      xrmm::GbqArgs g{};
+      g.data = static_cast<const uint8_t*>(op->dptr("dataT"));
+      g.out = static_cast<float*>(op->out_dev.empty() ? nullptr : op->out_dev[0]);
+      g.pcols = p.pcols;
+      g.bs = p.block_size;
+      k = xrmm::gbq_fast_ok(g) ? "gbq_words" : "gbq_scalar";
+    } else {
+      const int64_t n0 = code == xrmm::OP_QKV ? p.Nq : p.N;
+      k = xrmm_select_kernel(code, p.M, p.K, n0, p.bits, p.block_size, p.dtype, zk);
+    }
     op->kernel = k ? k : "generic";
     *out = op.release();
   }));
@@ -634,6 +811,11 @@ int xrmm_run(xrmm_op* op) {
         if (e != hipErrorNotReady) hip_check(e, "operator execution");
         if (std::chrono::steady_clock::now() > deadline) throw Device("Extended native operator timed out");
         std::this_thread::sleep_for(std::chrono::microseconds(20));
+      }
+      if (op->plan.contract->op == OP_GBQ) {  // failure code of the shader (vulkan.cpp:115)
+        uint32_t code = 0;
+        hip_check(hipMemcpy(&code, op->workspace, 4, hipMemcpyDeviceToHost), "hipMemcpy (status)");
+        if (code) throw Device("GPU operator contract validation failed: code " + std::to_string(code));
       }
     } catch (...) {
       op->poisoned = true;
@@ -698,7 +880,10 @@ const char* xrmm_info(xrmm_op* op) {
   if (op->executed) o << op->execution_ms; else o << "null";
   o << ",\"gpu_ms\":";
   if (op->has_gpu) o << op->gpu_ms; else o << "null";
-  o << ",\"dispatch_count\":" << (op->executed && op->plan.M > 0 ? 1 : 0) << ",\"persistent_bytes\":" << (op->closed ? 0 : op->arena_bytes)
+  const Plan& pl = op->plan;
+  const int pc = pl.contract->op;
+  const bool work = pc == OP_QMOE ? pl.T > 0 : pc == OP_GBQ ? pl.n_idx > 0 : pl.M > 0;
+  o << ",\"dispatch_count\":" << (op->executed && work ? 1 : 0) << ",\"persistent_bytes\":" << (op->closed ? 0 : op->arena_bytes)
     << ",\"device\":\"" << op->device_name << "\",\"kernel\":\"" << op->kernel << "\",\"outputs\":[";
   for (size_t i = 0; i < op->plan.outputs.size(); ++i) {
     const Tensor& t = op->plan.outputs[i];
