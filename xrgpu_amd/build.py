@@ -19,6 +19,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ_DIR = os.path.join(HERE, "_build")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libxrmm.so")
+RUNNER = os.path.join(LIB_DIR, "xrmm_execute")  # job-JSON runner over the C ABI
 ARCH = os.environ.get("XRMM_OFFLOAD_ARCH", "gfx950")
 
 # (source, extra defines, object name)
@@ -83,6 +84,12 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     tmp = LIB + ".tmp"
     _run([cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *[obj for _, _, obj in units], "-o", tmp], verbose)
     os.replace(tmp, LIB)
+    # the runner is host code only: the system C++ compiler, linked to the
+    # library beside it
+    cxx = shutil.which("g++") or shutil.which("c++") or cc
+    _run([cxx, "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"), os.path.join(CSRC, "xrmm_execute.cpp"),
+          "-L", LIB_DIR, "-lxrmm", "-Wl,-rpath,$ORIGIN", "-o", RUNNER + ".tmp"], verbose)
+    os.replace(RUNNER + ".tmp", RUNNER)
     return LIB
 
 
