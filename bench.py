@@ -29,7 +29,7 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
 FP16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, published
 PROFILES = os.path.join(ROOT, "profiles")
 SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048": 4, "qmoe_mixtral_t1": 6,
-         "bnb4_nf4_m1": 7, "gbq_embed_t2048": 8}
+         "bnb4_nf4_m1": 7, "gbq_embed_t2048": 8, "int8a_decode_m1": 1}
 # com.microsoft.MatMulBnb4 decode: the FFN up-projection shape in NF4, blocks of 64
 BNB4 = dict(M=1, K=4096, N=14336, bs=64)
 # com.microsoft.GatherBlockQuantized: a 128256 x 4096 4-bit embedding table
@@ -62,7 +62,7 @@ def make_replicas(torch, name, R, dev, seed):
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     reps = []
-    if name == "decode_up_m1":
+    if name in ("decode_up_m1", "int8a_decode_m1"):
         K, N, bs = 4096, 14336, 32
         A = torch.randn((1, K), device=dev, generator=g).half()
         for _ in range(R):
@@ -168,6 +168,11 @@ def step_fn(ops, name, w):
                             activation="swiglu", swiglu_fusion=1, expert_weight_bits=q["bits"], block_size=q["bs"],
                             workspace=ws)
         return f
+    if name == "int8a_decode_m1":
+        Y = torch.empty((1, w["N"]), dtype=torch.float16, device=A.device)
+        ws = torch.empty(ops.int8a_workspace_bytes(1, w["K"]), dtype=torch.uint8, device=A.device)
+        return lambda i: ops.matmul_nbits_int8a(A, reps[i % len(reps)]["B"], reps[i % len(reps)]["S"], K=w["K"],
+                                                N=w["N"], block_size=w["bs"], out=Y, workspace=ws)
     if name == "bnb4_nf4_m1":
         q = BNB4
         Y = torch.empty((q["M"], q["N"]), dtype=torch.float16, device=A.device)
@@ -309,7 +314,7 @@ def main():
     torch.cuda.set_device(dev)
     results = {}
     names = ["decode_up_m1", "prefill_m2048", "qkv_gqa_m4", "mlp_swiglu_m16", "qmoe_mixtral_t1", "bnb4_nf4_m1",
-             "gbq_embed_t2048"]
+             "gbq_embed_t2048", "int8a_decode_m1"]
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
     for name in names:
@@ -392,6 +397,14 @@ def main():
             "workload": "MatMulBnb4 fp16 M=1 K=4096 N=14336 NF4 block_size=64 (codes + fp16 absmax)",
             "us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
             "bytes_per_launch": nbytes, "kernel": ops.bnb4_kernel(q["M"], q["K"], q["N"], q["bs"], 1, 1)}
+    if "int8a_decode_m1" in results:
+        r = results["int8a_decode_m1"]
+        nbytes = 33_067_008
+        gbs = nbytes / (r["ms"] * 1e-3) / 1e9
+        out["int8a_decode_m1"] = {
+            "workload": "opt-in int8 activations (accuracy_level 4), MatMulNBits fp16 M=1 K=4096 N=14336 bs=32",
+            "us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": nbytes, "numerics": "not the reference's float32 arithmetic (opt-in)"}
     if "gbq_embed_t2048" in results:
         r, q = results["gbq_embed_t2048"], GBQ
         nbytes = q["n"] * (q["width"] // 2 + q["width"] // q["bs"] * 4 + q["width"] * 4 + 4)

@@ -294,6 +294,21 @@ int xrmm_matmul_bnb4(const void* A, const void* B, const void* absmax, void* Y, 
 const char* xrmm_matmul_bnb4_kernel(int64_t M, int64_t K, int64_t N, int32_t block_size, int32_t quant_type,
                                     int32_t trans_b, int32_t dtype);
 
+/* Opt-in int8 activations for MatMulNBits: the upstream operator's
+ * accuracy_level 4, NOT the reference's float32 arithmetic (xrGPU computes in
+ * float32 at every level, complex_kernel.glsl:83). Rows of A are quantized per
+ * block of 128 (scale = max|a| / 127, codes rint(a / scale)), the 4-bit
+ * weights enter as signed bytes (code - zero point) and chunk sums are exact
+ * int32 dot products scaled in float32. bits 4, power-of-two block_size >= 32
+ * dividing K, K a multiple of 128, zero points absent or packed uint8,
+ * 16-byte aligned A, B and workspace (>= xrmm_matmul_nbits_int8a_workspace_bytes
+ * bytes). Same argument meaning as xrmm_matmul_nbits otherwise. */
+int64_t xrmm_matmul_nbits_int8a_workspace_bytes(int64_t M, int64_t K);
+int xrmm_matmul_nbits_int8a(const void* A, const void* B, const void* scales, const void* zero_points,
+                            int32_t zp_dtype, const void* bias, void* Y, void* workspace, int64_t workspace_bytes,
+                            int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size, int32_t dtype,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -64,6 +64,9 @@ def _sig(lib):
       _vp)
     s("xrmm_matmul_bnb4", ctypes.c_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _vp)
     s("xrmm_matmul_bnb4_kernel", ctypes.c_char_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32)
+    s("xrmm_matmul_nbits_int8a_workspace_bytes", _i64, _i64, _i64)
+    s("xrmm_matmul_nbits_int8a", ctypes.c_int, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32,
+      _i32, _i32, _vp)
 
 
 def lib():

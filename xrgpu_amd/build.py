@@ -39,6 +39,7 @@ UNITS = [
     ("xrmm_gemm_zp.hip", ["-DXRMM_ZPK=2"], "gemm_zp2.o"),
     ("xrmm_moe.hip", [], "moe.o"),
     ("xrmm_quant.hip", [], "quant.o"),
+    ("xrmm_int8a.hip", [], "int8a.o"),
     ("xrmm_api.cpp", [], "api.o"),
     ("xrmm_operator.cpp", [], "operator.o"),
 ]

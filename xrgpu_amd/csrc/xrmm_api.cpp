@@ -374,3 +374,50 @@ const char* xrmm_matmul_bnb4_kernel(int64_t M, int64_t K, int64_t N, int32_t blo
   ok();
   return xrmm::bnb4_fast_ok(a) ? "bnb4_gemv" : "bnb4_scalar";
 }
+
+// ---------------------------------------------------------------------------
+// opt-in int8 activations (accuracy_level 4 of the upstream operator)
+
+int64_t xrmm_matmul_nbits_int8a_workspace_bytes(int64_t M, int64_t K) {
+  if (M < 0 || K <= 0 || K % xrmm::kI8aBlock != 0) return -1;
+  return xrmm::i8a_workspace_bytes(M, K);
+}
+
+int xrmm_matmul_nbits_int8a(const void* A, const void* B, const void* scales, const void* zero_points,
+                            int32_t zp_dtype, const void* bias, void* Y, void* workspace, int64_t workspace_bytes,
+                            int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size, int32_t dtype,
+                            void* stream) {
+  if (!t1_ok(dtype)) return fail(XRMM_EINVAL, "T1 must be float32 or float16");
+  if (bits != 4 || block_size < 32 || (block_size & (block_size - 1)) != 0 || K <= 0 || K % xrmm::kI8aBlock != 0 ||
+      K % block_size != 0 || N <= 0 || M < 0)
+    return fail(XRMM_EINVAL, "int8-activation path: bits 4, power-of-two block_size >= 32 dividing K, K a multiple of 128");
+  if (zp_dtype != XRMM_UNSPECIFIED && zp_dtype != XRMM_U8)
+    return fail(XRMM_EINVAL, "int8-activation path: zero points must be absent or packed uint8");
+  if (M == 0) return ok();
+  if (!A || !B || !scales || !Y || !workspace || (zp_dtype == XRMM_U8 && !zero_points))
+    return fail(XRMM_EINVAL, "null tensor pointer");
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (!al(A) || !al(B) || !al(workspace)) return fail(XRMM_EINVAL, "int8-activation path: A, B and the workspace must be 16-byte aligned");
+  if (workspace_bytes < xrmm::i8a_workspace_bytes(M, K))
+    return fail(XRMM_EINVAL, "workspace smaller than xrmm_matmul_nbits_int8a_workspace_bytes");
+  xrmm::Int8aArgs a{};
+  a.A = A;
+  a.B = static_cast<const uint8_t*>(B);
+  a.S = scales;
+  a.Z = zp_dtype == XRMM_U8 ? static_cast<const uint8_t*>(zero_points) : nullptr;
+  a.bias = bias;
+  a.Y = Y;
+  a.qa = static_cast<int8_t*>(workspace);
+  a.as = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + (M * K + 255) / 256 * 256);
+  a.M = M;
+  a.K = K;
+  a.N = N;
+  a.bs = block_size;
+  a.lbs = __builtin_ctz(static_cast<unsigned>(block_size));
+  const int64_t kb = K / block_size;
+  a.zrow = (kb * 4 + 7) / 8;
+  a.f16 = dtype == XRMM_F16;
+  const hipError_t e = xrmm::launch_i8a(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return dev_fail(e, "int8-activation MatMulNBits launch");
+  return ok();
+}

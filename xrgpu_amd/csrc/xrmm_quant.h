@@ -36,3 +36,30 @@ bool bnb4_fast_ok(const Bnb4Args& a);
 hipError_t launch_bnb4(const Bnb4Args& a, hipStream_t st);
 
 }  // namespace xrmm
+
+namespace xrmm {
+
+// Opt-in int8-activation MatMulNBits (accuracy_level 4 of the upstream
+// operator; not the reference's float32 arithmetic).
+constexpr int kI8aBlock = 128;  // activations per quantization block
+
+struct Int8aArgs {
+  const void* A;        // [M, K] float32 / float16
+  const uint8_t* B;     // [N, K / bs, bs / 2] 4-bit codes, low-first
+  const void* S;        // [N, K / bs] scales in A's dtype
+  const uint8_t* Z;     // [N, zrow] packed 4-bit zero points, or null (8)
+  const void* bias;     // [N] or null
+  void* Y;              // [M, N] in A's dtype
+  int8_t* qa;           // workspace: [M, K] codes, each 8-group as k0 k2 k4 k6 k1 k3 k5 k7
+  float* as;            // workspace: [M, K / 128] scales
+  int64_t M, K, N, zrow;
+  int bs, lbs, f16;
+};
+
+inline int64_t i8a_workspace_bytes(int64_t M, int64_t K) {
+  return (M * K + 255) / 256 * 256 + M * (K / kI8aBlock) * 4;
+}
+
+hipError_t launch_i8a(const Int8aArgs& a, hipStream_t st);
+
+}  // namespace xrmm

@@ -302,3 +302,38 @@ def bnb4_kernel(M, K, N, block_size=32, quant_type=1, trans_b=1, dtype=torch.flo
     if r is None:
         raise nat.XrmmInvalid(nat.last_error())
     return r.decode()
+
+
+def matmul_nbits_int8a(A, B, scales, zero_points=None, bias=None, *, K, N, bits=4, block_size=32, out=None,
+                       workspace=None, stream=None):
+    """Opt-in int8-activation MatMulNBits (the upstream operator's
+    accuracy_level 4, not the reference's float32 arithmetic): rows of A are
+    quantized per 128 (max|a| / 127) and multiplied with the 4-bit weights as
+    exact int32 dot products. Packed uint8 zero points only."""
+    _check_dev(A, B, scales, zero_points, bias, out, workspace)
+    if A.dtype not in _T1 or scales.dtype != A.dtype:
+        raise nat.XrmmInvalid("T1 must be float32 or float16")
+    if zero_points is not None and zero_points.dtype != torch.uint8:
+        raise nat.XrmmInvalid("int8-activation path: zero points must be absent or packed uint8")
+    _check_weights(B, scales, zero_points, N, K, bits, block_size, scales.dtype)
+    A2 = A.reshape(-1, K).contiguous()
+    M = int(A2.shape[0])
+    Y = out if out is not None else torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
+    need = int(nat.lib().xrmm_matmul_nbits_int8a_workspace_bytes(M, K))
+    if need < 0:
+        raise nat.XrmmInvalid("int8-activation path: K must be a positive multiple of 128")
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=A.device)
+    nat.check(nat.lib().xrmm_matmul_nbits_int8a(
+        _ptr(A2), _ptr(B), _ptr(scales), _ptr(zero_points), nat.U8 if zero_points is not None else nat.UNSPECIFIED,
+        _ptr(bias), _ptr(Y), _ptr(workspace), workspace.numel(), M, K, N, bits, block_size, _T1[A.dtype],
+        _stream(stream)))
+    return Y
+
+
+def int8a_workspace_bytes(M, K) -> int:
+    """Workspace bytes of ``matmul_nbits_int8a`` (activation codes and scales)."""
+    n = int(nat.lib().xrmm_matmul_nbits_int8a_workspace_bytes(int(M), int(K)))
+    if n < 0:
+        raise nat.XrmmInvalid("int8-activation path: K must be a positive multiple of 128")
+    return max(n, 16)
