@@ -233,8 +233,11 @@ __device__ __forceinline__ u32x4 bld16(rsrc_t r, uint32_t voff, uint32_t soff) {
 // Streaming variants for data read exactly once (weights, scales): the
 // non-temporal cache policy (aux = 2, "nt") keeps them from displacing
 // reused lines.
+#ifndef XRMM_WAUX
+#define XRMM_WAUX 2
+#endif
 __device__ __forceinline__ u32x4 bld16_nt(rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), static_cast<int>(soff), 2));
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), static_cast<int>(soff), XRMM_WAUX));
 }
 
 __device__ __forceinline__ uint32_t bld_u16(rsrc_t r, uint32_t voff, uint32_t soff) {
