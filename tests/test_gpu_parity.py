@@ -177,6 +177,9 @@ BIG_CASES = [
     (140, 512, 72, 128, "float", False),     # float zero points of any value
     (129, 320, 100, 64, None, False),
     (200, 1024, 256, 128, "packed", True),
+    # more tiles than CUs: 256-wide then 192-wide tiles on one grid
+    (256, 64, 65836, 64, "packed", True),    # 258 tile columns; narrow tiles partial and past N
+    (512, 128, 33768, 128, None, True),      # two row tiles of wide + narrow tiles
 ]
 
 

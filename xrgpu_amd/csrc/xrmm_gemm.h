@@ -8,6 +8,15 @@
 // with the other's MFMAs). The 32x32x16 form is used because it reaches the
 // matrix cores' full fp16 rate on gfx950; the 16x16x32 form does not.
 //
+// Tile widths. One workgroup fills a CU, so a grid of T tiles on C CUs runs
+// ceil(T / C) rounds and a partial last round leaves CUs idle (M = 2048,
+// N = 14336: 448 tiles, 1.75 rounds of work in 2). The grid may therefore
+// mix 256-wide tiles with 192-wide ones (waves own 2 x 3 MFMA tiles, 0.75 of
+// the work): with k rounds of wide tiles followed by j rounds of narrow ones
+// every CU does k + 0.75 j tile-units (1 + 0.75 for the shape above). The
+// host picks the mix with the shortest makespan (gemm_tiles); wide tiles
+// come first on the grid, so they are dispatched first.
+//
 // Pipeline. K advances in steps of 64 over a double-buffered LDS. Global loads
 // run two steps ahead into two register sets (each thread: four 16-byte pieces
 // of the activation tile, one 16-byte chunk of one weight column and its raw
@@ -25,7 +34,34 @@ constexpr int GB_M = 256, GB_N = 256, GB_K = 64, GB_T = 512;
 constexpr int GB_LD = GB_K + 8;                      // halfs per staged row (pad spreads banks)
 constexpr int GB_STAGE = (GB_M + GB_N) * GB_LD;      // halfs per pipeline stage
 constexpr size_t GB_LDS = 2 * GB_STAGE * sizeof(_Float16);  // two stages: 147,456 bytes
-constexpr int GB_TM = 2, GB_TN = 4;                  // 32x32 MFMA tiles per wave
+constexpr int GB_TM = 2;                             // 32x32 MFMA row tiles per wave (column tiles: TN)
+
+// Tile plan of a launch: the grid's first `nbig` = row tiles x nb workgroups
+// take 256 x 256 tiles (row tile bid / nb, column tile bid % nb); the rest take
+// 256 x 192 tiles (row tile j / ns, columns 256 nb + 192 (j % ns)).
+struct GemmTiles {
+  uint32_t nb, ns, nbig;
+};
+
+// Shortest-makespan mix of k rounds of 256-wide and j rounds of 192-wide tiles
+// on `cus` CUs (one workgroup per CU); all-wide tiles when no mix is shorter.
+inline GemmTiles gemm_tiles(int64_t M, int64_t N, int cus) {
+  const int64_t mt = (M + GB_M - 1) / GB_M, full = (N + 255) / 256;
+  GemmTiles best{static_cast<uint32_t>(full), 0u, static_cast<uint32_t>(mt * full)};
+  if (cus <= 0 || mt * full <= cus || cus % mt != 0) return best;
+  const int64_t per = cus / mt;                      // column tiles per row tile in one round
+  double best_t = static_cast<double>((mt * full + cus - 1) / cus);
+  for (int64_t k = 0; k * per * 256 < N + 256; ++k)
+    for (int64_t j = 1; 256 * k * per + 192 * j * per < N + 192 * per; ++j) {
+      if (256 * k * per + 192 * j * per < N) continue;
+      const double t = static_cast<double>(k) + 0.75 * static_cast<double>(j);
+      if (t < best_t - 0.05) {
+        best_t = t;
+        best = GemmTiles{static_cast<uint32_t>(k * per), static_cast<uint32_t>(j * per), static_cast<uint32_t>(mt * k * per)};
+      }
+    }
+  return best;
+}
 
 // Global-load registers of one K step.
 template <int SPC>
@@ -36,8 +72,9 @@ struct GbRegs {
   uint32_t z[SPC];   // raw zero-point bits (packed: the byte)
 };
 
-template <int ZPK, int SPC>
-__global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big(Launch L) {
+// One output tile: rows m0 .. m0 + 255, columns n0 .. n0 + 64 TN - 1.
+template <int ZPK, int SPC, int TN>
+__device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const int n0) {
   extern __shared__ __align__(16) unsigned char smem[];
   f16* lds = reinterpret_cast<f16*>(smem);
   constexpr uint32_t OOB = 0x80000000u;
@@ -46,7 +83,6 @@ __global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big(Launch L) {
   const int wm = wave >> 1, wn = wave & 1;
   const Proj& P = L.p[0];
   const int M = static_cast<int>(L.M), N = static_cast<int>(P.N), K = static_cast<int>(L.K);
-  const int m0 = static_cast<int>(blockIdx.y) * GB_M, n0 = static_cast<int>(blockIdx.x) * GB_N;
   const int Kp = static_cast<int>(L.kb * L.block_size);
   const uint32_t rowb = static_cast<uint32_t>(Kp / 2);
   const int nchunk = static_cast<int>(rowb / 16);
@@ -60,7 +96,7 @@ __global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big(Launch L) {
   // branch around the load).
   const int bc = tid >> 1, bh = tid & 1;
   const int bn = n0 + bc;
-  const bool bnval = bn < N;
+  const bool bnval = bc < 64 * TN && bn < N;  // narrow tiles: threads past the tile load nothing
   const uint32_t zrow = ZPK == ZP_PACKED ? static_cast<uint32_t>(L.zrow) : kb * (L.zp_dtype == DT_F32 ? 4u : 2u);
   const rsrc_t rB = mk_rsrc(P.B, static_cast<uint32_t>(N) * rowb);
   // scale / zero-point bounds rounded to 16 bytes: the range check zeroes a
@@ -133,29 +169,29 @@ __global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big(Launch L) {
     *reinterpret_cast<f16x8*>(Bs + bc * GB_LD + bh * 32 + d * 8) = b;
   };
 
-  f32x16 acc[GB_TM][GB_TN];
+  f32x16 acc[GB_TM][TN];
 #pragma unroll
   for (int i = 0; i < GB_TM; ++i)
 #pragma unroll
-    for (int j = 0; j < GB_TN; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   // Fragments of K slice kk (0..3) of a stage: lane (r, g) = (lane % 32,
   // lane / 32) reads row / column r, k = 16 kk + 8 g .. + 7.
-  f16x8 fa[2][GB_TM], fb[2][GB_TN];
+  f16x8 fa[2][GB_TM], fb[2][TN];
   auto read_frags = [&](int stage, int kk, int buf) {
     const int ko = kk * 16 + (lane >> 5) * 8;
     const f16* As = lds + stage * GB_STAGE + (wm * 64 + (lane & 31)) * GB_LD + ko;
-    const f16* Bs = lds + stage * GB_STAGE + (GB_M + wn * 128 + (lane & 31)) * GB_LD + ko;
+    const f16* Bs = lds + stage * GB_STAGE + (GB_M + wn * 32 * TN + (lane & 31)) * GB_LD + ko;
 #pragma unroll
     for (int i = 0; i < GB_TM; ++i) fa[buf][i] = *reinterpret_cast<const f16x8*>(As + i * 32 * GB_LD);
 #pragma unroll
-    for (int j = 0; j < GB_TN; ++j) fb[buf][j] = *reinterpret_cast<const f16x8*>(Bs + j * 32 * GB_LD);
+    for (int j = 0; j < TN; ++j) fb[buf][j] = *reinterpret_cast<const f16x8*>(Bs + j * 32 * GB_LD);
   };
   auto mfmas = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < GB_TN; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int i = 0; i < GB_TM; ++i)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0);
@@ -200,8 +236,8 @@ __global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big(Launch L) {
   const f16* biasp = static_cast<const f16*>(P.bias);
   f16* Y = static_cast<f16*>(P.Y);
 #pragma unroll
-  for (int j = 0; j < GB_TN; ++j) {
-    const int n = n0 + wn * 128 + j * 32 + (lane & 31);
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wn * 32 * TN + j * 32 + (lane & 31);
     if (n >= N) continue;
     const float bias = biasp ? static_cast<float>(biasp[n]) : 0.f;
 #pragma unroll
@@ -215,6 +251,22 @@ __global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big(Launch L) {
   }
 }
 
+// The grid is one dimension: workgroup bid takes a wide tile when bid < nbig
+// (a scalar, uniform branch), else a narrow one.
+template <int ZPK, int SPC>
+__global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big(Launch L, GemmTiles t) {
+  const uint32_t bid = blockIdx.x;
+  if (bid < t.nbig) {
+    gemm_tile<ZPK, SPC, 4>(L, static_cast<int>(bid / t.nb) * GB_M, static_cast<int>(bid % t.nb) * 256);
+  } else {
+    const uint32_t j = bid - t.nbig;
+    gemm_tile<ZPK, SPC, 3>(L, static_cast<int>(j / t.ns) * GB_M, static_cast<int>(t.nb * 256u + (j % t.ns) * 192u));
+  }
+}
+
+// Compute units of the current device (cached per device ordinal).
+int device_cus();
+
 template <int ZPK, int SPC>
 inline hipError_t launch_gemm_big(const Launch& L, hipStream_t st) {
   auto kern = k_gemm_q4_big<ZPK, SPC>;
@@ -223,8 +275,10 @@ inline hipError_t launch_gemm_big(const Launch& L, hipStream_t st) {
                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      static_cast<int>(GB_LDS));
   if (attr != hipSuccess) return attr;
-  const dim3 grid(static_cast<uint32_t>((L.p[0].N + GB_N - 1) / GB_N), static_cast<uint32_t>((L.M + GB_M - 1) / GB_M));
-  hipLaunchKernelGGL(kern, grid, dim3(GB_T), GB_LDS, st, L);
+  const GemmTiles t = gemm_tiles(L.M, L.p[0].N, device_cus());
+  const int64_t mt = (L.M + GB_M - 1) / GB_M;
+  const dim3 grid(static_cast<uint32_t>(mt * (t.nb + t.ns)));
+  hipLaunchKernelGGL(kern, grid, dim3(GB_T), GB_LDS, st, L, t);
   return hipGetLastError();
 }
 

@@ -25,6 +25,8 @@
 // reference's float32 weight rounded once to binary16. Codes are widened with
 // the exponent-bias trick: OR-ing a nibble into the mantissa of 1024.0h gives
 // 1024 + code exactly (and 1024 + 16*code for the high nibble of a byte).
+#include <atomic>
+
 #include "xrmm_gemv.h"
 #include "xrmm_gemv_dot.h"
 #include "xrmm_gemv_sk.h"
@@ -272,6 +274,18 @@ static bool q4_fast_ok(const Launch& L) {
     if (L.zp_kind == ZP_FLOAT && L.p[i].zp == nullptr) return false;
   }
   return true;
+}
+
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
 }
 
 // From this many rows the 256 x 256 GEMM wastes less on partial row tiles than
