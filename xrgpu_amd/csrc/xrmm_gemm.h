@@ -232,21 +232,41 @@ __device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const i
   }
   if (ks < ksteps) step(ks, 0, r1, r0);
 
-  // epilogue: lane holds D[8 (e / 4) + 4 (lane / 32) + e % 4][lane % 32] of each 32x32 tile
+  // Epilogue: lane holds D[8 (e / 4) + 4 (lane / 32) + e % 4][lane % 32] of
+  // each 32x32 tile. The tile (+ bias, rounded once to binary16) goes through
+  // LDS row-major, so Y is written in whole 16-byte pieces of its rows (a
+  // wave stores 1 KB of two rows per instruction) instead of 2-byte scatters
+  // that leave partial lines.
+  constexpr int YLD = 64 * TN + 8;  // halfs per staged output row (pad spreads banks)
+  static_assert(GB_M * YLD * 2 <= static_cast<int>(GB_LDS), "the output tile fits the LDS");
   const f16* biasp = static_cast<const f16*>(P.bias);
-  f16* Y = static_cast<f16*>(P.Y);
+  __syncthreads();  // every wave's last fragment reads are done
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int n = n0 + wn * 32 * TN + j * 32 + (lane & 31);
-    if (n >= N) continue;
-    const float bias = biasp ? static_cast<float>(biasp[n]) : 0.f;
+    const int c = wn * 32 * TN + j * 32 + (lane & 31);
+    const float bias = (biasp != nullptr && n0 + c < N) ? static_cast<float>(biasp[n0 + c]) : 0.f;
 #pragma unroll
-    for (int i = 0; i < GB_TM; ++i) {
+    for (int i = 0; i < GB_TM; ++i)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int m = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        if (m < M) Y[static_cast<int64_t>(m) * N + n] = static_cast<f16>(acc[i][j][e] + bias);
+        const int r = wm * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        lds[r * YLD + c] = static_cast<f16>(acc[i][j][e] + bias);
       }
+  }
+  __syncthreads();
+  f16* Y = static_cast<f16*>(P.Y);
+  constexpr int PPR = 8 * TN;  // 16-byte pieces per tile row
+  const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15u) == 0;
+  for (int idx = tid; idx < GB_M * PPR; idx += GB_T) {
+    const int r = idx / PPR, p = idx % PPR;
+    const int m = m0 + r, n = n0 + 8 * p;
+    if (m >= M || n >= N) continue;
+    const f16* src = lds + r * YLD + 8 * p;
+    f16* dst = Y + static_cast<int64_t>(m) * N + n;
+    if (vec) {
+      *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+    } else {
+      for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = src[e];
     }
   }
 }
