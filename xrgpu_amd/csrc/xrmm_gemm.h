@@ -37,8 +37,8 @@ constexpr size_t GB_LDS = 2 * GB_STAGE * sizeof(_Float16);  // two stages: 147,4
 constexpr int GB_TM = 2;                             // 32x32 MFMA row tiles per wave (column tiles: TN)
 
 // Tile plan of a launch: the grid's first `nbig` = row tiles x nb workgroups
-// take 256 x 256 tiles (row tile bid / nb, column tile bid % nb); the rest take
-// 256 x 192 tiles (row tile j / ns, columns 256 nb + 192 (j % ns)).
+// take 256 x 256 tiles (column tiles 0 .. nb - 1); the rest take 256 x 192
+// tiles (columns 256 nb + 192 j, j < ns). tile_of orders each set.
 struct GemmTiles {
   uint32_t nb, ns, nbig;
 };
@@ -271,16 +271,41 @@ __device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const i
   }
 }
 
+// Tile of workgroup b among the T = mt * nc tiles of one width. Consecutive
+// workgroups are dispatched to consecutive XCDs (eight on gfx950, each with
+// its own L2), so when T % 8 == 0 workgroup b takes logical tile
+// (b % 8) * (T / 8) + b / 8: every XCD walks a contiguous range of the
+// logical order. That order is a raster grouped by XRMM_GEMM_GROUP row tiles
+// (row fastest inside a group), so the tiles one XCD runs at once share a few
+// activation row panels and weight column panels in its L2 instead of
+// spanning every row panel.
+#ifndef XRMM_GEMM_GROUP
+#define XRMM_GEMM_GROUP 4
+#endif
+__device__ __forceinline__ void tile_of(uint32_t b, uint32_t mt, uint32_t nc, uint32_t& row, uint32_t& col) {
+  const uint32_t T = mt * nc;
+  const uint32_t l = (T & 7u) == 0 ? (b & 7u) * (T >> 3) + (b >> 3) : b;
+  constexpr uint32_t G = XRMM_GEMM_GROUP;
+  const uint32_t g = l / (G * nc);
+  const uint32_t rows = mt - g * G < G ? mt - g * G : G;  // row tiles in this group
+  const uint32_t r = l - g * G * nc;
+  row = g * G + r % rows;
+  col = r / rows;
+}
+
 // The grid is one dimension: workgroup bid takes a wide tile when bid < nbig
 // (a scalar, uniform branch), else a narrow one.
 template <int ZPK, int SPC>
 __global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big(Launch L, GemmTiles t) {
   const uint32_t bid = blockIdx.x;
+  const uint32_t mt = static_cast<uint32_t>((L.M + GB_M - 1) / GB_M);
+  uint32_t row, col;
   if (bid < t.nbig) {
-    gemm_tile<ZPK, SPC, 4>(L, static_cast<int>(bid / t.nb) * GB_M, static_cast<int>(bid % t.nb) * 256);
+    tile_of(bid, mt, t.nb, row, col);
+    gemm_tile<ZPK, SPC, 4>(L, static_cast<int>(row) * GB_M, static_cast<int>(col) * 256);
   } else {
-    const uint32_t j = bid - t.nbig;
-    gemm_tile<ZPK, SPC, 3>(L, static_cast<int>(j / t.ns) * GB_M, static_cast<int>(t.nb * 256u + (j % t.ns) * 192u));
+    tile_of(bid - t.nbig, mt, t.ns, row, col);
+    gemm_tile<ZPK, SPC, 3>(L, static_cast<int>(row) * GB_M, static_cast<int>(t.nb * 256u + col * 192u));
   }
 }
 
