@@ -45,21 +45,23 @@ struct GemmTiles {
 
 // Shortest-makespan mix of k rounds of 256-wide and j rounds of 192-wide tiles
 // on `cus` CUs (one workgroup per CU); all-wide tiles when no mix is shorter.
+// For j narrow rounds only the fewest wide rounds that still cover N matter,
+// so the search is over j alone (a few iterations per launch).
 inline GemmTiles gemm_tiles(int64_t M, int64_t N, int cus) {
   const int64_t mt = (M + GB_M - 1) / GB_M, full = (N + 255) / 256;
   GemmTiles best{static_cast<uint32_t>(full), 0u, static_cast<uint32_t>(mt * full)};
   if (cus <= 0 || mt * full <= cus || cus % mt != 0) return best;
-  const int64_t per = cus / mt;                      // column tiles per row tile in one round
+  const int64_t per = cus / mt;  // column tiles per row tile in one round
   double best_t = static_cast<double>((mt * full + cus - 1) / cus);
-  for (int64_t k = 0; k * per * 256 < N + 256; ++k)
-    for (int64_t j = 1; 256 * k * per + 192 * j * per < N + 192 * per; ++j) {
-      if (256 * k * per + 192 * j * per < N) continue;
-      const double t = static_cast<double>(k) + 0.75 * static_cast<double>(j);
-      if (t < best_t - 0.05) {
-        best_t = t;
-        best = GemmTiles{static_cast<uint32_t>(k * per), static_cast<uint32_t>(j * per), static_cast<uint32_t>(mt * k * per)};
-      }
+  for (int64_t j = 1; j <= 16; ++j) {
+    const int64_t rest = N - 192 * j * per;  // columns left for the wide tiles
+    const int64_t k = rest > 0 ? (rest + 256 * per - 1) / (256 * per) : 0;
+    const double t = static_cast<double>(k) + 0.75 * static_cast<double>(j);
+    if (t < best_t - 0.05) {
+      best_t = t;
+      best = GemmTiles{static_cast<uint32_t>(k * per), static_cast<uint32_t>(j * per), static_cast<uint32_t>(mt * k * per)};
     }
+  }
   return best;
 }
 
