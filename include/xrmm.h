@@ -300,7 +300,7 @@ const char* xrmm_matmul_bnb4_kernel(int64_t M, int64_t K, int64_t N, int32_t blo
  * block of 128 (scale = max|a| / 127, codes rint(a / scale)), the 4-bit
  * weights enter as signed bytes (code - zero point) and chunk sums are exact
  * int32 dot products scaled in float32. bits 4, power-of-two block_size >= 32
- * dividing K, K a multiple of 128, zero points absent or packed uint8,
+ * dividing K, K a multiple of 128 and at most 16384, zero points absent or packed uint8,
  * 16-byte aligned A, B and workspace (>= xrmm_matmul_nbits_int8a_workspace_bytes
  * bytes). Same argument meaning as xrmm_matmul_nbits otherwise. */
 int64_t xrmm_matmul_nbits_int8a_workspace_bytes(int64_t M, int64_t K);

@@ -36,6 +36,16 @@ def test_invalid_geometry_is_einval(kw, msg):
     assert msg in nat.last_error()
 
 
+@pytest.mark.parametrize("K,msg", [(100, "multiple of 128"), (16384 + 128, "K up to 16384")])
+def test_int8a_rejects_unsupported_k(K, msg):
+    """The int8-activation GEMV holds a column's codes in one wave (at most
+    16384 codes): a longer K is an error, not a silently truncated sum."""
+    rc = nat.lib().xrmm_matmul_nbits_int8a(None, None, None, None, nat.UNSPECIFIED, None, None, None, 0, 1, K, 8,
+                                           4, 32, nat.F16, None)
+    assert rc == nat.XRMM_EINVAL and msg in nat.last_error()
+    assert nat.lib().xrmm_matmul_nbits_int8a_workspace_bytes(1, K) == -1
+
+
 def test_empty_m_is_a_no_op_without_device():
     # M = 0 (fixture empty_zero_dim): nothing to launch, returns OK
     rc = nat.lib().xrmm_matmul_nbits(None, None, None, None, nat.UNSPECIFIED, None, None, 0, 32, 4, 4, 32,

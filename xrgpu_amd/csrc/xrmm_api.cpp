@@ -379,7 +379,7 @@ const char* xrmm_matmul_bnb4_kernel(int64_t M, int64_t K, int64_t N, int32_t blo
 // opt-in int8 activations (accuracy_level 4 of the upstream operator)
 
 int64_t xrmm_matmul_nbits_int8a_workspace_bytes(int64_t M, int64_t K) {
-  if (M < 0 || K <= 0 || K % xrmm::kI8aBlock != 0) return -1;
+  if (M < 0 || K <= 0 || K % xrmm::kI8aBlock != 0 || K > xrmm::kI8aMaxK) return -1;
   return xrmm::i8a_workspace_bytes(M, K);
 }
 
@@ -391,6 +391,7 @@ int xrmm_matmul_nbits_int8a(const void* A, const void* B, const void* scales, co
   if (bits != 4 || block_size < 32 || (block_size & (block_size - 1)) != 0 || K <= 0 || K % xrmm::kI8aBlock != 0 ||
       K % block_size != 0 || N <= 0 || M < 0)
     return fail(XRMM_EINVAL, "int8-activation path: bits 4, power-of-two block_size >= 32 dividing K, K a multiple of 128");
+  if (K > xrmm::kI8aMaxK) return fail(XRMM_EINVAL, "int8-activation path: K up to 16384 (one wave holds a column's codes)");
   if (zp_dtype != XRMM_UNSPECIFIED && zp_dtype != XRMM_U8)
     return fail(XRMM_EINVAL, "int8-activation path: zero points must be absent or packed uint8");
   if (M == 0) return ok();

@@ -119,6 +119,7 @@ hipError_t launch_t(const Int8aArgs& a, hipStream_t st) {
 
 hipError_t launch_i8a(const Int8aArgs& a, hipStream_t st) {
   if (a.M == 0) return hipSuccess;
+  if (a.K > kI8aMaxK) return hipErrorInvalidValue;  // the GEMV would drop the chunks past 16384 codes
   return a.f16 ? launch_t<f16>(a, st) : launch_t<float>(a, st);
 }
 

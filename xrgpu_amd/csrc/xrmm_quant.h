@@ -42,6 +42,9 @@ namespace xrmm {
 // Opt-in int8-activation MatMulNBits (accuracy_level 4 of the upstream
 // operator; not the reference's float32 arithmetic).
 constexpr int kI8aBlock = 128;  // activations per quantization block
+// A wave holds one column's codes in registers: 64 lanes x at most 8 chunks
+// of 32 codes.
+constexpr int64_t kI8aMaxK = 64 * 8 * 32;
 
 struct Int8aArgs {
   const void* A;        // [M, K] float32 / float16
