@@ -321,7 +321,7 @@ def matmul_nbits_int8a(A, B, scales, zero_points=None, bias=None, *, K, N, bits=
     Y = out if out is not None else torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
     need = int(nat.lib().xrmm_matmul_nbits_int8a_workspace_bytes(M, K))
     if need < 0:
-        raise nat.XrmmInvalid("int8-activation path: K must be a positive multiple of 128")
+        raise nat.XrmmInvalid("int8-activation path: K must be a positive multiple of 128, at most 16384")
     if workspace is None:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=A.device)
     nat.check(nat.lib().xrmm_matmul_nbits_int8a(
@@ -335,5 +335,5 @@ def int8a_workspace_bytes(M, K) -> int:
     """Workspace bytes of ``matmul_nbits_int8a`` (activation codes and scales)."""
     n = int(nat.lib().xrmm_matmul_nbits_int8a_workspace_bytes(int(M), int(K)))
     if n < 0:
-        raise nat.XrmmInvalid("int8-activation path: K must be a positive multiple of 128")
+        raise nat.XrmmInvalid("int8-activation path: K must be a positive multiple of 128, at most 16384")
     return max(n, 16)
