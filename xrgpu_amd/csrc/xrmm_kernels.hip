@@ -374,6 +374,7 @@ hipError_t launch(const Launch& L, hipStream_t st) {
   int64_t cols = L.p[0].N;
   if (L.op == OP_QKV) cols += L.p[1].N + L.p[2].N;
   constexpr int MB = 8;
+  if (cols > (int64_t(1) << 31) - 1) return hipErrorInvalidValue;  // launch limit
   const dim3 grid(static_cast<uint32_t>(cols), static_cast<uint32_t>((L.M + MB - 1) / MB));
   hipLaunchKernelGGL(k_generic<MB>, grid, dim3(64), 0, st, L);
   return hipGetLastError();
@@ -385,6 +386,7 @@ hipError_t launch_dequantize(const Launch& L, void* W, int out_dtype, hipStream_
   if (out_dtype == DT_F16 && L.bits == 4 && L.dtype == DT_F16 && L.bs_log2 >= 4 &&
       (L.kb * L.block_size) % 32 == 0 && aligned16(P.B)) {
     const int64_t n = P.N * (L.kb * L.blob / 16);
+    if ((n + 255) / 256 > (int64_t(1) << 31) - 1) return hipErrorInvalidValue;  // launch limit
     const dim3 grid(static_cast<uint32_t>((n + 255) / 256));
     const int spc = spc_of(L.block_size);
     const int zpk = P.zp ? L.zp_kind : ZP_NONE;
@@ -401,6 +403,7 @@ hipError_t launch_dequantize(const Launch& L, void* W, int out_dtype, hipStream_
     return hipGetLastError();
   }
   const int64_t n = P.N * L.K;
+  if ((n + 255) / 256 > (int64_t(1) << 31) - 1) return hipErrorInvalidValue;  // launch limit
   hipLaunchKernelGGL(k_dequant_f32, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, st, L, W, out_dtype);
   return hipGetLastError();
 }

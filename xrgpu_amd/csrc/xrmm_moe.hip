@@ -616,6 +616,10 @@ hipError_t launch_qmoe(const MoeArgs& a, hipStream_t st) {
     if (sm == SM_ROW) return launch_fast<8, SM_ROW>(a, st);
     return launch_fast<8, SM_CHUNK>(a, st);
   }
+  // one thread per (token, slot, column) and per (token, column): the grids
+  // must stay within the launch limit of 2^31 - 1 workgroups
+  const int64_t lim = (int64_t(1) << 31) - 1;
+  if ((a.T * a.k * a.I + MOE_T - 1) / MOE_T > lim || (a.T * a.H + MOE_T - 1) / MOE_T > lim) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_moe_route, dim3(static_cast<uint32_t>((a.T + 3) / 4)), dim3(MOE_T), 0, st, a.router, a.sel, a.wts,
                      static_cast<int>(a.T), static_cast<int>(a.E), a.k);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;

@@ -357,6 +357,7 @@ hipError_t launch_gbq(const GbqArgs& a, hipStream_t st) {
   if (a.n == 0 || a.width == 0) return hipSuccess;
   if (gbq_fast_ok(a)) {
     const int64_t bpr = (a.pcols / 4 + QT - 1) / QT;
+    if (a.n * bpr > (int64_t(1) << 31) - 1) return hipErrorInvalidValue;  // launch limit
     const dim3 grid(static_cast<uint32_t>(a.n * bpr));
     if (a.bits == 4)
       hipLaunchKernelGGL(k_gbq_words<4>, grid, dim3(QT), 0, st, a, bpr);
@@ -364,6 +365,7 @@ hipError_t launch_gbq(const GbqArgs& a, hipStream_t st) {
       hipLaunchKernelGGL(k_gbq_words<8>, grid, dim3(QT), 0, st, a, bpr);
     return hipGetLastError();
   }
+  if ((a.n * a.width + QT - 1) / QT > (int64_t(1) << 31) - 1) return hipErrorInvalidValue;  // launch limit
   hipLaunchKernelGGL(k_gbq_scalar, dim3(static_cast<uint32_t>((a.n * a.width + QT - 1) / QT)), dim3(QT), 0, st, a);
   return hipGetLastError();
 }
@@ -390,6 +392,7 @@ hipError_t launch_bnb4(const Bnb4Args& a, hipStream_t st) {
     if (mr == 2) return launch_bnb4_fast<float, 2>(a, st);
     return launch_bnb4_fast<float, 4>(a, st);
   }
+  if ((a.M * a.N + QT - 1) / QT > (int64_t(1) << 31) - 1) return hipErrorInvalidValue;  // launch limit
   const dim3 grid(static_cast<uint32_t>((a.M * a.N + QT - 1) / QT));
   if (a.f16)
     hipLaunchKernelGGL(k_bnb4_scalar<f16>, grid, dim3(QT), 0, st, a);
