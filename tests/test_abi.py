@@ -46,6 +46,19 @@ def test_int8a_rejects_unsupported_k(K, msg):
     assert nat.lib().xrmm_matmul_nbits_int8a_workspace_bytes(1, K) == -1
 
 
+def test_big_gemm_tile_threshold_override(monkeypatch):
+    """XRMM_GEMM_BIG_MIN_TILES moves the 256 x 256 GEMM's tile threshold
+    (read at every selection); malformed values keep the default."""
+    sel = lambda: nat.lib().xrmm_select_kernel(0, 256, 1024, 256, 4, 128, nat.F16, nat.U8).decode()
+    assert sel() == "gemm_q4_mfma"
+    monkeypatch.setenv("XRMM_GEMM_BIG_MIN_TILES", "0")
+    assert sel() == "gemm_q4_big"
+    monkeypatch.setenv("XRMM_GEMM_BIG_MIN_TILES", "-3")
+    assert sel() == "gemm_q4_mfma"
+    monkeypatch.setenv("XRMM_GEMM_BIG_MIN_TILES", "12x")
+    assert sel() == "gemm_q4_mfma"
+
+
 def test_empty_m_is_a_no_op_without_device():
     # M = 0 (fixture empty_zero_dim): nothing to launch, returns OK
     rc = nat.lib().xrmm_matmul_nbits(None, None, None, None, nat.UNSPECIFIED, None, None, 0, 32, 4, 4, 32,
@@ -68,8 +81,11 @@ def test_qkv_requires_norm_scale():
     (0, 5, 2048, 14336, 64, nat.F16, nat.F16, "gemv_q4_splitk"),
     (0, 16, 1024, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),   # 32 chunks: no even split
     (0, 16, 4096, 14336, 16, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),   # bs = 16
-    (0, 2048, 4096, 14336, 128, nat.F16, nat.U8, "gemm_q4_big"),
-    (0, 128, 4096, 14336, 32, nat.F16, nat.F16, "gemm_q4_big"),
+    (0, 2048, 4096, 14336, 128, nat.F16, nat.U8, "gemm_q4_big"),      # 448 tiles of 256 x 256
+    (0, 2048, 14336, 4096, 128, nat.F16, nat.U8, "gemm_q4_big"),      # 128 tiles: half the CUs
+    (0, 1024, 14336, 4096, 128, nat.F16, nat.U8, "gemm_q4_mfma"),     # 64 tiles: the 128 x 128 GEMM
+    (0, 256, 4096, 14336, 128, nat.F16, nat.UNSPECIFIED, "gemm_q4_mfma"),
+    (0, 128, 4096, 14336, 32, nat.F16, nat.F16, "gemm_q4_big"),       # float zero points: always big
     (0, 127, 4096, 14336, 32, nat.F16, nat.U8, "gemm_q4_mfma"),
     (0, 64, 4096, 14336, 32, nat.F16, nat.F16, "generic"),
     (1, 4, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_dot"),

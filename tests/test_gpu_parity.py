@@ -183,8 +183,15 @@ BIG_CASES = [
 ]
 
 
+@pytest.fixture
+def big_gemm(monkeypatch):
+    """Shapes below the 256 x 256 GEMM's tile threshold reach it through
+    XRMM_GEMM_BIG_MIN_TILES = 0, so its edge cases stay small."""
+    monkeypatch.setenv("XRMM_GEMM_BIG_MIN_TILES", "0")
+
+
 @pytest.mark.parametrize("M,K,N,bs,zp,bias", BIG_CASES)
-def test_gemm_big_parity(gpu, M, K, N, bs, zp, bias):
+def test_gemm_big_parity(gpu, big_gemm, M, K, N, bs, zp, bias):
     rng = np.random.default_rng(M * 31 + K + N + bs)
     A, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, np.float16, zp, bias)
     kind = None if zp is None else ("packed" if zp == "packed" else "float")
@@ -194,7 +201,7 @@ def test_gemm_big_parity(gpu, M, K, N, bs, zp, bias):
     assert_parity(Y, ref, np.float16)
 
 
-def test_gemm_big_float32_zero_points(gpu):
+def test_gemm_big_float32_zero_points(gpu, big_gemm):
     """T3 = float32 zero points with float16 activations on the 256 x 256 GEMM."""
     rng = np.random.default_rng(78)
     M, K, N, bs = 192, 1024, 80, 32
@@ -204,7 +211,7 @@ def test_gemm_big_float32_zero_points(gpu):
     assert_parity(Y, O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs), np.float16)
 
 
-def test_gemm_big_repeat_and_rows_independent(gpu):
+def test_gemm_big_repeat_and_rows_independent(gpu, big_gemm):
     """Two launches give identical bytes, and row r of a 384-row product equals
     the same row computed within a 128-row product (rows never mix)."""
     rng = np.random.default_rng(79)

@@ -26,6 +26,7 @@
 // the exponent-bias trick: OR-ing a nibble into the mantissa of 1024.0h gives
 // 1024 + code exactly (and 1024 + 16*code for the high nibble of a byte).
 #include <atomic>
+#include <cstdlib>
 
 #include "xrmm_gemv.h"
 #include "xrmm_gemv_dot.h"
@@ -292,6 +293,30 @@ int device_cus() {
 // the 128 x 128 one loses to its lower MFMA rate.
 constexpr int64_t kGemmBigMinM = 128;
 
+// ...and only with enough 256 x 256 tiles to occupy half of the 256 CUs (one
+// workgroup per CU): with fewer, the 128 x 128 GEMM's four times as many tiles
+// win (M=1024 K=14336 N=4096, 64 tiles: 245 against 321 us; M=256 K=4096
+// N=14336, 56 tiles: 75 against 96 us; at 112 and 128 tiles the two tie; at
+// 448 tiles the big GEMM takes 256 against 367 us). The environment variable
+// XRMM_GEMM_BIG_MIN_TILES overrides the threshold (0: the big GEMM from
+// kGemmBigMinM rows on). Float zero points always take the big GEMM.
+constexpr int64_t kGemmBigMinTiles = 128;
+
+static int64_t gemm_big_min_tiles() {
+  const char* e = std::getenv("XRMM_GEMM_BIG_MIN_TILES");
+  if (e != nullptr && *e != 0) {
+    char* end = nullptr;
+    const long long v = std::strtoll(e, &end, 10);
+    if (end != nullptr && *end == 0 && v >= 0) return v;
+  }
+  return kGemmBigMinTiles;
+}
+
+static bool gemm_big_fills(const Launch& L) {
+  const int64_t tiles = (L.M + GB_M - 1) / GB_M * ((L.p[0].N + 255) / 256);
+  return L.zp_kind == ZP_FLOAT || tiles >= gemm_big_min_tiles();
+}
+
 // Rows from which the split-K MFMA GEMV takes over from the dot GEMV (up to
 // 16 rows): the dot kernel's VALU work grows with every row, the MFMA's does
 // not. Measured with K = 4096: MatMulNBits at two rows is a tie (10.0 vs
@@ -305,7 +330,7 @@ Kernel select_kernel(const Launch& L) {
     if (L.M >= split_k_min_rows(L.op) && sk_fits(L)) return K_GEMV_SK;
     if ((L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 && dot_fits(L)) return K_GEMV_DOT;
     if (L.M >= 1 && L.M <= 16 && gemv_tiles(L) != 0) return K_GEMV_Q4;
-    if (L.M >= kGemmBigMinM && L.op == OP_MATMUL) return K_GEMM_BIG;
+    if (L.M >= kGemmBigMinM && L.op == OP_MATMUL && gemm_big_fills(L)) return K_GEMM_BIG;
     if (L.M > 16 && L.op == OP_MATMUL && L.zp_kind != ZP_FLOAT) return K_GEMM_Q4;
   }
   return K_GENERIC;
