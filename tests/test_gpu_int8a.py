@@ -35,6 +35,9 @@ CASES = [  # M, K, N, block, zero points, bias, dtype
     (16, 1024, 128, 128, True, False, np.float16),
     (40, 512, 96, 256, False, True, np.float32),
     (2, 8192, 64, 32, True, False, np.float32),
+    (8, 4096, 300, 64, True, True, np.float16),     # 32 KB of activation codes
+    (9, 4096, 100, 128, False, False, np.float32),
+    (64, 1024, 200, 64, True, True, np.float16),    # 64 rows
 ]
 
 
