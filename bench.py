@@ -303,7 +303,7 @@ def main():
     ap.add_argument("--only", default="")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build's hot path (MatMulNBits family) runs on a single device; "
+        print("bench.py measures one GPU: the MatMulNBits family runs on a single device here; "
               "multi-GPU sharding is a design note only.", file=sys.stderr)
         sys.exit(2)
 

@@ -1,6 +1,6 @@
 """NumPy oracle for com.microsoft.QMoE, opcode 1030 (test infrastructure only).
 
-This module is the CHECKER, never the product: only ``tests/``,
+This module is the oracle, test infrastructure and never the product: only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` may import it.
 
 It restates, on the CPU, the arithmetic of xrGPU's serial Vulkan shader for the

@@ -1,6 +1,6 @@
 """NumPy oracle for the MatMulNBits operator family (test infrastructure only).
 
-This module is the CHECKER, never the product. Only ``tests/``,
+This module is the oracle, test infrastructure and never the product. Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it. The product path (``xrgpu_amd``) never calls into it and fails
 loudly when its HIP library is missing.

@@ -1,7 +1,7 @@
 """NumPy oracle for com.microsoft.GatherBlockQuantized (opcode 1031) and
 com.microsoft.MatMulBnb4 (opcode 1026) (test infrastructure only).
 
-This module is the CHECKER, never the product: only ``tests/``,
+This module is the oracle, test infrastructure and never the product: only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` may import it.
 
 It restates, on the CPU, the arithmetic of xrGPU's serial Vulkan shader:
