@@ -183,6 +183,29 @@ BIG_CASES = [
 ]
 
 
+ODD_ZP_CASES = [
+    # M, K, N, bs: packed zero-point rows of an odd byte count (ceil(kb / 2)
+    # odd), so a column's zero points start at any byte offset
+    (1, 864, 64, 64),      # kb 14: 7-byte rows
+    (2, 11008, 40, 128),   # kb 86: 43-byte rows (a 7B-class down projection)
+    (1, 640, 100, 64),     # kb 10: 5-byte rows
+    (4, 11008, 36, 128),
+    (8, 11008, 48, 128),
+    (64, 864, 200, 64),
+    (300, 11008, 72, 128),
+]
+
+
+@pytest.mark.parametrize("M,K,N,bs", ODD_ZP_CASES)
+def test_packed_zero_points_odd_rows(gpu, M, K, N, bs):
+    rng = np.random.default_rng(M * 17 + K + N + bs)
+    A, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, np.float16, "packed", True)
+    assert Z.shape[1] % 2 == 1
+    Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
+    kern = ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16, "packed")
+    assert_parity(Y, O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs), np.float16, kern)
+
+
 @pytest.fixture
 def big_gemm(monkeypatch):
     """Shapes below the 256 x 256 GEMM's tile threshold reach it through

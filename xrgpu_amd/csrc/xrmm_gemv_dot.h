@@ -80,7 +80,7 @@ struct DotProj {
   const void* Z;
   void* Y;
   uint32_t N;
-  uint32_t wg0;  // first workgroup of this projection on the grid
+  uint32_t wg0;  // first wave of this projection on the grid (global wave index)
 };
 
 struct DotArgs {
@@ -118,12 +118,14 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // The workgroup's projection: Qkv lays Q, K and V side by side on the grid.
-  // Every projection's fields are loaded with the other arguments and picked
-  // with scalar selects, so no load depends on the choice.
+  // The wave's projection: Qkv lays the waves of Q, K and V side by side on
+  // the grid (a workgroup may hold waves of two projections: they share the
+  // activations). Every projection's fields are loaded with the other
+  // arguments and picked with scalar selects, so no load depends on the choice.
   const uint32_t bid = blockIdx.x;
+  const uint32_t gw = bid * W + wave;  // global wave index
   uint32_t pi = 0;
-  if constexpr (QKV) pi = (bid >= a.p[1].wg0 ? 1u : 0u) + (bid >= a.p[2].wg0 ? 1u : 0u);
+  if constexpr (QKV) pi = (gw >= a.p[1].wg0 ? 1u : 0u) + (gw >= a.p[2].wg0 ? 1u : 0u);
   auto pick = [&](auto v0, auto v1, auto v2) { return QKV ? (pi == 0 ? v0 : pi == 1 ? v1 : v2) : v0; };
   const uint8_t* Bp = pick(a.p[0].B, a.p[1].B, a.p[2].B);
   const void* Sp = pick(a.p[0].S, a.p[1].S, a.p[2].S);
@@ -134,7 +136,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
   const uint32_t K = a.K, kb = a.kb, rowb = a.rowb, zrow = a.zrow;
   const uint32_t nchunk = rowb >> 4;
   const int M = static_cast<int>(a.M);
-  const uint32_t col0 = ((bid - wg0) * W + wave) * C;
+  const uint32_t col0 = (gw - wg0) * C;
   // Columns past N (the grid's last waves) are clamped for loading and never
   // stored; no early exit, so no branch separates the argument loads.
   auto clampc = [&](uint32_t c) { return c < N ? c : N - 1; };
@@ -149,24 +151,29 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
   const uint32_t c0 = clampc(col0);
   const uint32_t sbytes = C * kb * 2u;
   const uint32_t zbytes = ZPK == ZP_NONE ? 0u : C * zrow;
+  // Loads start at the dword boundary at or below the wave's block (sdel /
+  // zdel bytes earlier): the range check zeroes a whole dword that straddles
+  // the bound, which only stays harmless for dword-aligned starts (a packed
+  // zero-point row may have any byte count, so a block may start anywhere).
+  const uint32_t sdel = (c0 * kb * 2u) & 3u, zdel = (c0 * zrow) & 3u;
   u32x4 sv[MP], zv[ZPK == ZP_NONE ? 1 : MP];
   {
-    // The range check zeroes a whole dword that straddles the bound, so the
-    // bound is rounded up to 16 bytes. Tensors on this path start 16-byte
-    // aligned, so the rounded bound stays inside the aligned 16-byte block
-    // holding the tensor's last byte; the extra bytes are never used.
+    // The bound is rounded up to 16 bytes so that dwords holding the last
+    // bytes are not zeroed. Tensors on this path start 16-byte aligned, so the
+    // rounded bound stays inside the aligned 16-byte block holding the
+    // tensor's last byte; the extra bytes are never used.
     const rsrc_t rS = mk_rsrc(Sp, (N * kb * 2u + 15u) & ~15u);
 #pragma unroll
     for (int q = 0; q < MP; ++q) {
       const uint32_t o = lane * 16u + 1024u * q;
-      sv[q] = bld16_nt(rS, o < sbytes ? c0 * kb * 2u + o : kOOB, 0);  // predicated, no branch: a branch here costs a full wait
+      sv[q] = bld16_nt(rS, o < sbytes + sdel ? c0 * kb * 2u - sdel + o : kOOB, 0);  // predicated, no branch: a branch here costs a full wait
     }
     if constexpr (ZPK != ZP_NONE) {
       const rsrc_t rZ = mk_rsrc(Zp, (N * zrow + 15u) & ~15u);
 #pragma unroll
       for (int q = 0; q < MP; ++q) {
         const uint32_t o = lane * 16u + 1024u * q;
-        zv[q] = bld16_nt(rZ, o < zbytes ? c0 * zrow + o : kOOB, 0);
+        zv[q] = bld16_nt(rZ, o < zbytes + zdel ? c0 * zrow - zdel + o : kOOB, 0);
       }
     }
   }
@@ -231,8 +238,8 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
 #pragma unroll
   for (int q = 0; q < MP; ++q) {
     const uint32_t o = lane * 16u + 1024u * q;
-    if (o < sbytes) *reinterpret_cast<u32x4*>(meta + o) = sv[q];
-    if (ZPK != ZP_NONE && o < zbytes) *reinterpret_cast<u32x4*>(meta + a.zoff + o) = zv[ZPK == ZP_NONE ? 0 : q];
+    if (o < sbytes + sdel) *reinterpret_cast<u32x4*>(meta + o) = sv[q];
+    if (ZPK != ZP_NONE && o < zbytes + zdel) *reinterpret_cast<u32x4*>(meta + a.zoff + o) = zv[ZPK == ZP_NONE ? 0 : q];
   }
   // Qkv: r = A + skip in float32 and x = r * inv * gamma with
   // inv = 1 / sqrt(sum_k r^2 / K + eps) per row (packedInput,
@@ -400,8 +407,8 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
     if (col0 + i >= N) break;  // wave-uniform, after the loads are in flight
     if (i + P < C) issue(wbuf[(i + P) % (P + 1)], col0 + i + P);
     const u32x4(&w)[CPL] = wbuf[i % (P + 1)];
-    const unsigned char* ms = meta + i * kb * 2u;
-    const unsigned char* mz = meta + a.zoff + i * zrow;
+    const unsigned char* ms = meta + sdel + i * kb * 2u;
+    const unsigned char* mz = meta + a.zoff + zdel + i * zrow;
     float y[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) y[m] = 0.f;
@@ -464,7 +471,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
 
 // Host side: argument block for a geometry and C columns per wave, and the
 // workgroup's LDS bytes.
-inline uint32_t dot_wgs(int64_t N, int C, int W) { return static_cast<uint32_t>((N + C * W - 1) / (C * W)); }
+inline uint32_t dot_waves(int64_t N, int C) { return static_cast<uint32_t>((N + C - 1) / C); }
 
 inline DotArgs dot_args(const Launch& L, int C, int W, uint32_t act_bytes) {
   DotArgs a;
@@ -474,13 +481,14 @@ inline DotArgs dot_args(const Launch& L, int C, int W, uint32_t act_bytes) {
   a.gamma = L.gamma;
   a.residual = L.residual;
   a.eps = L.eps;
-  uint32_t wg = 0;
+  uint32_t wv = 0;  // waves before this projection
   for (int i = 0; i < 3; ++i) {
     const bool used = i < L.nproj;
     const Proj& P = L.p[used ? i : 0];
-    a.p[i] = DotProj{P.B, P.scales, P.zp, P.Y, static_cast<uint32_t>(P.N), used ? wg : 0xFFFFFFFFu};
-    if (used) wg += dot_wgs(P.N, C, W);
+    a.p[i] = DotProj{P.B, P.scales, P.zp, P.Y, static_cast<uint32_t>(P.N), used ? wv : 0xFFFFFFFFu};
+    if (used) wv += dot_waves(P.N, C);
   }
+  (void)W;
   a.K = static_cast<uint32_t>(L.K);
   a.kb = static_cast<uint32_t>(L.kb);
   a.rowb = static_cast<uint32_t>(L.kb * L.blob);
@@ -489,9 +497,11 @@ inline DotArgs dot_args(const Launch& L, int C, int W, uint32_t act_bytes) {
   a.M = static_cast<uint32_t>(L.M);
   a.bsl = static_cast<uint32_t>(L.bs_log2);
   const uint32_t sb = static_cast<uint32_t>(C) * a.kb * 2u;
-  a.zoff = (sb + 15u) & ~15u;
+  // + up to 3 bytes before a dword-aligned load start: scale blocks start
+  // dword-aligned when C is even, packed zero-point blocks anywhere
+  a.zoff = (sb + ((C & 1) ? 3u : 0u) + 15u) & ~15u;
   const uint32_t zb = L.zp_kind == ZP_NONE ? 0u : static_cast<uint32_t>(C) * a.zrow;
-  a.meta_bytes = (a.zoff + zb + 15u) & ~15u;
+  a.meta_bytes = (a.zoff + zb + (L.zp_kind == ZP_PACKED ? 3u : 0u) + 15u) & ~15u;
   a.act_bytes = act_bytes;
   return a;
 }
@@ -543,7 +553,8 @@ inline int dot_meta_pieces(const Launch& L) {
   const int64_t sb = c * L.kb * 2;
   const int64_t zb = L.zp_kind == ZP_PACKED ? c * L.zrow
                      : L.zp_kind == ZP_FLOAT ? c * L.kb * (L.zp_dtype == DT_F32 ? 4 : 2) : 0;
-  const int64_t mx = sb > zb ? sb : zb;
+  const int64_t sl = sb + ((c & 1) ? 3 : 0), zl = zb + (L.zp_kind == ZP_PACKED ? 3 : 0);  // as in dot_args
+  const int64_t mx = sl > zl ? sl : zl;
   return mx <= 1024 ? 1 : mx <= 1024 * DOT_META_PIECES ? DOT_META_PIECES : 0;
 }
 
@@ -557,8 +568,9 @@ inline bool dot_fits(const Launch& L) {
   const int64_t act = int64_t(mr) * cpl * 4 * 64 * 16 + int64_t(mr) * cpl * spc * 2 * 64 * 4;
   const int64_t zesz = L.zp_dtype == DT_F32 ? 4 : 2;
   const int64_t zrow = L.zp_kind == ZP_PACKED ? L.zrow : L.kb * zesz;
-  const int64_t zoff = (int64_t(c) * L.kb * 2 + 15) & ~int64_t(15);
-  const int64_t meta = (zoff + (L.zp_kind == ZP_NONE ? 0 : int64_t(c) * zrow) + 15) & ~int64_t(15);
+  const int64_t zoff = (int64_t(c) * L.kb * 2 + ((c & 1) ? 3 : 0) + 15) & ~int64_t(15);  // as in dot_args
+  const int64_t meta = (zoff + (L.zp_kind == ZP_NONE ? 0 : int64_t(c) * zrow) + (L.zp_kind == ZP_PACKED ? 3 : 0) + 15) &
+                       ~int64_t(15);
   const int64_t stat = int64_t(w) * mr * 4;
   return act + w * meta + stat <= 160 * 1024;
 }
@@ -567,8 +579,9 @@ template <int ZPK, int SPC, int CPL, int MR, int MP, int OPK, bool SK>
 inline hipError_t launch_dot6(const Launch& L, hipStream_t st) {
   constexpr int C = dot_c(MR, CPL), W = dot_w(MR, CPL);
   const DotArgs a = dot_args(L, C, W, dot_act_bytes<MR, CPL, SPC>());
-  uint32_t grid = 0;
-  for (int i = 0; i < L.nproj; ++i) grid += dot_wgs(L.p[i].N, C, W);
+  uint32_t waves = 0;
+  for (int i = 0; i < L.nproj; ++i) waves += dot_waves(L.p[i].N, C);
+  const uint32_t grid = (waves + W - 1) / W;
   const size_t lds = dot_lds_bytes(a, W);
   auto kern = k_gemv_dot<ZPK, SPC, CPL, C, dot_p(MR, CPL), MR, W, MP, OPK, SK>;
   if (lds > 64 * 1024) {
