@@ -193,6 +193,9 @@ ODD_ZP_CASES = [
     (8, 11008, 48, 128),
     (64, 864, 200, 64),
     (300, 11008, 72, 128),
+    (16, 1056, 200, 16),   # the MFMA GEMV: 33-byte rows, tile staging from odd offsets
+    (9, 2080, 77, 32),
+    (12, 1312, 100, 32),   # 21-byte rows
 ]
 
 
