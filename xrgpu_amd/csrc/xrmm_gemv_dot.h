@@ -525,10 +525,10 @@ inline size_t dot_lds_bytes(const DotArgs& a, int W) { return a.act_bytes + stat
 #define XRMM_DOT_NARROW_W 4
 #endif
 #ifndef XRMM_DOT_WIDE_C
-#define XRMM_DOT_WIDE_C 4
+#define XRMM_DOT_WIDE_C 2
 #endif
 #ifndef XRMM_DOT_WIDE_W
-#define XRMM_DOT_WIDE_W 8
+#define XRMM_DOT_WIDE_W 12
 #endif
 constexpr bool dot_wide(int mr, int cpl) { return mr >= 4 && cpl <= 4; }
 constexpr int dot_c(int mr, int cpl) { return dot_wide(mr, cpl) ? XRMM_DOT_WIDE_C : XRMM_DOT_NARROW_C; }
