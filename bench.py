@@ -266,31 +266,119 @@ def dense_fp16_reference(torch, steps: int = 30):
             "us": round(ms * 1e3, 1), "tflops": round(2 * M * K * N / (ms * 1e-3) / 1e12, 1)}
 
 
-def cpu_baseline(budget_s: float = 20.0):
-    """The NumPy oracle on this host for the decode GEMV workload (bounded)."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, runs=5, budget_s=8.0):
+    """Median wall time of ``fn`` over up to ``runs`` runs after one warm-up,
+    stopping early once ``budget_s`` is spent."""
+    import numpy as np
+    fn()
+    times, t_start = [], time.perf_counter()
+    while len(times) < runs and (not times or time.perf_counter() - t_start < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline():
+    """The NumPy oracle on this host's cores, three legs per workload (bounded).
+
+    For the decode workload (M=1 K=4096 N=14336, fp16, no zp) and the
+    CPU-oracle workload (M=1 K=N=2048, fp32, packed zp): (i) end to end
+    (unpack + float32 dequantise + float64 matvec + one rounding), (ii) the
+    matvec alone on a pre-dequantised float64 W, (iii) end to end with one BLAS
+    thread. ``value`` is leg (i) of the decode workload, the headline's
+    workload."""
     import numpy as np
     from oracle import oracle as O
     from xrgpu_amd import workloads
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+        from threadpoolctl import threadpool_info, threadpool_limits
+        info = threadpool_info()
+        threads = max([p.get("num_threads", 1) for p in info] or [1])
+        blas = sorted({f"{p.get('internal_api')} {p.get('version')}" for p in info if p.get("user_api") == "blas"})
     except Exception:
-        threads = 1
-    w = workloads.make("decode_up_m1")
-    i, at = w["inputs"], w["attrs"]
-    O.matmul_nbits(i["aT"][:, :], i["bT"][:64], i["scalesT"][:64], K=at["K"], N=64, block_size=32)  # warm
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 5 and time.perf_counter() - t_start < budget_s:
-        t0 = time.perf_counter()
-        O.matmul_nbits(i["aT"], i["bT"], i["scalesT"], K=at["K"], N=at["N"], block_size=32)
-        times.append(time.perf_counter() - t0)
-    t = float(np.median(times))
-    gbs = workloads.algorithmic_bytes(w) / t / 1e9
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": int(threads), "kind": "port",
-            "sample": f"NumPy oracle (unpack + fp32 dequant + fp64 matvec), full decode GEMV "
-                      f"M=1 K=4096 N=14336, median of {len(times)} runs, {t * 1e3:.1f} ms/call; "
-                      f"BLAS threads={threads}, host cores={len(os.sched_getaffinity(0))}"}
+        threadpool_limits, threads, blas = None, 1, []
+    legs = {}
+    for wname in ("decode_up_m1", "cpu_f32_k2048"):
+        w = workloads.make(wname)
+        i, at = w["inputs"], w["attrs"]
+        Z = i.get("zeroPointsT")
+        nbytes = workloads.algorithmic_bytes(w)
+
+        def e2e():
+            return O.matmul_nbits(i["aT"], i["bT"], i["scalesT"], Z, K=at["K"], N=at["N"], block_size=at["block_size"])
+        W = O.dequantize(i["bT"], i["scalesT"], Z, at["K"], 4, at["block_size"]).astype(np.float64)
+        x = i["aT"].astype(np.float64)
+        t1, n1 = _median_time(e2e)
+        t2, n2 = _median_time(lambda: x @ W.T)
+        if threadpool_limits is not None:
+            with threadpool_limits(limits=1):
+                t3, n3 = _median_time(e2e)
+        else:
+            t3, n3 = t1, n1
+        del W
+        legs[wname] = {"bytes": nbytes,
+                       "end_to_end": {"ms": round(t1 * 1e3, 3), "GBps": round(nbytes / t1 / 1e9, 4), "runs": n1},
+                       "matmul_only": {"ms": round(t2 * 1e3, 3), "GBps": round(nbytes / t2 / 1e9, 4), "runs": n2},
+                       "one_thread": {"ms": round(t3 * 1e3, 3), "GBps": round(nbytes / t3 / 1e9, 4), "runs": n3}}
+    d = legs["decode_up_m1"]["end_to_end"]
+    return {"value": d["GBps"], "unit": "GB/s", "cores": int(threads), "kind": "port",
+            "sample": f"NumPy oracle (unpack + fp32 dequant + fp64 matvec) on the full decode GEMV M=1 K=4096 "
+                      f"N=14336, median of {d['runs']} runs, {d['ms']} ms/call; three legs on it and on the "
+                      f"fp32 K=N=2048 workload in 'legs'",
+            "legs": legs, "blas": blas, "blas_threads": int(threads), "host_cores": len(os.sched_getaffinity(0)),
+            "cpu_model": _cpu_model()}
+
+
+def stream_ceiling(torch, ops, steps, warmup, nbytes=33_067_008, R=10):
+    """The plain read of the decode workload's bytes: R rotating buffers of
+    ``nbytes`` (330 MB, beyond the Infinity Cache), one buffer read per step
+    by xrmm_stream_read, timed like the decode leg; best of 1, 2, 4 and 8
+    loads per lane."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    bufs = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda", generator=g) for _ in range(R)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    per = {}
+    for u in (1, 2, 4, 8):
+        ms, _, _ = time_steps(torch, lambda i, u=u: ops.stream_read(bufs[i % R], loads_per_lane=u, sink=sink),
+                              steps, warmup)
+        per[u] = ms
+    best = min(per, key=per.get)
+    ms = per[best]
+    del bufs
+    torch.cuda.empty_cache()
+    return {"what": f"plain 16-byte non-temporal read of {nbytes} B (the decode GEMV's bytes), {R} rotating buffers",
+            "us": round(ms * 1e3, 3), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
+            "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "loads_per_lane": best,
+            "us_by_loads_per_lane": {str(k): round(v * 1e3, 3) for k, v in per.items()}}
+
+
+def copy_calibration():
+    """Counter calibration for rocprofv3 byte counters: five device copies of
+    256 MiB (each reads and writes exactly 268435456 bytes). Run under
+    ``rocprofv3 --pmc FETCH_SIZE`` / ``--pmc WRITE_SIZE``; the copy kernel's
+    counter values give the counter-to-bytes factors rocprof_summary uses."""
+    import torch
+    nbytes = 256 << 20
+    x = torch.ones(nbytes // 4, device="cuda")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(f"copy calibration: {nbytes} bytes read and written per dispatch", flush=True)
 
 
 def main():
@@ -301,7 +389,12 @@ def main():
     ap.add_argument("--replicas", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run the rocprofv3 byte-counter calibration copies and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: the MatMulNBits family runs on a single device here; "
               "multi-GPU sharding is a design note only.", file=sys.stderr)
@@ -318,7 +411,9 @@ def main():
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
     for name in names:
-        R = {"prefill_m2048": 2, "qmoe_mixtral_t1": 2, "gbq_embed_t2048": 8}.get(name, args.replicas)
+        # every leg rotates more weight bytes than the 256 MB Infinity Cache
+        # holds (Qkv: 24 x 13.7 MB = 328 MB)
+        R = {"prefill_m2048": 2, "qmoe_mixtral_t1": 2, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24}.get(name, args.replicas)
         w = make_replicas(torch, name, R, dev, seed=SEEDS[name])
         fn = step_fn(ops, name, w)
         steps = args.steps if name != "prefill_m2048" else max(10, args.steps // 10)
@@ -326,6 +421,7 @@ def main():
         p10, p50, p90 = per_launch_percentiles(torch, fn, min(100, steps), 5)
         wl = workloads.make(name, scale_down=1) if name == "decode_up_m1" else None
         results[name] = dict(ms=ms, eager_ms=eager_ms, wall_ms=wall_ms, p10=p10, p50=p50, p90=p90, steps=steps, replicas=R)
+        print(f"[bench] {name}: {ms * 1e3:.3f} us/step over {steps} steps", file=sys.stderr, flush=True)
         del w, fn, wl
         torch.cuda.empty_cache()
 
@@ -340,6 +436,7 @@ def main():
         return int(float(v)) if v else None
 
     out = {}
+    ceiling = stream_ceiling(torch, ops, args.steps, args.warmup) if "decode_up_m1" in results else None
     if "decode_up_m1" in results:
         r = results["decode_up_m1"]
         decode_kernel = ops.select_kernel("MatMulNBits", 1, 4096, 14336, 4, 32)
@@ -362,6 +459,8 @@ def main():
                          "frac": round(gbs / HBM_PEAK_GBS, 4),
                          "traffic": traffic_of("decode_up_m1_gemv.md", decode_kernel),
                          "kernel": decode_kernel, "bytes_per_launch": nbytes},
+            "stream_ceiling": ceiling,
+            "decode_over_stream_ceiling": round(ceiling["us"] / (r["ms"] * 1e3), 4),
         }
     if "prefill_m2048" in results:
         r = results["prefill_m2048"]
@@ -379,7 +478,8 @@ def main():
             r = results[name]
             gbs = nbytes / (r["ms"] * 1e-3) / 1e9
             out[name] = {"us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-                         "bytes_per_launch": nbytes}
+                         "bytes_per_launch": nbytes, "replicas": r["replicas"],
+                         "rotated_bytes": nbytes * r["replicas"]}
     if "qmoe_mixtral_t1" in results:
         r, q = results["qmoe_mixtral_t1"], QMOE
         nbytes = qmoe_algorithmic_bytes(**q)
@@ -414,6 +514,7 @@ def main():
             "us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
             "bytes_per_launch": nbytes}
     if not args.no_cpu:
+        print("[bench] CPU baseline (NumPy oracle)", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
 

@@ -309,6 +309,15 @@ int xrmm_matmul_nbits_int8a(const void* A, const void* B, const void* scales, co
                             int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size, int32_t dtype,
                             void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Measurement (no counterpart in the reference, which publishes no throughput
+ * for this path): read `bytes` (a multiple of 16) at 16-byte aligned `src`
+ * once with 16-byte non-temporal loads, `loads_per_lane` (1, 2, 4 or 8) per
+ * lane issued back to back, and write nothing to the 4-byte `sink` in
+ * practice. The plain read rate of a decode GEMV's bytes, which its time is
+ * compared with. */
+int xrmm_stream_read(const void* src, uint64_t bytes, void* sink, int32_t loads_per_lane, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

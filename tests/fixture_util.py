@@ -5,9 +5,10 @@ Generators follow the rules of the reference harness
 ``cycle`` (np.resize of the list) and ``linspace`` (float64 inclusive then one
 cast). The upstream ``fillFloat32`` generator is not in the reference either
 (tests/test_upstream_operator_fixtures.py:52-58 treats it as unsupported);
-when ``substitute`` is set, such inputs get seeded N(0,1)*scale values so the
-case's shape, attributes and other inputs are still exercised (those cases
-carry no explicit outputs, so the oracle supplies the expectation).
+when ``substitute`` is set, such inputs get seeded ``offset + scale*U(-1,1)``
+values (the generator's own offset and scale) so the case's shape, attributes
+and other inputs are still exercised (those cases carry no explicit outputs,
+so the oracle supplies the expectation).
 """
 from __future__ import annotations
 
@@ -56,7 +57,10 @@ def materialize(spec, seed_key: str = "", substitute: bool = False):
         if dtype == np.uint8:
             arr = rng.integers(0, 256, count, dtype=np.uint8)
         else:
-            arr = (rng.standard_normal(count) * float(data.get("scale", 1.0))).astype(dtype)
+            # bounded like the upstream sin/cos product it stands in for:
+            # offset + scale * u with |u| <= 1
+            u = rng.uniform(-1.0, 1.0, count)
+            arr = (float(data.get("offset", 0.0)) + float(data.get("scale", 1.0)) * u).astype(dtype)
     else:
         raise ValueError("unsupported generator " + str(kind))
     return arr.reshape(shape)

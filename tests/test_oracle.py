@@ -228,6 +228,63 @@ def test_activation_closed_forms():
     assert O.fused_activation(np.array([-1000.0]), 2)[0] == 0.0
 
 
+def _reference_erf(x):
+    """The reference shader's own erf (complex_math.glsl:185-199): an odd Taylor
+    series below 0.5, sign(x) above 6, Abramowitz and Stegun 7.1.26 between
+    (absolute error <= 1.5e-7). An approximation independent of scipy's erf,
+    so agreement pins the oracle's gelu to the erf form the shader evaluates."""
+    x = np.asarray(x, dtype=np.float64)
+    t = np.abs(x)
+    z = x * x
+    p = 1.0 + z * (-1 / 3 + z * (1 / 10 + z * (-1 / 42 + z * (1 / 216 + z * (-1 / 1320 + z * (1 / 9360 - z / 75600))))))
+    small = 1.1283791670955126 * x * p
+    a = 1.0 / (1.0 + 0.3275911 * t)
+    q = (((((1.061405429 * a - 1.453152027) * a) + 1.421413741) * a - 0.284496736) * a + 0.254829592) * a
+    y = np.sign(x) * (1.0 - q * np.exp(-t * t))
+    return np.where(t < 0.5, small, np.where(t > 6.0, np.sign(x), y))
+
+
+def test_gelu_is_the_erf_form():
+    """fused kind 3 for opcode 1027 is 0.5 x (1 + erf(x / sqrt 2))
+    (complex_kernel.glsl:41-44), not the tanh form the other opcodes use."""
+    g = lambda v: float(O.fused_activation(np.array([v]), 3)[0])  # noqa: E731
+    # x * Phi(x) at +-1: Phi(1) = 0.8413447460685429 (standard normal CDF)
+    assert abs(g(1.0) - 0.8413447460685429) < 1e-15
+    assert abs(g(-1.0) - (-0.15865525393145707)) < 1e-15
+    assert g(0.0) == 0.0
+    # erf is odd, so gelu(x) - gelu(-x) = x exactly in real arithmetic
+    x = np.linspace(-8.0, 8.0, 321)
+    d = O.fused_activation(x, 3) - O.fused_activation(-x, 3)
+    assert np.allclose(d, x, rtol=0, atol=1e-14)
+    # far from the tanh approximation where the two forms part (|x| near 2.5-3)
+    tanh_form = 0.5 * x * (1 + np.tanh(0.7978845608028654 * (x + 0.044715 * x ** 3)))
+    for v in (2.5, -2.5, 3.0, -3.0):
+        i = int(np.argmin(np.abs(x - v)))
+        assert abs(O.fused_activation(x[i:i + 1], 3)[0] - tanh_form[i]) > 1e-4
+    # and within the shader's own erf approximation's bound everywhere
+    ref = 0.5 * x * (1.0 + _reference_erf(x * 0.7071067811865475))
+    assert np.max(np.abs(O.fused_activation(x, 3) - ref) / np.maximum(np.abs(x), 1.0)) < 2e-7
+
+
+def test_gelu_serial_float32_order_matches():
+    """The serial float32 restatement (erff) of the gelu Mlp path agrees with
+    the float64 oracle within the fp32 bar."""
+    rng = np.random.default_rng(33)
+    M, K, N, bs = 3, 96, 7, 32
+    kb = O.k_blocks(K, bs)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    gB, uB = (rng.integers(0, 256, (N, kb, bs // 2), dtype=np.uint8) for _ in range(2))
+    gS, uS = (rng.uniform(0.01, 0.2, (N, kb)).astype(np.float32) for _ in range(2))
+    gb = rng.standard_normal(N).astype(np.float32)
+    y, _ = O.matmul_nbits_mlp(A, gB, gS, uB, uS, K=K, N=N, gate_bias=gb, block_size=bs, activation="gelu")
+    ys, _ = serial.matmul_nbits_mlp(A, gB, gS, uB, uS, K=K, N=N, gate_bias=gb, block_size=bs, act=3)
+    ok, err, lim = O.tolerance_ok(ys, y, np.float32)
+    assert ok, (err, lim)
+    # the gelu result differs from the silu one (the activation kind reaches the epilogue)
+    ysilu, _ = O.matmul_nbits_mlp(A, gB, gS, uB, uS, K=K, N=N, gate_bias=gb, block_size=bs, activation="silu")
+    assert not O.tolerance_ok(ysilu, y, np.float32)[0]
+
+
 @pytest.mark.parametrize("bits,bs,K,N,M,zp", [(4, 32, 70, 5, 3, "packed"), (2, 16, 33, 4, 2, "float"),
                                              (8, 16, 40, 3, 1, "none"), (4, 128, 256, 9, 2, "float")])
 def test_numpy_oracle_matches_serial_float32_order(bits, bs, K, N, M, zp):
@@ -264,3 +321,54 @@ def test_tolerance_rule():
     assert O.tolerance_ok(e + np.float16(0.015), e, np.float16)[0]
     assert not O.tolerance_ok(e + np.float16(0.03), e, np.float16)[0]
     assert not O.tolerance_ok(np.array([np.nan, 0, 0]), np.zeros(3), np.float16)[0]
+
+
+def test_tolerance_rule_nonfinite():
+    inf, nan = np.inf, np.nan
+    e = np.array([inf, -inf, nan, 1.0])
+    assert O.tolerance_ok(np.array([inf, -inf, nan, 1.0]), e, np.float32)[0]
+    assert not O.tolerance_ok(np.array([-inf, -inf, nan, 1.0]), e, np.float32)[0]  # sign of Inf
+    assert not O.tolerance_ok(np.array([inf, -inf, 0.0, 1.0]), e, np.float32)[0]   # NaN expected
+    assert not O.tolerance_ok(np.array([inf, nan, nan, 1.0]), e, np.float32)[0]    # Inf expected
+
+
+def nonfinite_activations(rng, M, K, dtype):
+    """Rows with +Inf, -Inf, both (columns may cancel to NaN), NaN, then finite rows."""
+    A = rng.standard_normal((M, K)).astype(dtype)
+    pos = rng.permutation(K)[:4]
+    if M > 0:
+        A[0, pos[0]] = np.inf
+    if M > 1:
+        A[1, pos[1]] = -np.inf
+    if M > 2:
+        A[2, pos[2]], A[2, pos[3]] = np.inf, -np.inf
+    if M > 3:
+        A[3, pos[0]] = np.nan
+    return A
+
+
+@pytest.mark.parametrize("zp", ["none", "packed", "float"])
+def test_nonfinite_policy_matches_serial_order(zp):
+    """+-Inf / NaN activations: the float64 oracle gives the same non-finite
+    pattern (NaN, +Inf, -Inf per element) as the reference's serial float32
+    loop ``sum += a * W`` (complex_kernel.glsl:83) restated in C, and the same
+    finite values within the fp32 bar. Codes equal to the zero point make
+    W = 0, so Inf * 0 = NaN cases occur."""
+    rng = np.random.default_rng(71)
+    M, K, N, bs = 5, 96, 40, 32
+    kb = O.k_blocks(K, bs)
+    A = nonfinite_activations(rng, M, K, np.float32)
+    B = rng.integers(0, 256, (N, kb, bs // 2), dtype=np.uint8)
+    S = rng.uniform(0.01, 0.2, (N, kb)).astype(np.float32)
+    Z = None
+    if zp == "packed":
+        Z = rng.integers(0, 256, (N, O.packed_zp_bytes(kb, 4)), dtype=np.uint8)
+    elif zp == "float":
+        Z = rng.integers(0, 16, (N, kb)).astype(np.float32)
+    y = O.matmul_nbits(A, B, S, Z, K=K, N=N, block_size=bs)
+    ys = serial.matmul_nbits(A, B, S, Z, K=K, N=N, block_size=bs)
+    for f in (np.isnan, np.isposinf, np.isneginf):
+        assert np.array_equal(f(y), f(ys))
+    assert np.isnan(y).any() and np.isposinf(y).any() and np.isneginf(y).any()
+    assert np.all(np.isfinite(y[4:]))
+    assert O.tolerance_ok(ys, y, np.float32)[0]

@@ -40,6 +40,7 @@ UNITS = [
     ("xrmm_moe.hip", [], "moe.o"),
     ("xrmm_quant.hip", [], "quant.o"),
     ("xrmm_int8a.hip", [], "int8a.o"),
+    ("xrmm_probe.hip", [], "probe.o"),
     ("xrmm_api.cpp", [], "api.o"),
     ("xrmm_operator.cpp", [], "operator.o"),
 ]

@@ -65,6 +65,7 @@ int geometry(xrmm::Launch& L, int op, int64_t M, int64_t K, int32_t bits, int32_
   L.bs_log2 = -1;
   for (int i = 0; i < 31; ++i)
     if (block_size == (1 << i)) L.bs_log2 = i;
+  L.exact_weights = xrmm::ExactWeightsScope::active();
   return XRMM_OK;
 }
 
@@ -82,6 +83,14 @@ int set_status(int code, const std::string& msg) {
   g_error = code == XRMM_OK ? std::string() : msg;
   return code;
 }
+
+namespace {
+thread_local bool g_exact_weights = false;
+}
+
+ExactWeightsScope::ExactWeightsScope(bool on) : prev_(g_exact_weights) { g_exact_weights = on; }
+ExactWeightsScope::~ExactWeightsScope() { g_exact_weights = prev_; }
+bool ExactWeightsScope::active() { return g_exact_weights; }
 }  // namespace xrmm
 
 extern "C" {

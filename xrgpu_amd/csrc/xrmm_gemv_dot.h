@@ -320,6 +320,10 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
       }
     }
   }
+  // Whether any staged activation is +-Inf or NaN. The per-chunk sums below
+  // are finite exactly when all 32 activations of the chunk are (|sum| <=
+  // 32 * 65504 * 1032, far below FLT_MAX), so they double as the detector.
+  bool nonfinite = false;
   {
     const f16x2 c1024 = {static_cast<f16>(1024.f), static_cast<f16>(1024.f)};
     const f16x2 c64 = {static_cast<f16>(64.f), static_cast<f16>(64.f)};
@@ -355,13 +359,68 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
             if constexpr (ZPK != ZP_NONE) t[e & 1] = __builtin_amdgcn_fdot2(pr[e], c1, t[e & 1], false);
           }
           float* sums = reinterpret_cast<float*>(smem + PAIRS) + (((m * CPL + j) * SPC + h) * 2) * 64 + l;
-          sums[0] = -((b[0] + b[1]) + (b[2] + b[3]));
+          const float nb = -((b[0] + b[1]) + (b[2] + b[3]));
+          nonfinite |= !__builtin_isfinite(nb);
+          sums[0] = nb;
           sums[64] = t[0] + t[1];
         }
       }
     }
   }
+  __shared__ uint32_t wave_nonfinite[W];
+  {
+    const bool any = __builtin_amdgcn_ballot_w64(nonfinite) != 0;
+    if (lane == 0) wave_nonfinite[wave] = any ? 1u : 0u;
+  }
   __syncthreads();
+  uint32_t special = 0;
+#pragma unroll
+  for (int w = 0; w < W; ++w) special |= wave_nonfinite[w];
+
+  if (special != 0) {
+    // Some staged activation is +-Inf or NaN: the folded-bias sums above would
+    // turn an infinite activation into Inf - Inf. The workgroup takes the
+    // reference's per-element form instead (complex_kernel.glsl:80,83):
+    // W = (code - z) * scale in float32, then sum += x * W, so +-Inf * W gives
+    // +-Inf (NaN where W is 0) exactly as the serial shader does. Activations
+    // come from the staged pairs (A, or the normalised Qkv input).
+    const f16* S16 = static_cast<const f16*>(Sp);
+    f16* Yo = static_cast<f16*>(Yp);
+    const f16* bo = QKV ? nullptr : static_cast<const f16*>(a.bias);
+    for (int i = 0; i < C; ++i) {
+      const uint32_t col = col0 + static_cast<uint32_t>(i);
+      if (col >= N) break;
+      float y[MR];
+#pragma unroll
+      for (int m = 0; m < MR; ++m) y[m] = 0.f;
+      for (uint32_t k = lane; k < K; k += 64) {
+        const uint32_t b = k >> a.bsl;
+        const uint32_t byte = Bp[col * rowb + (k >> 1)];  // 4-bit: byte k/2 of the row, low nibble first
+        const float code = static_cast<float>((byte >> ((k & 1u) * 4u)) & 15u);
+        float z = 8.f;
+        if constexpr (ZPK == ZP_PACKED) {
+          z = static_cast<float>((static_cast<const uint8_t*>(Zp)[col * zrow + (b >> 1)] >> ((b & 1u) * 4u)) & 15u);
+        } else if constexpr (ZPK == ZP_FLOAT) {
+          z = a.zesz == 4 ? static_cast<const float*>(Zp)[col * kb + b]
+                          : static_cast<float>(static_cast<const f16*>(Zp)[col * kb + b]);
+        }
+        const float w = (code - z) * static_cast<float>(S16[col * kb + b]);
+        const uint32_t ch = k >> 5, g = (k >> 3) & 3u, e = k & 7u;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const f16* xp = reinterpret_cast<const f16*>(
+              smem + ((((m * CPL + (ch >> 6)) * 4 + g) * 64 + (ch & 63u)) * 16u) + (e & 3u) * 4u + (e >> 2) * 2u);
+          y[m] = __builtin_fmaf(static_cast<float>(*xp), w, y[m]);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const float tot = wave_total(y[m]);
+        if (lane == 0 && m < M) Yo[static_cast<uint32_t>(m) * N + col] = static_cast<f16>(tot + (bo ? static_cast<float>(bo[col]) : 0.f));
+      }
+    }
+    return;
+  }
 
   // ---- this lane's activation pairs and constants, into registers
   f16x2 ap[MR][CPL][16];
@@ -510,9 +569,10 @@ inline size_t dot_lds_bytes(const DotArgs& a, int W) { return a.act_bytes + stat
 
 // Launch shape of the dot GEMV: columns per wave (C) and waves per workgroup
 // (W), one column prefetched. Measured: 2 x 4 on the one-row decode workload;
-// 4 x 8 with four rows, where the activation staging is four times larger and
-// fewer, larger workgroups amortise it (Qkv GQA decode 14.0 -> 11.5 us), as
-// long as the staging leaves LDS room for eight waves' scale blocks.
+// 2 x 12 with four rows (wide), where the activation staging is four times
+// larger and fewer, larger workgroups amortise it; each wave picks its Qkv
+// projection from its global wave index, so the Qkv GQA decode workload fills
+// exactly 256 workgroups (10.67 us against 10.95 us for 8 waves x 4 columns).
 // The XRMM_DOT_* macros override the shape for tuning builds; every
 // translation unit of one library must see the same values.
 #ifndef XRMM_DOT_P
@@ -559,8 +619,9 @@ inline int dot_meta_pieces(const Launch& L) {
 }
 
 // Whether the dot GEMV applies: rows, chunk rounds and scale blocks within its
-// instantiations, and the workgroup's LDS (staged activations, eight or four
-// waves' scale / zero-point slices, the Qkv row-sum scratch) within 160 KB.
+// instantiations, and the workgroup's LDS (staged activations, W waves' scale /
+// zero-point slices, the Qkv row-sum scratch and the per-wave non-finite flags)
+// within 160 KB.
 inline bool dot_fits(const Launch& L) {
   const int mr = dot_mr(L.M), cpl = dot_cpl(L);
   if (mr == 0 || cpl == 0 || dot_meta_pieces(L) == 0) return false;
@@ -571,7 +632,7 @@ inline bool dot_fits(const Launch& L) {
   const int64_t zoff = (int64_t(c) * L.kb * 2 + ((c & 1) ? 3 : 0) + 15) & ~int64_t(15);  // as in dot_args
   const int64_t meta = (zoff + (L.zp_kind == ZP_NONE ? 0 : int64_t(c) * zrow) + (L.zp_kind == ZP_PACKED ? 3 : 0) + 15) &
                        ~int64_t(15);
-  const int64_t stat = int64_t(w) * mr * 4;
+  const int64_t stat = int64_t(w) * mr * 4 + int64_t(w) * 4;  // Qkv row sums, per-wave non-finite flags
   return act + w * meta + stat <= 160 * 1024;
 }
 

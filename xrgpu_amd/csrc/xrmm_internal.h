@@ -40,6 +40,26 @@ struct Launch {
   void* residual;        // nullable
   float eps;
   Proj p[3];
+  // Only kernels that keep every dequantised weight in float32 (the dot GEMV
+  // applies scales to float32 block sums; the generic kernel uses the
+  // reference formula): set when a binary16 weight (code - z) * scale could
+  // leave the binary16 range.
+  bool exact_weights;
+};
+
+// While alive on the calling thread, launches described on that thread set
+// Launch::exact_weights (the request lifecycle turns it on at run time for
+// weights whose scales it has checked on the host).
+class ExactWeightsScope {
+ public:
+  explicit ExactWeightsScope(bool on);
+  ~ExactWeightsScope();
+  ExactWeightsScope(const ExactWeightsScope&) = delete;
+  ExactWeightsScope& operator=(const ExactWeightsScope&) = delete;
+  static bool active();
+
+ private:
+  bool prev_;
 };
 
 // Kernel families the dispatcher chooses between.

@@ -326,6 +326,14 @@ static bool gemm_big_fills(const Launch& L) {
 inline int64_t split_k_min_rows(int op) { return op == OP_MATMUL ? 3 : op == OP_QKV ? 5 : 1; }
 
 Kernel select_kernel(const Launch& L) {
+  if (L.exact_weights) {
+    // the dot GEMV scales float32 block sums; every other fast kernel stages
+    // binary16 weights
+    if (q4_fast_ok(L) && fits_i32(L) && (L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 &&
+        L.M < split_k_min_rows(L.op) && dot_fits(L))
+      return K_GEMV_DOT;
+    return K_GENERIC;
+  }
   if (q4_fast_ok(L) && fits_i32(L)) {
     if (L.M >= split_k_min_rows(L.op) && sk_fits(L)) return K_GEMV_SK;
     if ((L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 && dot_fits(L)) return K_GEMV_DOT;

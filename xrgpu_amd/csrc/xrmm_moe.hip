@@ -443,15 +443,17 @@ __global__ __launch_bounds__(MOE_T) void k_moe_gemv(MoeArgs a, int gpw, int tile
 
   if constexpr (fc2) {
     if (combine) {
-      // The partials went out as device-coherent stores; once every one of
-      // them has completed (s_waitcnt 0 in each thread, then the barrier) the
-      // arrival is counted, and the last of the token's k * ks workgroups on
-      // this row tile reads them back with device-coherent loads and sums
-      // them. No cache-wide write-back or invalidation is needed.
+      // The partials went out as device-coherent stores. Every thread waits
+      // for its stores (s_waitcnt 0), the barrier orders them before thread
+      // 0's arrival count, and the count is an agent-scope acquire-release:
+      // its release publishes the workgroup's partials, its acquire (in the
+      // last of the token's k * ks workgroups on this row tile) orders the
+      // device-coherent loads that read them back after every other
+      // workgroup's release.
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (tid == 0)
-        s_last = __hip_atomic_fetch_add(a.cnt + t * tiles2 + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        s_last = __hip_atomic_fetch_add(a.cnt + t * tiles2 + tile, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
                  static_cast<uint32_t>(a.k * ks - 1);
       __syncthreads();
       if (s_last) {

@@ -565,6 +565,41 @@ void hip_check(hipError_t e, const char* where) {
   if (e != hipSuccess) throw Device(std::string(where) + ": " + hipGetErrorString(e));
 }
 
+// Whether a binary16 weight (code - z) * scale of a float16 request could leave
+// the binary16 range (|w| > 65504), where the reference's float32 weight
+// (complex_kernel.glsl:80) stays finite. The fast kernels that stage binary16
+// weights would saturate such weights to +-Inf, so the run then uses only
+// kernels that keep weights in float32.
+bool weights_need_float32(const Plan& p) {
+  const int op = p.contract->op;
+  if (p.dtype != XRMM_F16 || (op != xrmm::OP_MATMUL && op != xrmm::OP_QKV && op != xrmm::OP_MLP)) return false;
+  static const char* const kMatMul[][2] = {{"scalesT", "zeroPointsT"}};
+  static const char* const kQkv[][2] = {{"qScalesT", "qZeroPointsT"}, {"kScalesT", "kZeroPointsT"}, {"vScalesT", "vZeroPointsT"}};
+  static const char* const kMlp[][2] = {{"gateScalesT", "gateZeroPointsT"}, {"upScalesT", "upZeroPointsT"}};
+  const char* const(*ports)[2] = op == xrmm::OP_MATMUL ? kMatMul : op == xrmm::OP_QKV ? kQkv : kMlp;
+  const int nports = op == xrmm::OP_MATMUL ? 1 : op == xrmm::OP_QKV ? 3 : 2;
+  const double code_max = double((1 << p.bits) - 1);
+  auto max_abs = [](const Tensor& t) {
+    const uint64_t n = numel(t.shape);
+    std::vector<float> v(n);
+    convert(t.data, t.storage, reinterpret_cast<uint8_t*>(v.data()), XRMM_F32, n, false);
+    double m = 0;
+    for (float x : v)
+      if (std::fabs(double(x)) > m) m = std::fabs(double(x));  // NaN compares false: a NaN weight is NaN either way
+    return m;
+  };
+  for (int i = 0; i < nports; ++i) {
+    const Tensor* s = p.get(ports[i][0]);
+    if (!s || !numel(s->shape)) continue;
+    const Tensor* z = p.get(ports[i][1]);
+    double zdiff = double(1 << (p.bits - 1));  // implicit midpoint
+    if (z && z->dtype == XRMM_U8) zdiff = code_max;
+    else if (z) zdiff = max_abs(*z) + code_max;
+    if (max_abs(*s) * zdiff > 65504.0) return true;
+  }
+  return false;
+}
+
 }  // namespace
 
 struct xrmm_op {
@@ -580,6 +615,7 @@ struct xrmm_op {
   void* workspace = nullptr;            // QMoE workspace / GatherBlockQuantized status word
   uint64_t workspace_bytes = 0;
   bool closed = false, executed = false, poisoned = false, has_gpu = false;
+  bool exact_weights = false;  // weights_need_float32 at prepare
   double execution_ms = 0, gpu_ms = 0;
   std::string kernel, device_name, info_json;
 
@@ -614,6 +650,7 @@ struct xrmm_op {
 
   // Enqueue the operator through the zero-copy entry points.
   int enqueue() {
+    const xrmm::ExactWeightsScope exact(exact_weights);
     const Plan& p = plan;
     void* s = stream;
     const int32_t zd = p.zp_dtype;
@@ -778,6 +815,8 @@ int xrmm_prepare(const xrmm_request* request, const xrmm_options* options, xrmm_
       g.bs = p.block_size;
       k = xrmm::gbq_fast_ok(g) ? "gbq_words" : "gbq_scalar";
     } else {
+      op->exact_weights = weights_need_float32(p);
+      const xrmm::ExactWeightsScope exact(op->exact_weights);
       const int64_t n0 = code == xrmm::OP_QKV ? p.Nq : p.N;
       k = xrmm_select_kernel(code, p.M, p.K, n0, p.bits, p.block_size, p.dtype, zk);
     }

@@ -78,6 +78,33 @@ def _check_weights(B, S, Z, N, K, bits, bs, dtype, name=""):
             raise nat.XrmmInvalid(f"{name}zero points must have shape {list(want)}, got {tuple(Z.shape)}")
 
 
+def _check_out(out, shape, dtype, name="out"):
+    """A caller-supplied output must match what the kernels write through its pointer."""
+    if out is not None and (out.dtype != dtype or tuple(out.shape) != tuple(shape)):
+        raise nat.XrmmInvalid(f"{name} must be {dtype} {list(shape)}, got {out.dtype} {tuple(out.shape)}")
+
+
+def _check_aux(t, shape, dtype, name):
+    """skip / normScale / biases: the kernels read them with A's dtype and the given element count."""
+    if t is not None and (t.dtype != dtype or t.numel() != _numel(shape) or (len(shape) == 1 and t.dim() != 1)):
+        raise nat.XrmmInvalid(f"{name} must be {dtype} with shape {list(shape)}, got {t.dtype} {tuple(t.shape)}")
+
+
+def _numel(shape):
+    n = 1
+    for d in shape:
+        n *= int(d)
+    return n
+
+
+def _one_zp_dtype(zps, what):
+    present = [z for z in zps if z is not None]
+    zdt = _zp_dtype(present[0]) if present else nat.UNSPECIFIED
+    if any(_zp_dtype(z) != zdt for z in present):
+        raise nat.XrmmInvalid(f"zero points of the {what} projections must share a dtype")
+    return zdt
+
+
 def matmul_nbits(A, B, scales, zero_points=None, bias=None, *, K=None, N=None, bits=4,
                  block_size=32, out=None, stream=None):
     """com.microsoft.MatMulNBits on the GPU. Returns Y ``A.shape[:-1] + [N]``."""
@@ -85,11 +112,12 @@ def matmul_nbits(A, B, scales, zero_points=None, bias=None, *, K=None, N=None, b
     N = int(N if N is not None else B.shape[0])
     if A.shape[-1] != K:
         raise nat.XrmmInvalid("A's last dimension must equal K")
-    _check_dev(A, B, scales, zero_points, bias, out)
     _check_weights(B, scales, zero_points, N, K, bits, block_size, A.dtype)
     if bias is not None and (bias.dtype != A.dtype or tuple(bias.shape) != (N,)):
         raise nat.XrmmInvalid("bias must be [N] of A's dtype")
     M = A.numel() // K
+    _check_out(out, tuple(A.shape[:-1]) + (N,), A.dtype)
+    _check_dev(A, B, scales, zero_points, bias, out)
     if out is None:
         out = torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
     nat.check(nat.lib().xrmm_matmul_nbits(_ptr(A), _ptr(B), _ptr(scales), _ptr(zero_points),
@@ -107,15 +135,18 @@ def matmul_nbits_qkv(A, q_B, q_scales, k_B, k_scales, v_B, v_scales, *, norm_sca
     Nq = int(Nq if Nq is not None else q_B.shape[0])
     Nkv = int(Nkv if Nkv is not None else k_B.shape[0])
     zps = (q_zero_points, k_zero_points, v_zero_points)
-    _check_dev(A, skip, norm_scale, q_B, q_scales, k_B, k_scales, v_B, v_scales, *zps)
     for (Bm, S, Z, n, nm) in ((q_B, q_scales, zps[0], Nq, "q_"), (k_B, k_scales, zps[1], Nkv, "k_"),
                               (v_B, v_scales, zps[2], Nkv, "v_")):
         _check_weights(Bm, S, Z, n, K, bits, block_size, A.dtype, nm)
-    present = [z for z in zps if z is not None]
-    zdt = _zp_dtype(present[0]) if present else nat.UNSPECIFIED
-    if any(_zp_dtype(z) != zdt for z in present):
-        raise nat.XrmmInvalid("zero points of the three projections must share a dtype")
+    zdt = _one_zp_dtype(zps, "three")
+    if A.shape[-1] != K:
+        raise nat.XrmmInvalid("A's last dimension must equal K")
     M = A.numel() // K
+    _check_aux(skip, (M, K), A.dtype, "skip")
+    if norm_scale is None:
+        raise nat.XrmmInvalid("Missing complex input: normScaleT")
+    _check_aux(norm_scale, (K,), A.dtype, "norm_scale")
+    _check_dev(A, skip, norm_scale, q_B, q_scales, k_B, k_scales, v_B, v_scales, *zps)
     lead = tuple(A.shape[:-1])
     Q = torch.empty(lead + (Nq,), dtype=A.dtype, device=A.device)
     Ko = torch.empty(lead + (Nkv,), dtype=A.dtype, device=A.device)
@@ -137,13 +168,18 @@ def matmul_nbits_mlp(A, gate_B, gate_scales, up_B, up_scales, *, skip=None, norm
     N = int(N if N is not None else gate_B.shape[0])
     if activation not in nat.ACT:
         raise nat.XrmmInvalid("Unknown fused activation: " + str(activation))
-    _check_dev(A, skip, norm_scale, gate_B, gate_scales, up_B, up_scales, gate_bias, up_bias,
-               gate_zero_points, up_zero_points)
     _check_weights(gate_B, gate_scales, gate_zero_points, N, K, bits, block_size, A.dtype, "gate_")
     _check_weights(up_B, up_scales, up_zero_points, N, K, bits, block_size, A.dtype, "up_")
-    present = [z for z in (gate_zero_points, up_zero_points) if z is not None]
-    zdt = _zp_dtype(present[0]) if present else nat.UNSPECIFIED
+    zdt = _one_zp_dtype((gate_zero_points, up_zero_points), "gate and up")
+    if A.shape[-1] != K:
+        raise nat.XrmmInvalid("A's last dimension must equal K")
     M = A.numel() // K
+    _check_aux(skip, (M, K), A.dtype, "skip")
+    _check_aux(norm_scale, (K,), A.dtype, "norm_scale")
+    _check_aux(gate_bias, (N,), A.dtype, "gate_bias")
+    _check_aux(up_bias, (N,), A.dtype, "up_bias")
+    _check_dev(A, skip, norm_scale, gate_B, gate_scales, up_B, up_scales, gate_bias, up_bias,
+               gate_zero_points, up_zero_points)
     Y = torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
     R = torch.empty_like(A) if want_residual else None
     nat.check(nat.lib().xrmm_matmul_nbits_mlp(
@@ -244,7 +280,8 @@ def gather_block_quantized(data, indices, scales, zero_points=None, *, bits=4, b
     stream and raises ``XrmmError`` ("GPU operator contract validation failed:
     code 55") as the reference's run does.
     """
-    _check_dev(data, indices, scales, zero_points, status)
+    if status is not None and (status.dtype not in (torch.int32, torch.uint32) or status.numel() < 1):
+        raise nat.XrmmInvalid("status must be an int32 or uint32 tensor of at least one element")
     if data.dtype != torch.uint8 or (zero_points is not None and zero_points.dtype != torch.uint8):
         raise nat.XrmmInvalid("Logical dtype outside frozen contract: dataT")
     if scales.dtype != torch.float32:
@@ -260,6 +297,7 @@ def gather_block_quantized(data, indices, scales, zero_points=None, *, bits=4, b
         raise nat.XrmmInvalid("Unsupported GatherBlockQuantized geometry")
     if zero_points is not None and tuple(zero_points.shape) != (rows, (blocks * bits + 7) // 8):
         raise nat.XrmmInvalid("Unsupported GatherBlockQuantized geometry")
+    _check_dev(data, indices, scales, zero_points, status)
     data, indices, scales = data.contiguous(), indices.contiguous(), scales.contiguous()
     out = torch.empty((int(indices.shape[0]), width), dtype=torch.float32, device=data.device)
     if status is None:
@@ -280,7 +318,6 @@ def matmul_bnb4(A, B, absmax, *, K, N, block_size=32, quant_type=1, trans_b=1, o
     A ``[M, K]`` float32/float16, B uint8 ``ceil(N*K/2)`` bytes (even flat index
     in the high nibble), absmax ``ceil(N*K/block_size)`` in A's dtype.
     """
-    _check_dev(A, B, absmax, out)
     if A.dtype not in _T1 or absmax.dtype != A.dtype:
         raise nat.XrmmInvalid("Logical dtype outside frozen contract: aT")
     if B.dtype != torch.uint8:
@@ -289,8 +326,10 @@ def matmul_bnb4(A, B, absmax, *, K, N, block_size=32, quant_type=1, trans_b=1, o
         raise nat.XrmmInvalid("Invalid packed matmul geometry")
     if B.numel() < (N * K + 1) // 2 or absmax.numel() < (N * K + block_size - 1) // max(block_size, 1):
         raise nat.XrmmInvalid("Invalid packed matmul geometry")
-    A, B, absmax = A.contiguous(), B.contiguous(), absmax.contiguous()
     M = int(A.shape[0])
+    _check_out(out, (M, N), A.dtype)
+    _check_dev(A, B, absmax, out)
+    A, B, absmax = A.contiguous(), B.contiguous(), absmax.contiguous()
     Y = out if out is not None else torch.empty((M, N), dtype=A.dtype, device=A.device)
     nat.check(nat.lib().xrmm_matmul_bnb4(_ptr(A), _ptr(B), _ptr(absmax), _ptr(Y), M, K, N, int(block_size),
                                          int(quant_type), int(trans_b), _T1[A.dtype], _stream(stream)))
@@ -310,14 +349,19 @@ def matmul_nbits_int8a(A, B, scales, zero_points=None, bias=None, *, K, N, bits=
     accuracy_level 4, not the reference's float32 arithmetic): rows of A are
     quantized per 128 (max|a| / 127) and multiplied with the 4-bit weights as
     exact int32 dot products. Packed uint8 zero points only."""
-    _check_dev(A, B, scales, zero_points, bias, out, workspace)
     if A.dtype not in _T1 or scales.dtype != A.dtype:
         raise nat.XrmmInvalid("T1 must be float32 or float16")
     if zero_points is not None and zero_points.dtype != torch.uint8:
         raise nat.XrmmInvalid("int8-activation path: zero points must be absent or packed uint8")
     _check_weights(B, scales, zero_points, N, K, bits, block_size, scales.dtype)
+    if A.shape[-1] != K:
+        raise nat.XrmmInvalid("A's last dimension must equal K")
+    if bias is not None and (bias.dtype != A.dtype or tuple(bias.shape) != (N,)):
+        raise nat.XrmmInvalid("bias must be [N] of A's dtype")
     A2 = A.reshape(-1, K).contiguous()
     M = int(A2.shape[0])
+    _check_out(out, tuple(A.shape[:-1]) + (N,), A.dtype)
+    _check_dev(A, B, scales, zero_points, bias, out, workspace)
     Y = out if out is not None else torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
     need = int(nat.lib().xrmm_matmul_nbits_int8a_workspace_bytes(M, K))
     if need < 0:
@@ -337,3 +381,14 @@ def int8a_workspace_bytes(M, K) -> int:
     if n < 0:
         raise nat.XrmmInvalid("int8-activation path: K must be a positive multiple of 128, at most 16384")
     return max(n, 16)
+
+
+def stream_read(buf, *, loads_per_lane=4, sink=None, stream=None):
+    """Read ``buf`` (a device tensor of a multiple of 16 bytes) once on the GPU
+    with 16-byte loads: the plain read rate a decode GEMV is compared with."""
+    _check_dev(buf, sink)
+    if sink is None:
+        sink = torch.zeros(1, dtype=torch.int32, device=buf.device)
+    nat.check(nat.lib().xrmm_stream_read(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink),
+                                         int(loads_per_lane), _stream(stream)))
+    return sink

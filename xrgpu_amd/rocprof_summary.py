@@ -61,6 +61,10 @@ def main(argv=None):
     ap.add_argument("--cal-write")
     ap.add_argument("--cal-kernel", default="copyBuffer")
     ap.add_argument("--cal-bytes", type=int, default=268435456)
+    ap.add_argument("--pmc", action="append", default=[],
+                    help="*_counter_collection.csv of a further --pmc run (repeatable): every counter recorded "
+                         "for the kernel is listed as its per-dispatch mean")
+    ap.add_argument("--cus", type=int, default=256, help="compute units, for the MFMA busy fraction")
     ap.add_argument("--command", required=True, help="the command line that produced the CSVs")
     ap.add_argument("--out", required=True)
     a = ap.parse_args(argv)
@@ -85,6 +89,21 @@ def main(argv=None):
                   f"fetch_factor: {ff:.4f}", f"write_factor: {fw:.4f}",
                   f"traffic_bytes_per_launch: {traffic:.0f}",
                   f"traffic_over_algorithmic: {traffic / a.algorithmic_bytes:.4f}"]
+    if a.pmc:
+        vals = {}
+        for path in a.pmc:
+            for r in _rows(path):
+                if a.kernel in r["Kernel_Name"]:
+                    vals.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+        lines += [""] + [f"{k}_per_dispatch: {statistics.fmean(v):.1f} (n={len(v)})" for k, v in sorted(vals.items())]
+        mean = {k: statistics.fmean(v) for k, v in vals.items()}
+        if "GRBM_GUI_ACTIVE" in mean:
+            lines.append(f"GRBM_GUI_ACTIVE_per_ns: {mean['GRBM_GUI_ACTIVE'] / st['avg_ns']:.3f}")
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and "GRBM_GUI_ACTIVE" in mean:
+            lines.append(f"mfma_busy_fraction: {mean['SQ_VALU_MFMA_BUSY_CYCLES'] / (mean['GRBM_GUI_ACTIVE'] * a.cus * 4):.4f}"
+                         f"  (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x {a.cus} CUs x 4 SIMDs))")
+        if "SQ_LDS_BANK_CONFLICT" in mean and "SQ_LDS_IDX_ACTIVE" in mean and mean["SQ_LDS_IDX_ACTIVE"]:
+            lines.append(f"lds_bank_conflict_over_active: {mean['SQ_LDS_BANK_CONFLICT'] / mean['SQ_LDS_IDX_ACTIVE']:.4f}")
     lines += ["", "command:", a.command, ""]
     with open(a.out, "w") as f:
         f.write("\n".join(lines))
