@@ -568,7 +568,12 @@ inline DotArgs dot_args(const Launch& L, int C, int W, uint32_t act_bytes) {
 inline size_t dot_lds_bytes(const DotArgs& a, int W) { return a.act_bytes + static_cast<size_t>(W) * a.meta_bytes; }
 
 // Launch shape of the dot GEMV: columns per wave (C) and waves per workgroup
-// (W), one column prefetched. Measured: 2 x 4 on the one-row decode workload;
+// (W); P columns' weight loads are issued before the activation staging, so
+// with P = C every weight load of a wave is in flight before its barrier
+// (decode workload 7.4 us against 7.8 us with P = 1; issuing later columns'
+// loads as earlier ones are consumed, or staging each lane's activations in
+// registers without LDS, measured slower). Measured: 2 x 4 on the one-row
+// decode workload;
 // 2 x 12 with four rows (wide), where the activation staging is four times
 // larger and fewer, larger workgroups amortise it; each wave picks its Qkv
 // projection from its global wave index, so the Qkv GQA decode workload fills
@@ -576,7 +581,7 @@ inline size_t dot_lds_bytes(const DotArgs& a, int W) { return a.act_bytes + stat
 // The XRMM_DOT_* macros override the shape for tuning builds; every
 // translation unit of one library must see the same values.
 #ifndef XRMM_DOT_P
-#define XRMM_DOT_P 1
+#define XRMM_DOT_P 2
 #endif
 #ifndef XRMM_DOT_NARROW_C
 #define XRMM_DOT_NARROW_C 2
