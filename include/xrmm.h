@@ -309,6 +309,21 @@ int xrmm_matmul_nbits_int8a(const void* A, const void* B, const void* scales, co
                             int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size, int32_t dtype,
                             void* stream);
 
+/* Allocation-free variant of xrmm_matmul_nbits_int8a. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and results as xrmm_matmul_nbits_int8a without the workspace:
+ * the activation codes and scales go to a static device scratch of 2 MiB per
+ * GPU (held until the process ends), so calls with
+ * xrmm_matmul_nbits_int8a_workspace_bytes(M, K) > 2 MiB fail with XRMM_EINVAL
+ * (e.g. M = 64 at K = 16384 fits). The call allocates nothing (the scratch's
+ * address is looked up once per device). Every call on a GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (different streams, or host threads)
+ * race and must be serialised by the caller. */
+int xrmm_matmul_nbits_int8a_noalloc(const void* A, const void* B, const void* scales, const void* zero_points,
+                                    int32_t zp_dtype, const void* bias, void* Y, int64_t M, int64_t K, int64_t N,
+                                    int32_t bits, int32_t block_size, int32_t dtype, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Measurement (no counterpart in the reference, which publishes no throughput
  * for this path): read `bytes` (a multiple of 16) at 16-byte aligned `src`

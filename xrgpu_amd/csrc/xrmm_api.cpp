@@ -392,6 +392,25 @@ int64_t xrmm_matmul_nbits_int8a_workspace_bytes(int64_t M, int64_t K) {
   return xrmm::i8a_workspace_bytes(M, K);
 }
 
+int xrmm_matmul_nbits_int8a_noalloc(const void* A, const void* B, const void* scales, const void* zero_points,
+                                    int32_t zp_dtype, const void* bias, void* Y, int64_t M, int64_t K, int64_t N,
+                                    int32_t bits, int32_t block_size, int32_t dtype, void* stream) {
+  // Same contract as xrmm_matmul_nbits_int8a; the workspace is the library's
+  // static device scratch, so nothing is allocated. Inputs past the scratch
+  // are rejected before any device work.
+  if (M > 0 && K > 0 && K % xrmm::kI8aBlock == 0 && K <= xrmm::kI8aMaxK &&
+      xrmm::i8a_workspace_bytes(M, K) > xrmm::kI8aScratchBytes)
+    return fail(XRMM_EINVAL, "allocation-free int8-activation path: M*K codes and scales exceed the " +
+                                 std::to_string(xrmm::kI8aScratchBytes) + "-byte device scratch");
+  void* ws = nullptr;
+  if (M > 0) {
+    const hipError_t e = xrmm::i8a_scratch(static_cast<hipStream_t>(stream), &ws);
+    if (e != hipSuccess) return dev_fail(e, "int8-activation scratch (hipGetSymbolAddress)");
+  }
+  return xrmm_matmul_nbits_int8a(A, B, scales, zero_points, zp_dtype, bias, Y, ws, xrmm::kI8aScratchBytes, M, K, N,
+                                 bits, block_size, dtype, stream);
+}
+
 int xrmm_matmul_nbits_int8a(const void* A, const void* B, const void* scales, const void* zero_points,
                             int32_t zp_dtype, const void* bias, void* Y, void* workspace, int64_t workspace_bytes,
                             int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size, int32_t dtype,

@@ -11,6 +11,9 @@
 //    (c | 0x80) - z, then ^ 0x80, per byte without borrows), and for each row
 //    form exact int32 chunk sums with v_dot4_i32_i8, scaled by the weight
 //    block's and the activation block's scales in float32.
+#include <atomic>
+#include <mutex>
+
 #include "xrmm_device.h"
 #include "xrmm_quant.h"
 
@@ -116,6 +119,42 @@ hipError_t launch_t(const Int8aArgs& a, hipStream_t st) {
 }
 
 }  // namespace
+
+// Scratch of the allocation-free entry point: activation codes and scales
+// (xrmm_matmul_nbits_int8a_noalloc). Each GPU holds its own copy for the
+// lifetime of the process; host code must use the address from i8a_scratch,
+// never this name (in host code it is a stand-in, not a device address).
+static __device__ __align__(256) uint8_t scratch[kI8aScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+}  // namespace
+
+hipError_t i8a_scratch(hipStream_t stream, void** ptr) {
+  int dev = 0;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      int cur = 0;
+      if ((e = hipGetDevice(&cur)) != hipSuccess) return e;
+      if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (cur != dev) (void)hipSetDevice(cur);
+      if (e != hipSuccess) return e;
+      if (p == nullptr) return hipErrorInvalidSymbol;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *ptr = p;
+  return hipSuccess;
+}
 
 hipError_t launch_i8a(const Int8aArgs& a, hipStream_t st) {
   if (a.M == 0) return hipSuccess;

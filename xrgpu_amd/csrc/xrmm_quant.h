@@ -65,4 +65,11 @@ inline int64_t i8a_workspace_bytes(int64_t M, int64_t K) {
 
 hipError_t launch_i8a(const Int8aArgs& a, hipStream_t st);
 
+// Bytes of the static device scratch behind xrmm_matmul_nbits_int8a_noalloc.
+constexpr int64_t kI8aScratchBytes = int64_t(2) << 20;
+
+// Device address of that scratch on the device `stream` runs on, looked up once
+// per device (hipGetSymbolAddress with the device current) and cached.
+hipError_t i8a_scratch(hipStream_t stream, void** ptr);
+
 }  // namespace xrmm

@@ -375,6 +375,31 @@ def matmul_nbits_int8a(A, B, scales, zero_points=None, bias=None, *, K, N, bits=
     return Y
 
 
+def matmul_nbits_int8a_noalloc(A, B, scales, zero_points=None, bias=None, *, K, N, bits=4, block_size=32, out=None,
+                               stream=None):
+    """``matmul_nbits_int8a`` without a workspace: the library's static 2 MiB
+    device scratch holds the activation codes (nothing is allocated by the
+    library; ``out`` avoids the one torch allocation here). Calls overlapping on
+    one GPU share that scratch and race."""
+    if A.dtype not in _T1 or scales.dtype != A.dtype:
+        raise nat.XrmmInvalid("T1 must be float32 or float16")
+    if zero_points is not None and zero_points.dtype != torch.uint8:
+        raise nat.XrmmInvalid("int8-activation path: zero points must be absent or packed uint8")
+    _check_weights(B, scales, zero_points, N, K, bits, block_size, scales.dtype)
+    if A.shape[-1] != K:
+        raise nat.XrmmInvalid("A's last dimension must equal K")
+    if bias is not None and (bias.dtype != A.dtype or tuple(bias.shape) != (N,)):
+        raise nat.XrmmInvalid("bias must be [N] of A's dtype")
+    M = A.numel() // K
+    _check_out(out, tuple(A.shape[:-1]) + (N,), A.dtype)
+    _check_dev(A, B, scales, zero_points, bias, out)
+    Y = out if out is not None else torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
+    nat.check(nat.lib().xrmm_matmul_nbits_int8a_noalloc(
+        _ptr(A), _ptr(B), _ptr(scales), _ptr(zero_points), nat.U8 if zero_points is not None else nat.UNSPECIFIED,
+        _ptr(bias), _ptr(Y), M, K, N, bits, block_size, _T1[A.dtype], _stream(stream)))
+    return Y
+
+
 def int8a_workspace_bytes(M, K) -> int:
     """Workspace bytes of ``matmul_nbits_int8a`` (activation codes and scales)."""
     n = int(nat.lib().xrmm_matmul_nbits_int8a_workspace_bytes(int(M), int(K)))
