@@ -144,7 +144,7 @@ def test_qkv_nonfinite_rows(gpu, M, K, Nq, Nkv, bs, dtype, skip_nf, family):
 MLP_CASES = [
     # M, K, N, bs, dtype, norm, expected family
     (8, 2048, 64, 32, np.float16, False, "gemv_q4_splitk"),
-    (6, 1024, 40, 64, np.float16, True, "gemv_q4_splitk"),
+    (6, 1024, 40, 64, np.float16, True, "gemv_q4_mfma"),
     (4, 96, 24, 32, np.float32, False, "generic"),
     (4, 96, 24, 32, np.float32, True, "generic"),
 ]
