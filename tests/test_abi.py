@@ -88,7 +88,10 @@ def test_qkv_requires_norm_scale():
     (0, 128, 4096, 14336, 32, nat.F16, nat.F16, "gemm_q4_big"),       # float zero points: always big
     (0, 127, 4096, 14336, 32, nat.F16, nat.U8, "gemm_q4_mfma"),
     (0, 64, 4096, 14336, 32, nat.F16, nat.F16, "generic"),
-    (1, 4, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_dot"),
+    (1, 4, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_mq"),
+    (1, 4, 4096, 4096, 64, nat.F16, nat.F16, "gemv_q4_dot"),      # float zero points
+    (1, 2, 8192, 4096, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_dot"),  # K beyond the MFMA GEMV's 4096
+    (1, 4, 4096, 4096, 16, nat.F16, nat.U8, "gemv_q4_dot"),       # bs = 16
     (1, 8, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_splitk"),
     (2, 16, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_splitk"),
     (2, 16, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),

@@ -107,8 +107,9 @@ def test_dot_gemv_finite_workgroups_unaffected(gpu):
 
 QKV_CASES = [
     # M, K, Nq, Nkv, bs, dtype, skip_nonfinite, expected family
-    (4, 2048, 64, 32, 32, np.float16, False, "gemv_q4_dot"),
-    (2, 1024, 40, 24, 64, np.float16, True, "gemv_q4_dot"),
+    (4, 2048, 64, 32, 32, np.float16, False, "gemv_q4_mq"),
+    (2, 1024, 40, 24, 64, np.float16, True, "gemv_q4_mq"),
+    (3, 1024, 40, 24, 16, np.float16, True, "gemv_q4_dot"),
     (8, 2048, 64, 32, 32, np.float16, False, "gemv_q4_splitk"),
     (5, 96, 16, 8, 32, np.float32, True, "generic"),
 ]

@@ -400,17 +400,27 @@ def test_qkv_parity(gpu, M, K, Nq, Nkv, bs, dtype, zp, skip):
 
 
 QKV_DOT_CASES = [
-    # M, K, Nq, Nkv, bs, zp, skip on the dot GEMV (M <= 4): every chunk-round
-    # count, rows 1..4, bs 16..64, every zero-point kind, K tails, column counts
-    # that leave a projection's last wave partly empty
+    # M, K, Nq, Nkv, bs, zp, skip for up to four rows: the four-row MFMA GEMV
+    # (integer zero points, block_size >= 32, K <= 4096) or else the dot GEMV;
+    # every chunk-round count, rows 1..4, bs 16..256, every zero-point kind, K
+    # tails, column counts that leave a projection's last tile or wave partly
+    # empty
     (4, 4096, 256, 64, 64, "packed", False),   # the GQA decode layout, narrower
     (2, 2048, 96, 40, 32, None, True),
-    (3, 8192, 33, 17, 32, "float", True),      # four chunk rounds, odd widths
-    (1, 1024, 20, 12, 16, "packed", True),     # bs = 16: two blocks per chunk
-    (4, 288, 40, 24, 32, "float_int", True),   # K tail inside the only chunk round
-    (4, 16384, 64, 32, 64, None, False),       # eight chunk rounds
+    (3, 8192, 33, 17, 32, "float", True),      # four chunk rounds, odd widths (dot)
+    (1, 1024, 20, 12, 16, "packed", True),     # bs = 16: two blocks per chunk (dot)
+    (4, 288, 40, 24, 32, "float_int", True),   # K tail inside the only chunk round (dot)
+    (4, 16384, 64, 32, 64, None, False),       # eight chunk rounds (dot)
     (1, 64, 1, 1, 32, None, True),             # one column per projection
+    (4, 1024, 33, 17, 128, "packed", True),    # odd widths, four chunks per block
+    (4, 4096, 16, 16, 256, "packed", False),   # eight chunks per block
+    (2, 96, 20, 12, 32, "packed", True),       # three blocks: odd packed zero-point rows
+    (3, 4000, 48, 16, 32, None, True),         # K tail inside the last block
 ]
+
+
+def qkv_gemv_family(M, K, bs, zp):
+    return "gemv_q4_mq" if bs >= 32 and zp in (None, "packed") and K <= 4096 else "gemv_q4_dot"
 
 
 @pytest.mark.parametrize("M,K,Nq,Nkv,bs,zp,skip", QKV_DOT_CASES)
@@ -423,7 +433,7 @@ def test_qkv_dot_parity(gpu, M, K, Nq, Nkv, bs, zp, skip):
     parts = [rand_case(rng, 1, K, n, 4, bs, dt, zp)[1:4] for n in (Nq, Nkv, Nkv)]
     kind = None if zp is None else ("packed" if zp == "packed" else "float")
     o = ops()
-    assert o.select_kernel("MatMulNBitsQkv", M, K, Nq, 4, bs, torch.float16, kind) == "gemv_q4_dot"
+    assert o.select_kernel("MatMulNBitsQkv", M, K, Nq, 4, bs, torch.float16, kind) == qkv_gemv_family(M, K, bs, zp)
     Q, Kk, V, R = o.matmul_nbits_qkv(dev(A), *[dev(x) for p in parts for x in p[:2]], norm_scale=dev(g), skip=dev(sk),
                                      block_size=bs, q_zero_points=dev(parts[0][2]), k_zero_points=dev(parts[1][2]),
                                      v_zero_points=dev(parts[2][2]))
@@ -598,7 +608,7 @@ def test_workload_decode_up_m1(gpu):
 def test_workload_qkv_gqa_m4(gpu):
     w = workloads.make("qkv_gqa_m4")
     i, at = w["inputs"], w["attrs"]
-    assert ops().select_kernel("MatMulNBitsQkv", 4, at["K"], at["Nq"], 4, at["block_size"], zp="packed") == "gemv_q4_dot"
+    assert ops().select_kernel("MatMulNBitsQkv", 4, at["K"], at["Nq"], 4, at["block_size"], zp="packed") == "gemv_q4_mq"
     outs = [host(t) for t in _run_workload(w)]
     ref = O.matmul_nbits_qkv(i["aT"], i["qBT"], i["qScalesT"], i["kBT"], i["kScalesT"], i["vBT"], i["vScalesT"],
                              K=at["K"], Nq=at["Nq"], Nkv=at["Nkv"], norm_scale=i["normScaleT"],

@@ -31,6 +31,8 @@ UNITS = [
     ("xrmm_gemv_dot_zp.hip", ["-DXRMM_ZPK=0"], "dot_zp0.o"),
     ("xrmm_gemv_dot_zp.hip", ["-DXRMM_ZPK=1"], "dot_zp1.o"),
     ("xrmm_gemv_dot_zp.hip", ["-DXRMM_ZPK=2"], "dot_zp2.o"),
+    ("xrmm_gemv_mq_zp.hip", ["-DXRMM_ZPK=0"], "mq_zp0.o"),
+    ("xrmm_gemv_mq_zp.hip", ["-DXRMM_ZPK=2"], "mq_zp2.o"),
     ("xrmm_gemv_sk_zp.hip", ["-DXRMM_ZPK=0"], "sk_zp0.o"),
     ("xrmm_gemv_sk_zp.hip", ["-DXRMM_ZPK=1"], "sk_zp1.o"),
     ("xrmm_gemv_sk_zp.hip", ["-DXRMM_ZPK=2"], "sk_zp2.o"),

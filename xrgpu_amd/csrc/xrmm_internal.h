@@ -40,8 +40,9 @@ struct Launch {
   void* residual;        // nullable
   float eps;
   Proj p[3];
-  // Only kernels that keep every dequantised weight in float32 (the dot GEMV
-  // applies scales to float32 block sums; the generic kernel uses the
+  // Only kernels that never round a dequantised weight to binary16 (the dot
+  // GEMV applies scales to float32 block sums, the four-row MFMA GEMV to
+  // float32 chunk sums of exact integer weights, the generic kernel uses the
   // reference formula): set when a binary16 weight (code - z) * scale could
   // leave the binary16 range.
   bool exact_weights;
@@ -63,7 +64,7 @@ class ExactWeightsScope {
 };
 
 // Kernel families the dispatcher chooses between.
-enum Kernel { K_GENERIC = 0, K_GEMV_Q4 = 1, K_GEMM_Q4 = 2, K_GEMV_DOT = 3, K_GEMM_BIG = 4, K_GEMV_SK = 5 };
+enum Kernel { K_GENERIC = 0, K_GEMV_Q4 = 1, K_GEMM_Q4 = 2, K_GEMV_DOT = 3, K_GEMM_BIG = 4, K_GEMV_SK = 5, K_GEMV_MQ = 6 };
 
 // Choose a kernel family for the geometry (host only, no device calls).
 Kernel select_kernel(const Launch& L);

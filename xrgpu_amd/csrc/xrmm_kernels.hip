@@ -30,6 +30,7 @@
 
 #include "xrmm_gemv.h"
 #include "xrmm_gemv_dot.h"
+#include "xrmm_gemv_mq.h"
 #include "xrmm_gemv_sk.h"
 #include "xrmm_gemm.h"
 
@@ -325,16 +326,26 @@ static bool gemm_big_fills(const Launch& L) {
 // split-K grid short of workgroups); Mlp has no dot kernel.
 inline int64_t split_k_min_rows(int op) { return op == OP_MATMUL ? 3 : op == OP_QKV ? 5 : 1; }
 
+// Qkv with up to four rows: the MFMA GEMV (integer zero points, whole 32-code
+// blocks, K up to 4096 at 4 bits) takes the GQA decode workload in 8.6 us
+// against 10.7 us on the dot GEMV, whose four activation rows cost 16
+// v_dot2 per weight dword; for MatMulNBits it only ties the split-K GEMV at
+// three or four rows (10.1 / 10.4 against 10.0 / 9.9 us at K = 4096,
+// N = 14336) and loses to the dot GEMV below.
+inline bool mq_takes(const Launch& L) { return L.op == OP_QKV && L.M <= 4 && mq_fits(L); }
+
 Kernel select_kernel(const Launch& L) {
   if (L.exact_weights) {
-    // the dot GEMV scales float32 block sums; every other fast kernel stages
-    // binary16 weights
+    // the dot and four-row MFMA GEMVs keep weights out of binary16; every
+    // other fast kernel stages binary16 weights
+    if (q4_fast_ok(L) && fits_i32(L) && mq_takes(L)) return K_GEMV_MQ;
     if (q4_fast_ok(L) && fits_i32(L) && (L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 &&
         L.M < split_k_min_rows(L.op) && dot_fits(L))
       return K_GEMV_DOT;
     return K_GENERIC;
   }
   if (q4_fast_ok(L) && fits_i32(L)) {
+    if (mq_takes(L)) return K_GEMV_MQ;
     if (L.M >= split_k_min_rows(L.op) && sk_fits(L)) return K_GEMV_SK;
     if ((L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 && dot_fits(L)) return K_GEMV_DOT;
     if (L.M >= 1 && L.M <= 16 && gemv_tiles(L) != 0) return K_GEMV_Q4;
@@ -349,6 +360,7 @@ const char* kernel_name(Kernel k) {
     case K_GEMV_Q4: return "gemv_q4_mfma";
     case K_GEMV_DOT: return "gemv_q4_dot";
     case K_GEMV_SK: return "gemv_q4_splitk";
+    case K_GEMV_MQ: return "gemv_q4_mq";
     case K_GEMM_Q4: return "gemm_q4_mfma";
     case K_GEMM_BIG: return "gemm_q4_big";
     default: return "generic";
@@ -380,6 +392,7 @@ hipError_t launch(const Launch& L, hipStream_t st) {
   Kernel k = select_kernel(L);
   const int zpk = effective_zpk(L);
   if (zpk < 0) k = K_GENERIC;  // mixed presence of zero points
+  if (k == K_GEMV_MQ) return zpk == ZP_PACKED ? launch_mq_for<ZP_PACKED>(L, st) : launch_mq_for<ZP_NONE>(L, st);
   if (k == K_GEMV_DOT) {
     if (zpk == ZP_NONE) return launch_dot_for<ZP_NONE>(L, st);
     if (zpk == ZP_PACKED) return launch_dot_for<ZP_PACKED>(L, st);
