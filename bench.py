@@ -29,7 +29,10 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
 FP16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, published
 PROFILES = os.path.join(ROOT, "profiles")
 SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048": 4, "qmoe_mixtral_t1": 6,
-         "bnb4_nf4_m1": 7, "gbq_embed_t2048": 8, "int8a_decode_m1": 1}
+         "bnb4_nf4_m1": 7, "gbq_embed_t2048": 8, "int8a_decode_m1": 1, "f32_k2048_m1": 0}
+# The CPU-oracle workload on the GPU: MatMulNBits float32, M=1, K=N=2048,
+# block_size 32, packed zero points (2,703,360 algorithmic bytes per call)
+F32 = dict(M=1, K=2048, N=2048, bs=32)
 # com.microsoft.MatMulBnb4 decode: the FFN up-projection shape in NF4, blocks of 64
 BNB4 = dict(M=1, K=4096, N=14336, bs=64)
 # com.microsoft.GatherBlockQuantized: a 128256 x 4096 4-bit embedding table
@@ -67,6 +70,16 @@ def make_replicas(torch, name, R, dev, seed):
         A = torch.randn((1, K), device=dev, generator=g).half()
         for _ in range(R):
             reps.append(dict(B=_gen_weights(torch, g, N, K // bs, bs // 2, dev), S=_scales(torch, g, (N, K // bs), dev)))
+        return dict(A=A, reps=reps, K=K, N=N, bs=bs)
+    if name == "f32_k2048_m1":
+        q = F32
+        K, N, bs = q["K"], q["N"], q["bs"]
+        kb = K // bs
+        A = torch.randn((q["M"], K), device=dev, generator=g)
+        for _ in range(R):
+            reps.append(dict(B=_gen_weights(torch, g, N, kb, bs // 2, dev),
+                             S=torch.rand((N, kb), device=dev, generator=g) * 0.019 + 0.001,
+                             Z=torch.randint(0, 256, (N, (kb + 1) // 2), dtype=torch.uint8, device=dev, generator=g)))
         return dict(A=A, reps=reps, K=K, N=N, bs=bs)
     if name == "prefill_m2048":
         M, K, N, bs = 2048, 4096, 14336, 128
@@ -137,6 +150,13 @@ def step_fn(ops, name, w):
     if name == "decode_up_m1":
         Y = torch.empty((1, w["N"]), dtype=torch.float16, device=A.device)
         return lambda i: ops.matmul_nbits(A, reps[i % len(reps)]["B"], reps[i % len(reps)]["S"], block_size=w["bs"], out=Y)
+    if name == "f32_k2048_m1":
+        Y = torch.empty((1, w["N"]), dtype=torch.float32, device=A.device)
+
+        def f(i):
+            r = reps[i % len(reps)]
+            return ops.matmul_nbits(A, r["B"], r["S"], r["Z"], block_size=w["bs"], out=Y)
+        return f
     if name == "prefill_m2048":
         Y = torch.empty((w["M"], w["N"]), dtype=torch.float16, device=A.device)
 
@@ -406,14 +426,15 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     results = {}
-    names = ["decode_up_m1", "prefill_m2048", "qkv_gqa_m4", "mlp_swiglu_m16", "qmoe_mixtral_t1", "bnb4_nf4_m1",
-             "gbq_embed_t2048", "int8a_decode_m1"]
+    names = ["decode_up_m1", "prefill_m2048", "qkv_gqa_m4", "mlp_swiglu_m16", "f32_k2048_m1", "qmoe_mixtral_t1",
+             "bnb4_nf4_m1", "gbq_embed_t2048", "int8a_decode_m1"]
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
     for name in names:
         # every leg rotates more weight bytes than the 256 MB Infinity Cache
         # holds (Qkv: 24 x 13.7 MB = 328 MB)
-        R = {"prefill_m2048": 2, "qmoe_mixtral_t1": 2, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24}.get(name, args.replicas)
+        R = {"prefill_m2048": 2, "qmoe_mixtral_t1": 2, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24,
+             "f32_k2048_m1": 100}.get(name, args.replicas)
         w = make_replicas(torch, name, R, dev, seed=SEEDS[name])
         fn = step_fn(ops, name, w)
         steps = args.steps if name != "prefill_m2048" else max(10, args.steps // 10)
@@ -480,6 +501,15 @@ def main():
             out[name] = {"us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                          "bytes_per_launch": nbytes, "replicas": r["replicas"],
                          "rotated_bytes": nbytes * r["replicas"]}
+    if "f32_k2048_m1" in results:
+        r, q = results["f32_k2048_m1"], F32
+        nbytes = 2_703_360
+        gbs = nbytes / (r["ms"] * 1e-3) / 1e9
+        out["f32_k2048_m1"] = {
+            "workload": "MatMulNBits float32 M=1 K=2048 N=2048 bs=32 packed zp (the CPU-oracle workload, on the GPU)",
+            "us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": nbytes, "replicas": r["replicas"],
+            "kernel": ops.select_kernel("MatMulNBits", q["M"], q["K"], q["N"], 4, q["bs"], torch.float32, zp="packed")}
     if "qmoe_mixtral_t1" in results:
         r, q = results["qmoe_mixtral_t1"], QMOE
         nbytes = qmoe_algorithmic_bytes(**q)

@@ -85,9 +85,10 @@ def test_qkv_requires_norm_scale():
     (0, 2048, 14336, 4096, 128, nat.F16, nat.U8, "gemm_q4_big"),      # 128 tiles: half the CUs
     (0, 1024, 14336, 4096, 128, nat.F16, nat.U8, "gemm_q4_mfma"),     # 64 tiles: the 128 x 128 GEMM
     (0, 256, 4096, 14336, 128, nat.F16, nat.UNSPECIFIED, "gemm_q4_mfma"),
-    (0, 128, 4096, 14336, 32, nat.F16, nat.F16, "gemm_q4_big"),       # float zero points: always big
+    (0, 128, 4096, 14336, 32, nat.F16, nat.F16, "gemm_q4_mfma"),      # float zero points: the same tile rule
+    (0, 2048, 4096, 14336, 32, nat.F16, nat.F32, "gemm_q4_big"),
     (0, 127, 4096, 14336, 32, nat.F16, nat.U8, "gemm_q4_mfma"),
-    (0, 64, 4096, 14336, 32, nat.F16, nat.F16, "generic"),
+    (0, 64, 4096, 14336, 32, nat.F16, nat.F16, "gemm_q4_mfma"),
     (1, 4, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_mq"),
     (1, 4, 4096, 4096, 64, nat.F16, nat.F16, "gemv_q4_dot"),      # float zero points
     (1, 2, 8192, 4096, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_dot"),  # K beyond the MFMA GEMV's 4096
@@ -95,7 +96,10 @@ def test_qkv_requires_norm_scale():
     (1, 8, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_splitk"),
     (2, 16, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_splitk"),
     (2, 16, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),
-    (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "generic"),
+    (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),       # the CPU-oracle workload, float32
+    (0, 4, 4096, 14336, 64, nat.F32, nat.F32, "gemv_q4_f32"),
+    (0, 5, 2048, 2048, 32, nat.F32, nat.U8, "generic"),             # float32 beyond four rows
+    (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),
     (0, 4, 16384, 14336, 16, nat.F16, nat.UNSPECIFIED, "generic"),  # dot staging would exceed 160 KB of LDS
     (0, 1, 33, 8, 32, nat.F16, nat.UNSPECIFIED, "generic"),
     (0, 4, 64, 8, 8, nat.F16, nat.UNSPECIFIED, "generic"),

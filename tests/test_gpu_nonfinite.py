@@ -67,8 +67,12 @@ MNB_CASES = [
     (8, 4096, 40, 64, np.float16, "packed", "gemv_q4_splitk"),
     (5, 512, 48, 16, np.float16, "packed", "gemv_q4_mfma"),
     (48, 512, 128, 32, np.float16, "packed", "gemm_q4_mfma"),
-    (128, 512, 256, 64, np.float16, "float", "gemm_q4_big"),
+    (128, 512, 256, 64, np.float16, "float", "gemm_q4_mfma"),
+    (2048, 256, 4096, 64, np.float16, "packed", "gemm_q4_big"),
     (5, 96, 40, 32, np.float32, "packed", "generic"),
+    (4, 96, 40, 32, np.float32, "packed", "gemv_q4_f32"),
+    (3, 2048, 33, 64, np.float32, "float", "gemv_q4_f32"),
+    (1, 4096, 64, 16, np.float32, None, "gemv_q4_f32"),
     (4, 100, 17, 32, np.float16, None, "generic"),   # K % 8 != 0
 ]
 
@@ -172,15 +176,17 @@ def test_mlp_nonfinite_activations(gpu, M, K, N, bs, dtype, norm, family):
 @pytest.mark.parametrize("M,K,N,bs,zp,family", [(1, 1024, 64, 32, None, "gemv_q4_dot"),
                                                  (5, 2048, 64, 32, "packed", "gemv_q4_splitk"),
                                                  (48, 512, 128, 32, "packed", "gemm_q4_mfma"),
-                                                 (128, 512, 256, 64, "float", "gemm_q4_big")])
+                                                 (128, 512, 256, 64, "float", "gemm_q4_mfma"),
+                                                 (2048, 256, 4096, 64, "packed", "gemm_q4_big")])
 def test_large_scales_within_binary16_weight_range(gpu, M, K, N, bs, zp, family):
-    """Scales up to 65504 / 15 keep every binary16 weight finite: each kernel
-    family matches the oracle with such scales (tiny activations keep Y in
-    range)."""
+    """Scales up to 4000 keep every binary16 weight finite (15 * 4000 < 65504;
+    the binary16 scale nearest 65504 / 15 is 4368, whose 15-fold is 65520 and
+    rounds to +Inf): each kernel family matches the oracle with such scales
+    (tiny activations keep Y in range)."""
     rng = np.random.default_rng(M + K + N + 1)
     assert ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16, zkind(zp)) == family
     A = (rng.standard_normal((M, K)) * 1e-3).astype(np.float16)
-    B, S, Z = weights(rng, K, N, bs, np.float16, zp, scale_lo=1000.0, scale_hi=65504.0 / 15)
+    B, S, Z = weights(rng, K, N, bs, np.float16, zp, scale_lo=1000.0, scale_hi=4000.0)
     Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), K=K, N=N, block_size=bs))
     ref = O.matmul_nbits(A, B, S, Z, K=K, N=N, block_size=bs)
     ok, err, lim = O.tolerance_ok(Y, ref, np.float16)

@@ -143,12 +143,50 @@ def test_gemv_dot_float32_zero_points(gpu):
     assert_parity(Y, O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs), np.float16)
 
 
+F32_CASES = [
+    # M, K, N, bs, zp, bias: float32 activations (the contract's T1 = float32)
+    # on the float32 GEMV, up to four rows: one to four chunk rounds, block
+    # sizes 16 (two blocks per chunk) to 128, every zero-point kind (float
+    # zero points as float32 and float16), K tails, N below one wave
+    (1, 2048, 2048, 32, "packed", False),   # the CPU-oracle workload's geometry
+    (1, 4096, 1000, 32, None, True),
+    (2, 4096, 333, 64, "float", False),
+    (2, 8192, 70, 128, "packed", True),     # four chunk rounds
+    (4, 1024, 96, 16, "float_int", True),
+    (4, 288, 17, 32, "packed", False),      # K tail inside the only chunk round
+    (1, 100, 5, 32, None, True),            # K tail inside the only block
+    (2, 512, 1, 16, "packed", True),        # N = 1
+]
+
+
+# float zero points run as float32 and as float16 (both are the contract's T3)
+F32_PARAMS = [c + (np.float32,) for c in F32_CASES] + \
+             [c + (np.float16,) for c in F32_CASES if c[4] in ("float", "float_int")]
+
+
+@pytest.mark.parametrize("M,K,N,bs,zp,bias,zdt", F32_PARAMS)
+def test_gemv_fp32_parity(gpu, M, K, N, bs, zp, bias, zdt):
+    rng = np.random.default_rng(M * 5 + K + N + bs)
+    A, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, np.float32, zp, bias)
+    if Z is not None and Z.dtype != np.uint8:
+        Z = Z.astype(zdt)
+    kind = None if zp is None else ("packed" if zp == "packed" else "float")
+    assert ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float32, kind) == "gemv_q4_f32"
+    Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
+    ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs)
+    assert Y.dtype == np.float32
+    assert_parity(Y, ref, np.float32)
+
+
 GEMM_CASES = [
     # M, K, N, bs, zp, bias: 17 <= M < 128 runs the 128 x 128 GEMM
     (17, 256, 64, 32, None, False),
     (64, 512, 130, 32, "packed", True),
     (96, 288, 40, 32, "packed", True),   # K tail
     (127, 1024, 256, 128, "packed", True),
+    (33, 512, 96, 32, "float", True),       # float zero points (the reference's T3)
+    (64, 1024, 130, 64, "float_int", False),
+    (120, 288, 70, 16, "float", True),      # bs = 16, K tail
 ]
 
 
@@ -156,8 +194,8 @@ GEMM_CASES = [
 def test_gemm_fp16_parity(gpu, M, K, N, bs, zp, bias):
     rng = np.random.default_rng(M * 7 + K + N + bs)
     A, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, np.float16, zp, bias)
-    assert ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16,
-                               None if zp is None else "packed") == "gemm_q4_mfma"
+    kind = None if zp is None else ("packed" if zp == "packed" else "float")
+    assert ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16, kind) == "gemm_q4_mfma"
     Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
     ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs)
     assert_parity(Y, ref, np.float16)

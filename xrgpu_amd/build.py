@@ -33,6 +33,9 @@ UNITS = [
     ("xrmm_gemv_dot_zp.hip", ["-DXRMM_ZPK=2"], "dot_zp2.o"),
     ("xrmm_gemv_mq_zp.hip", ["-DXRMM_ZPK=0"], "mq_zp0.o"),
     ("xrmm_gemv_mq_zp.hip", ["-DXRMM_ZPK=2"], "mq_zp2.o"),
+    ("xrmm_gemv_f32_zp.hip", ["-DXRMM_ZPK=0"], "f32_zp0.o"),
+    ("xrmm_gemv_f32_zp.hip", ["-DXRMM_ZPK=1"], "f32_zp1.o"),
+    ("xrmm_gemv_f32_zp.hip", ["-DXRMM_ZPK=2"], "f32_zp2.o"),
     ("xrmm_gemv_sk_zp.hip", ["-DXRMM_ZPK=0"], "sk_zp0.o"),
     ("xrmm_gemv_sk_zp.hip", ["-DXRMM_ZPK=1"], "sk_zp1.o"),
     ("xrmm_gemv_sk_zp.hip", ["-DXRMM_ZPK=2"], "sk_zp2.o"),

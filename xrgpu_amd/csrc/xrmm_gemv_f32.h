@@ -1,0 +1,321 @@
+// MatMulNBits GEMV for float32 activations (the contract's T1 = float32),
+// 4-bit weights, up to four rows. Float32 arithmetic throughout, as the
+// reference's serial loop (complex_kernel.glsl:80,83): codes convert exactly
+// to float32 and multiply the activations with fused multiply-adds, so the
+// float32 bar (1e-5 * max|Y|) holds with margin.
+//
+// Work split. A wave owns C consecutive output columns; its lanes split K:
+// lane l takes the 16-byte chunks l, l + 64, ... of each column, so one load
+// instruction reads 1 KB of contiguous codes. Every weight load of the wave is
+// issued before the activation staging. The workgroup stages the activation
+// rows once in LDS (float32, natural order) together with their sums per 16
+// codes, and the wave's scale / zero-point block in its own LDS slice; one
+// barrier, then no further synchronisation.
+//
+// Arithmetic. For a dword x of codes c0..c7 (low nibble first),
+// x & 0x0F0F0F0F holds c0, c2, c4, c6 in its bytes and (x >> 4) & 0x0F0F0F0F
+// holds c1, c3, c5, c7; v_cvt_f32_ubyte{0..3} turns each byte into a float.
+// sum_k (c_k - z) a_k = sum_k c_k a_k - z sum_k a_k per block half, with the
+// activation sums from the staging, then times the block scale.
+#pragma once
+#include "xrmm_gemv_dot.h"
+
+namespace xrmm {
+
+struct F32Args {
+  const float* A;
+  const uint8_t* B;
+  const float* S;
+  const void* Z;       // packed u8 [N, zrow] or float [N, kb] (zesz bytes each)
+  const float* bias;
+  float* Y;
+  uint32_t N, K, kb, rowb, zrow, M, bsl, zesz;
+  uint32_t meta_bytes;  // per-wave LDS slice: C*kb*4 scales (+ zero points), 16-aligned
+  uint32_t zoff;        // zero points' offset inside the slice
+};
+
+// LDS of the staged activations: [MR][nchunk] chunks of 32 floats at a
+// stride of 36 (the pad puts the 16 lanes of a 16-byte read on distinct
+// banks), then the sums [MR][2 * nchunk] (one per 16 codes).
+constexpr uint32_t kF32ChunkStride = 36;
+
+template <int MR>
+__host__ __device__ constexpr uint32_t f32_act_bytes(uint32_t nchunk) {
+  return MR * nchunk * kF32ChunkStride * 4u + MR * nchunk * 2u * 4u;
+}
+
+// Byte i of x as a float (the compiler emits v_cvt_f32_ubyte{i}).
+__device__ __forceinline__ float ubyte(uint32_t x, int i) {
+  return static_cast<float>((x >> (8 * i)) & 0xFFu);
+}
+
+template <int ZPK, int CPL, int C, int MR, int W>
+__global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t N = a.N, K = a.K, kb = a.kb, rowb = a.rowb, zrow = a.zrow;
+  const uint32_t nchunk = rowb >> 4;
+  const int M = static_cast<int>(a.M);
+  const uint32_t col0 = (blockIdx.x * W + wave) * C;
+  auto clampc = [&](uint32_t c) { return c < N ? c : N - 1; };
+  const uint32_t act_floats = MR * nchunk * kF32ChunkStride;
+  float* xs = reinterpret_cast<float*>(smem);        // [MR][nchunk][36]
+  float* sums = xs + act_floats;                     // [MR][2 * nchunk]
+  unsigned char* meta = smem + f32_act_bytes<MR>(nchunk) + wave * a.meta_bytes;
+
+  // ---- the wave's scale / zero-point block (C consecutive rows), 16-byte
+  // pieces; loads start at the dword boundary at or below the block
+  const uint32_t c0 = clampc(col0);
+  const uint32_t sbytes = C * kb * 4u;
+  const uint32_t zbytes = ZPK == ZP_NONE ? 0u : C * zrow;
+  const uint32_t zdel = (c0 * zrow) & 3u;
+  constexpr int MP = 4;  // up to 4 KB per block
+  u32x4 sv[MP], zv[ZPK == ZP_NONE ? 1 : MP];
+  {
+    const rsrc_t rS = mk_rsrc(a.S, N * kb * 4u);
+#pragma unroll
+    for (int q = 0; q < MP; ++q) {
+      const uint32_t o = lane * 16u + 1024u * q;
+      sv[q] = bld16_nt(rS, o < sbytes ? c0 * kb * 4u + o : kOOB, 0);
+    }
+    if constexpr (ZPK != ZP_NONE) {
+      const rsrc_t rZ = mk_rsrc(a.Z, (N * zrow + 15u) & ~15u);
+#pragma unroll
+      for (int q = 0; q < MP; ++q) {
+        const uint32_t o = lane * 16u + 1024u * q;
+        zv[q] = bld16_nt(rZ, o < zbytes + zdel ? c0 * zrow - zdel + o : kOOB, 0);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- activations of the workgroup: 16-byte pieces (4 floats), thread t
+  // takes pieces t, t + 64 W, ...
+  const rsrc_t rA = mk_rsrc(a.A, static_cast<uint32_t>(M) * K * 4u);
+  constexpr int PIECES_PER_ROW_MAX = 64 * CPL * 8;  // nchunk * 32 floats / 4
+  constexpr int PPT = (MR * PIECES_PER_ROW_MAX + W * 64 - 1) / (W * 64);
+  const uint32_t ppr = nchunk * 8u;  // pieces per staged row
+  u32x4 av[PPT];
+#pragma unroll
+  for (int it = 0; it < PPT; ++it) {
+    const uint32_t p = static_cast<uint32_t>(tid) + it * W * 64u;
+    const uint32_t m = p / ppr, k = (p % ppr) * 4u;
+    const bool ok = static_cast<int>(m) < M && k < K;  // K % 4 == 0 on this path
+    av[it] = bld16(rA, ok ? (m * K + k) * 4u : kOOB, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- weights: every chunk of the wave's C columns
+  const rsrc_t rB = mk_rsrc(a.B, N * rowb);
+  u32x4 wv[C][CPL];
+#pragma unroll
+  for (int i = 0; i < C; ++i)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const uint32_t ch = static_cast<uint32_t>(lane + 64 * j);
+      wv[i][j] = bld16_nt(rB, ch < nchunk ? clampc(col0 + i) * rowb + ch * 16u : kOOB, 0);
+    }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- stage: the wave's meta slice, the activations and their 16-code sums
+#pragma unroll
+  for (int q = 0; q < MP; ++q) {
+    const uint32_t o = lane * 16u + 1024u * q;
+    if (o < sbytes) *reinterpret_cast<u32x4*>(meta + o) = sv[q];
+    if (ZPK != ZP_NONE && o < zbytes + zdel) *reinterpret_cast<u32x4*>(meta + a.zoff + o) = zv[ZPK == ZP_NONE ? 0 : q];
+  }
+#pragma unroll
+  for (int it = 0; it < PPT; ++it) {
+    const uint32_t p = static_cast<uint32_t>(tid) + it * W * 64u;
+    if (p < MR * ppr) *reinterpret_cast<u32x4*>(xs + (p >> 3) * kF32ChunkStride + (p & 7u) * 4u) = av[it];
+  }
+  __syncthreads();
+  // sums per 16 codes: thread t sums half h = t, t + 64 W, ...
+  for (uint32_t h = static_cast<uint32_t>(tid); h < MR * nchunk * 2u; h += W * 64u) {
+    const float* x = xs + (h >> 1) * kF32ChunkStride + (h & 1u) * 16u;
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      s0 += x[e];
+      s1 += x[e + 1];
+    }
+    sums[h] = s0 + s1;
+  }
+  __syncthreads();
+
+  // ---- columns
+  float out[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) out[m] = 0.f;
+  const unsigned char* zmeta = meta + a.zoff + zdel;
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    if (col0 + i >= N) break;  // wave-uniform
+    float y[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) y[m] = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const uint32_t ch = static_cast<uint32_t>(lane + 64 * j);
+      const uint32_t chc = ch < nchunk ? ch : nchunk - 1;  // past-the-row lanes: in-range reads, no contribution
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {  // 16-code halves
+        const uint32_t b = (chc * 32u + 16u * h) >> a.bsl;
+        const float s = *reinterpret_cast<const float*>(meta + (i * kb + b) * 4u);
+        float z = 8.f;
+        if constexpr (ZPK == ZP_PACKED) {
+          z = static_cast<float>((zmeta[i * zrow + (b >> 1)] >> ((b & 1u) * 4u)) & 15u);
+        } else if constexpr (ZPK == ZP_FLOAT) {
+          const unsigned char* zp = zmeta + i * zrow + b * a.zesz;
+          z = a.zesz == 4 ? *reinterpret_cast<const float*>(zp) : static_cast<float>(*reinterpret_cast<const f16*>(zp));
+        }
+        float cv[16];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const uint32_t x = wv[i][j][2 * h + q];
+          const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            cv[8 * q + 2 * e] = ubyte(lo, e);
+            cv[8 * q + 2 * e + 1] = ubyte(hi, e);
+          }
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const float* x = xs + (m * nchunk + chc) * kF32ChunkStride + 16u * h;
+          const f32x4 x0 = *reinterpret_cast<const f32x4*>(x), x1 = *reinterpret_cast<const f32x4*>(x + 4);
+          const f32x4 x2 = *reinterpret_cast<const f32x4*>(x + 8), x3 = *reinterpret_cast<const f32x4*>(x + 12);
+          const float xv[16] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3],
+                                x2[0], x2[1], x2[2], x2[3], x3[0], x3[1], x3[2], x3[3]};
+          float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+          for (int e = 0; e < 16; e += 2) {
+            p0 = __builtin_fmaf(cv[e], xv[e], p0);
+            p1 = __builtin_fmaf(cv[e + 1], xv[e + 1], p1);
+          }
+          const float sa = sums[(m * nchunk + chc) * 2u + h];
+          float t = __builtin_fmaf(-z, sa, p0 + p1);
+          if (!__builtin_isfinite(sa)) {
+            // an infinite activation: the folded form would give Inf - Inf;
+            // the reference's per-element (code - z) * a keeps +-Inf
+            t = 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) t = __builtin_fmaf(cv[e] - z, xv[e], t);
+          }
+          // lanes past the row read the last chunk (in-range addresses) and
+          // add nothing: a zero scale would turn an infinite activation into NaN
+          y[m] = ch < nchunk ? __builtin_fmaf(s, t, y[m]) : y[m];
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float tot = wave_total(y[m]);
+      out[m] = lane == i ? tot : out[m];
+    }
+  }
+  const uint32_t mycol = col0 + static_cast<uint32_t>(lane);
+  if (lane < C && mycol < N) {
+    const float b = a.bias ? a.bias[mycol] : 0.f;
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      if (m < M) a.Y[static_cast<uint32_t>(m) * N + mycol] = out[m] + b;
+  }
+}
+
+// Host side: C columns per wave, W waves per workgroup.
+constexpr int kF32C = 2, kF32W = 8;
+
+inline int f32_cpl(const Launch& L) {
+  const int64_t chunks = L.kb * L.blob / 16;
+  for (int c = 1; c <= 4; c *= 2)
+    if (chunks <= 64 * c) return c;
+  return 0;
+}
+
+inline int f32_mr(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 0; }
+
+inline uint32_t f32_meta_bytes(const Launch& L, uint32_t& zoff) {
+  const uint32_t sb = static_cast<uint32_t>(kF32C * L.kb * 4);
+  zoff = (sb + 15u) & ~15u;
+  const int64_t zrow = L.zp_kind == ZP_PACKED ? L.zrow : L.kb * (L.zp_dtype == DT_F32 ? 4 : 2);
+  const uint32_t zb = L.zp_kind == ZP_NONE ? 0u : static_cast<uint32_t>(kF32C * zrow);
+  return (zoff + zb + 3u + 15u) & ~15u;
+}
+
+// fp32, 4-bit, power-of-two block_size >= 16, K a multiple of 4, 16-byte
+// aligned tensors, up to four rows, rows of at most 256 chunks, the wave's
+// scale / zero-point block within 4 KB and the staging within 160 KB of LDS.
+inline bool f32_fits(const Launch& L) {
+  if (L.dtype != DT_F32 || L.bits != 4 || L.bs_log2 < 4 || L.op != OP_MATMUL || L.K % 4 != 0) return false;
+  if ((L.kb * L.block_size) % 32 != 0) return false;
+  const int mr = f32_mr(L.M), cpl = f32_cpl(L);
+  if (mr == 0 || cpl == 0) return false;
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (!al(L.A) || !al(L.p[0].B) || !al(L.p[0].scales) || !al(L.p[0].zp)) return false;
+  if (L.zp_kind == ZP_FLOAT && L.p[0].zp == nullptr) return false;
+  uint32_t zoff = 0;
+  const uint32_t meta = f32_meta_bytes(L, zoff);
+  if (kF32C * L.kb * 4 > 4096 || meta - zoff > 4096 + 16) return false;
+  const uint32_t nchunk = static_cast<uint32_t>(L.kb * L.blob / 16);
+  if (mr * f32_cpl(L) > 8) return false;  // activation loads per thread (registers)
+  const int64_t lds = int64_t(mr) * nchunk * kF32ChunkStride * 4 + int64_t(mr) * nchunk * 2 * 4 + int64_t(kF32W) * meta;
+  return lds <= 160 * 1024;
+}
+
+template <int ZPK, int CPL, int MR>
+inline hipError_t launch_f32_3(const Launch& L, hipStream_t st) {
+  F32Args a{};
+  const Proj& P = L.p[0];
+  a.A = static_cast<const float*>(L.A);
+  a.B = P.B;
+  a.S = static_cast<const float*>(P.scales);
+  a.Z = P.zp;
+  a.bias = static_cast<const float*>(P.bias);
+  a.Y = static_cast<float*>(P.Y);
+  a.N = static_cast<uint32_t>(P.N);
+  a.K = static_cast<uint32_t>(L.K);
+  a.kb = static_cast<uint32_t>(L.kb);
+  a.rowb = static_cast<uint32_t>(L.kb * L.blob);
+  a.zesz = L.zp_dtype == DT_F32 ? 4u : 2u;
+  a.zrow = L.zp_kind == ZP_PACKED ? static_cast<uint32_t>(L.zrow) : a.kb * a.zesz;
+  a.M = static_cast<uint32_t>(L.M);
+  a.bsl = static_cast<uint32_t>(L.bs_log2);
+  a.meta_bytes = f32_meta_bytes(L, a.zoff);
+  const uint32_t nchunk = a.rowb / 16u;
+  const size_t lds = f32_act_bytes<MR>(nchunk) + size_t(kF32W) * a.meta_bytes;
+  auto kern = k_gemv_f32<ZPK, CPL, kF32C, MR, kF32W>;
+  if (lds > 64 * 1024) {
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+  }
+  const uint32_t waves = static_cast<uint32_t>((P.N + kF32C - 1) / kF32C);
+  hipLaunchKernelGGL(kern, dim3((waves + kF32W - 1) / kF32W), dim3(kF32W * 64), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int ZPK, int CPL>
+inline hipError_t launch_f32_2(const Launch& L, hipStream_t st) {
+  switch (f32_mr(L.M)) {
+    case 1: return launch_f32_3<ZPK, CPL, 1>(L, st);
+    case 2: return launch_f32_3<ZPK, CPL, 2>(L, st);
+    default: return launch_f32_3<ZPK, CPL, 4>(L, st);
+  }
+}
+
+template <int ZPK>
+inline hipError_t launch_f32_1(const Launch& L, hipStream_t st) {
+  switch (f32_cpl(L)) {
+    case 1: return launch_f32_2<ZPK, 1>(L, st);
+    case 2: return launch_f32_2<ZPK, 2>(L, st);
+    default: return launch_f32_2<ZPK, 4>(L, st);
+  }
+}
+
+// Entry of one zero-point kind (defined in xrmm_gemv_f32_zp.hip).
+template <int ZPK>
+hipError_t launch_f32_for(const Launch& L, hipStream_t st);
+
+}  // namespace xrmm

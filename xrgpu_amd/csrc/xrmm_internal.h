@@ -64,7 +64,8 @@ class ExactWeightsScope {
 };
 
 // Kernel families the dispatcher chooses between.
-enum Kernel { K_GENERIC = 0, K_GEMV_Q4 = 1, K_GEMM_Q4 = 2, K_GEMV_DOT = 3, K_GEMM_BIG = 4, K_GEMV_SK = 5, K_GEMV_MQ = 6 };
+enum Kernel { K_GENERIC = 0, K_GEMV_Q4 = 1, K_GEMM_Q4 = 2, K_GEMV_DOT = 3, K_GEMM_BIG = 4, K_GEMV_SK = 5, K_GEMV_MQ = 6,
+              K_GEMV_F32 = 7 };
 
 // Choose a kernel family for the geometry (host only, no device calls).
 Kernel select_kernel(const Launch& L);

@@ -31,6 +31,7 @@
 #include "xrmm_gemv.h"
 #include "xrmm_gemv_dot.h"
 #include "xrmm_gemv_mq.h"
+#include "xrmm_gemv_f32.h"
 #include "xrmm_gemv_sk.h"
 #include "xrmm_gemm.h"
 
@@ -300,7 +301,7 @@ constexpr int64_t kGemmBigMinM = 128;
 // N=14336, 56 tiles: 75 against 96 us; at 112 and 128 tiles the two tie; at
 // 448 tiles the big GEMM takes 256 against 367 us). The environment variable
 // XRMM_GEMM_BIG_MIN_TILES overrides the threshold (0: the big GEMM from
-// kGemmBigMinM rows on). Float zero points always take the big GEMM.
+// kGemmBigMinM rows on). Every zero-point kind follows the same rule.
 constexpr int64_t kGemmBigMinTiles = 128;
 
 static int64_t gemm_big_min_tiles() {
@@ -315,7 +316,7 @@ static int64_t gemm_big_min_tiles() {
 
 static bool gemm_big_fills(const Launch& L) {
   const int64_t tiles = (L.M + GB_M - 1) / GB_M * ((L.p[0].N + 255) / 256);
-  return L.zp_kind == ZP_FLOAT || tiles >= gemm_big_min_tiles();
+  return tiles >= gemm_big_min_tiles();
 }
 
 // Rows from which the split-K MFMA GEMV takes over from the dot GEMV (up to
@@ -344,13 +345,15 @@ Kernel select_kernel(const Launch& L) {
       return K_GEMV_DOT;
     return K_GENERIC;
   }
+  // float32 activations (the contract's T1 = float32), 4-bit, up to four rows
+  if (f32_fits(L) && fits_i32(L)) return K_GEMV_F32;
   if (q4_fast_ok(L) && fits_i32(L)) {
     if (mq_takes(L)) return K_GEMV_MQ;
     if (L.M >= split_k_min_rows(L.op) && sk_fits(L)) return K_GEMV_SK;
     if ((L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 && dot_fits(L)) return K_GEMV_DOT;
     if (L.M >= 1 && L.M <= 16 && gemv_tiles(L) != 0) return K_GEMV_Q4;
     if (L.M >= kGemmBigMinM && L.op == OP_MATMUL && gemm_big_fills(L)) return K_GEMM_BIG;
-    if (L.M > 16 && L.op == OP_MATMUL && L.zp_kind != ZP_FLOAT) return K_GEMM_Q4;
+    if (L.M > 16 && L.op == OP_MATMUL) return K_GEMM_Q4;
   }
   return K_GENERIC;
 }
@@ -361,6 +364,7 @@ const char* kernel_name(Kernel k) {
     case K_GEMV_DOT: return "gemv_q4_dot";
     case K_GEMV_SK: return "gemv_q4_splitk";
     case K_GEMV_MQ: return "gemv_q4_mq";
+    case K_GEMV_F32: return "gemv_q4_f32";
     case K_GEMM_Q4: return "gemm_q4_mfma";
     case K_GEMM_BIG: return "gemm_q4_big";
     default: return "generic";
@@ -392,6 +396,11 @@ hipError_t launch(const Launch& L, hipStream_t st) {
   Kernel k = select_kernel(L);
   const int zpk = effective_zpk(L);
   if (zpk < 0) k = K_GENERIC;  // mixed presence of zero points
+  if (k == K_GEMV_F32) {
+    if (zpk == ZP_NONE) return launch_f32_for<ZP_NONE>(L, st);
+    if (zpk == ZP_PACKED) return launch_f32_for<ZP_PACKED>(L, st);
+    return launch_f32_for<ZP_FLOAT>(L, st);
+  }
   if (k == K_GEMV_MQ) return zpk == ZP_PACKED ? launch_mq_for<ZP_PACKED>(L, st) : launch_mq_for<ZP_NONE>(L, st);
   if (k == K_GEMV_DOT) {
     if (zpk == ZP_NONE) return launch_dot_for<ZP_NONE>(L, st);
@@ -415,6 +424,7 @@ hipError_t launch(const Launch& L, hipStream_t st) {
   }
   if (k == K_GEMM_Q4) {
     if (zpk == ZP_NONE) return launch_gemm1<ZP_NONE>(L, st);
+    if (zpk == ZP_FLOAT) return launch_gemm1<ZP_FLOAT>(L, st);
     return launch_gemm1<ZP_PACKED>(L, st);
   }
   int64_t cols = L.p[0].N;
