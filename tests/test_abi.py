@@ -96,6 +96,11 @@ def test_qkv_requires_norm_scale():
     (1, 8, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_splitk"),
     (2, 16, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_splitk"),
     (2, 16, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),
+    (2, 17, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemm_q4_fused"),   # Mlp prefill
+    (2, 2048, 4096, 14336, 64, nat.F16, nat.U8, "gemm_q4_fused"),
+    (1, 64, 2048, 512, 32, nat.F16, nat.U8, "gemm_q4_fused"),           # Qkv prefill
+    (1, 17, 4096, 4096, 16, nat.F16, nat.F16, "gemm_q4_fused"),
+    (1, 32, 96, 16, 32, nat.F32, nat.UNSPECIFIED, "generic"),           # float32 prefill
     (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),       # the CPU-oracle workload, float32
     (0, 4, 4096, 14336, 64, nat.F32, nat.F32, "gemv_q4_f32"),
     (0, 5, 2048, 2048, 32, nat.F32, nat.U8, "generic"),             # float32 beyond four rows

@@ -115,6 +115,8 @@ QKV_CASES = [
     (2, 1024, 40, 24, 64, np.float16, True, "gemv_q4_mq"),
     (3, 1024, 40, 24, 16, np.float16, True, "gemv_q4_dot"),
     (8, 2048, 64, 32, 32, np.float16, False, "gemv_q4_splitk"),
+    (32, 1024, 40, 24, 32, np.float16, False, "gemm_q4_fused"),
+    (20, 512, 130, 3, 16, np.float16, True, "gemm_q4_fused"),
     (5, 96, 16, 8, 32, np.float32, True, "generic"),
 ]
 
@@ -150,6 +152,8 @@ MLP_CASES = [
     # M, K, N, bs, dtype, norm, expected family
     (8, 2048, 64, 32, np.float16, False, "gemv_q4_splitk"),
     (6, 1024, 40, 64, np.float16, True, "gemv_q4_mfma"),
+    (24, 2048, 64, 32, np.float16, False, "gemm_q4_fused"),
+    (130, 1024, 40, 64, np.float16, True, "gemm_q4_fused"),
     (4, 96, 24, 32, np.float32, False, "generic"),
     (4, 96, 24, 32, np.float32, True, "generic"),
 ]

@@ -571,6 +571,98 @@ def test_mlp_parity(gpu, M, K, N, bs, dtype, skip, norm, biases, act):
     assert np.array_equal(host(R), r)
 
 
+QKV_GEMM_CASES = [
+    # M, K, Nq, Nkv, bs, zp, skip on the fused 128 x 128 GEMM (M > 16): row
+    # tiles full and partial, projections narrower than one column tile, K
+    # tails inside a K step, every zero-point kind, bs 16..128
+    (64, 2048, 512, 128, 32, "packed", True),   # GQA prefill layout, narrower
+    (17, 1024, 40, 24, 64, None, False),       # one row past the GEMVs, odd widths
+    (200, 4096, 256, 64, 128, "float", True),  # two row tiles, the second partial
+    (130, 512, 130, 3, 16, "packed", True),    # bs = 16; a 3-column projection
+    (33, 96, 20, 12, 32, "float_int", True),   # K = 96: half a K step at the end
+    (48, 1000, 136, 8, 64, None, True),        # K = 1000 padded to 1024 by the blocks
+]
+
+
+@pytest.mark.parametrize("M,K,Nq,Nkv,bs,zp,skip", QKV_GEMM_CASES)
+def test_qkv_gemm_parity(gpu, M, K, Nq, Nkv, bs, zp, skip):
+    rng = np.random.default_rng(M * 7 + K + Nq + Nkv + bs)
+    dt = np.float16
+    A = rng.standard_normal((M, K)).astype(dt)
+    sk = rng.standard_normal((M, K)).astype(dt) if skip else None
+    g = rng.uniform(0.5, 1.5, K).astype(dt)
+    parts = [rand_case(rng, 1, K, n, 4, bs, dt, zp)[1:4] for n in (Nq, Nkv, Nkv)]
+    kind = None if zp is None else ("packed" if zp == "packed" else "float")
+    o = ops()
+    assert o.select_kernel("MatMulNBitsQkv", M, K, Nq, 4, bs, torch.float16, kind) == "gemm_q4_fused"
+    Q, Kk, V, R = o.matmul_nbits_qkv(dev(A), *[dev(x) for p in parts for x in p[:2]], norm_scale=dev(g), skip=dev(sk),
+                                     block_size=bs, q_zero_points=dev(parts[0][2]), k_zero_points=dev(parts[1][2]),
+                                     v_zero_points=dev(parts[2][2]))
+    ref = O.matmul_nbits_qkv(A, parts[0][0], parts[0][1], parts[1][0], parts[1][1], parts[2][0], parts[2][1], K=K,
+                             Nq=Nq, Nkv=Nkv, norm_scale=g, skip=sk, block_size=bs, q_zero_points=parts[0][2],
+                             k_zero_points=parts[1][2], v_zero_points=parts[2][2])
+    for got, exp, nm in zip((Q, Kk, V), ref[:3], "qkv"):
+        assert_parity(host(got), exp, dt, nm)
+    assert np.array_equal(host(R), ref[3])  # residual A + skip: bit-exact
+
+
+MLP_GEMM_CASES = [
+    # M, K, N, bs, zp, skip, norm, biases, act, residual on the fused GEMM
+    (64, 2048, 5632, 32, None, False, True, False, "silu", True),   # the SwiGLU prefill layout (M = 64)
+    (17, 1024, 72, 64, "packed", True, True, True, "silu", True),
+    (130, 512, 33, 32, None, True, False, True, "gelu", True),       # N below one 64-output tile
+    (40, 4096, 100, 128, "float", False, False, False, "relu", False),
+    (256, 992, 64, 16, "packed", True, True, True, "tanh", True),    # bs = 16; K ends half way into a step
+    (24, 256, 96, 32, None, False, True, True, "sigmoid", False),
+    (24, 256, 96, 32, "float_int", True, False, True, "none", True),
+    (24, 256, 96, 32, None, True, True, False, "swiglu", False),
+]
+
+
+@pytest.mark.parametrize("M,K,N,bs,zp,skip,norm,biases,act,res", MLP_GEMM_CASES)
+def test_mlp_gemm_parity(gpu, M, K, N, bs, zp, skip, norm, biases, act, res):
+    rng = np.random.default_rng(M * 37 + K + N + bs)
+    dt = np.float16
+    A = rng.standard_normal((M, K)).astype(dt)
+    sk = rng.standard_normal((M, K)).astype(dt) if skip else None
+    g = rng.uniform(0.5, 1.5, K).astype(dt) if norm else None
+    _, gB, gS, gZ, gb = rand_case(rng, 1, K, N, 4, bs, dt, zp, biases)
+    _, uB, uS, uZ, ub = rand_case(rng, 1, K, N, 4, bs, dt, zp, biases)
+    kind = None if zp is None else ("packed" if zp == "packed" else "float")
+    assert ops().select_kernel("MatMulNBitsMlp", M, K, N, 4, bs, torch.float16, kind) == "gemm_q4_fused"
+    Y, R = ops().matmul_nbits_mlp(dev(A), dev(gB), dev(gS), dev(uB), dev(uS), skip=dev(sk), norm_scale=dev(g),
+                                  gate_bias=dev(gb), up_bias=dev(ub), block_size=bs, activation=act,
+                                  gate_zero_points=dev(gZ), up_zero_points=dev(uZ), want_residual=res)
+    ref, r = O.matmul_nbits_mlp(A, gB, gS, uB, uS, K=K, N=N, skip=sk, norm_scale=g, gate_bias=gb, up_bias=ub,
+                                block_size=bs, activation=act, gate_zero_points=gZ, up_zero_points=uZ)
+    assert_parity(host(Y), ref, dt)
+    if res:
+        assert np.array_equal(host(R), r)
+
+
+def test_gemm_fused_rows_independent(gpu):
+    """A row's outputs do not depend on the other rows of its tile (each row's
+    normalisation factor is its own) and a repeat gives the same bits."""
+    rng = np.random.default_rng(5)
+    M, K, N, bs = 96, 1024, 160, 32
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    A[7] *= np.float16(50.0)  # one row far louder than the others
+    g = rng.uniform(0.5, 1.5, K).astype(np.float16)
+    _, gB, gS, _, _ = rand_case(rng, 1, K, N, 4, bs, np.float16, None)
+    _, uB, uS, _, _ = rand_case(rng, 1, K, N, 4, bs, np.float16, None)
+    o = ops()
+    run = lambda X: host(o.matmul_nbits_mlp(dev(X), dev(gB), dev(gS), dev(uB), dev(uS), norm_scale=dev(g),
+                                            block_size=bs)[0])
+    Y1, Y2 = run(A), run(A)
+    assert np.array_equal(Y1, Y2)
+    A2 = A.copy()
+    A2[7] = 0
+    Y3 = run(A2)
+    assert np.array_equal(np.delete(Y1, 7, 0), np.delete(Y3, 7, 0))
+    ref, _ = O.matmul_nbits_mlp(A, gB, gS, uB, uS, K=K, N=N, norm_scale=g, block_size=bs)
+    assert_parity(Y1, ref, np.float16)
+
+
 @pytest.mark.parametrize("name", ["pinned_plain_gb_ub", "pinned_norm_nogb_noub", "pinned_skipsum_gb_ub"])
 @pytest.mark.parametrize("dtype", [np.float32, np.float16])
 def test_fixture_mlp_pinned(gpu, name, dtype):

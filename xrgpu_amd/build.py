@@ -42,6 +42,9 @@ UNITS = [
     ("xrmm_gemm_zp.hip", ["-DXRMM_ZPK=0"], "gemm_zp0.o"),
     ("xrmm_gemm_zp.hip", ["-DXRMM_ZPK=1"], "gemm_zp1.o"),
     ("xrmm_gemm_zp.hip", ["-DXRMM_ZPK=2"], "gemm_zp2.o"),
+    ("xrmm_gemm_fused_zp.hip", ["-DXRMM_ZPK=0"], "fused_zp0.o"),
+    ("xrmm_gemm_fused_zp.hip", ["-DXRMM_ZPK=1"], "fused_zp1.o"),
+    ("xrmm_gemm_fused_zp.hip", ["-DXRMM_ZPK=2"], "fused_zp2.o"),
     ("xrmm_moe.hip", [], "moe.o"),
     ("xrmm_quant.hip", [], "quant.o"),
     ("xrmm_int8a.hip", [], "int8a.o"),

@@ -11,9 +11,15 @@
 //                are dequantised in registers to fp16 and multiplied on
 //                v_mfma_f32_16x16x32_f16 against the activations staged once
 //                in LDS. Qkv/Mlp fuse the RMS prologue and the SwiGLU epilogue.
-//  * k_gemm_q4   16 < M < 128, fp16, 4-bit. LDS-tiled MFMA GEMM with 128 x 128
-//                tiles: activation tiles and weight tiles dequantised to fp16
-//                are staged in LDS and fed to v_mfma_f32_32x32x16_f16.
+//  * k_gemv_dot / k_gemv_sk / k_gemv_mq / k_gemv_f32 (xrmm_gemv_*.h): the
+//                decode GEMVs (v_dot2 on block sums, split-K MFMA, four-row
+//                MFMA for Qkv, float32 activations).
+//  * k_gemm_q4   MatMulNBits, 16 < M, fp16, 4-bit, while 256 x 256 tiles would
+//                not fill the chip. LDS-tiled MFMA GEMM with 128 x 128 tiles:
+//                activation tiles and weight tiles dequantised to fp16 are
+//                staged in LDS and fed to v_mfma_f32_32x32x16_f16.
+//  * k_gemm_fused  Qkv / Mlp, 16 < M (xrmm_gemm_fused.h): the same tiling with
+//                the RMS prologue, residual and SwiGLU epilogue fused.
 //  * k_gemm_q4_big  M >= 128, fp16, 4-bit (xrmm_gemm.h): 256 x 256 tiles on
 //                eight waves, dequantisation interleaved with the MFMAs.
 //  * k_generic   every other geometry (fp32, 2/8-bit, float zero points with a
@@ -34,6 +40,7 @@
 #include "xrmm_gemv_f32.h"
 #include "xrmm_gemv_sk.h"
 #include "xrmm_gemm.h"
+#include "xrmm_gemm_fused.h"
 
 namespace xrmm {
 
@@ -354,6 +361,7 @@ Kernel select_kernel(const Launch& L) {
     if (L.M >= 1 && L.M <= 16 && gemv_tiles(L) != 0) return K_GEMV_Q4;
     if (L.M >= kGemmBigMinM && L.op == OP_MATMUL && gemm_big_fills(L)) return K_GEMM_BIG;
     if (L.M > 16 && L.op == OP_MATMUL) return K_GEMM_Q4;
+    if (L.M > 16) return K_GEMM_FUSED;
   }
   return K_GENERIC;
 }
@@ -367,6 +375,7 @@ const char* kernel_name(Kernel k) {
     case K_GEMV_F32: return "gemv_q4_f32";
     case K_GEMM_Q4: return "gemm_q4_mfma";
     case K_GEMM_BIG: return "gemm_q4_big";
+    case K_GEMM_FUSED: return "gemm_q4_fused";
     default: return "generic";
   }
 }
@@ -421,6 +430,11 @@ hipError_t launch(const Launch& L, hipStream_t st) {
     if (zpk == ZP_NONE) return launch_gemm_big_for<ZP_NONE>(L, st);
     if (zpk == ZP_PACKED) return launch_gemm_big_for<ZP_PACKED>(L, st);
     return launch_gemm_big_for<ZP_FLOAT>(L, st);
+  }
+  if (k == K_GEMM_FUSED) {
+    if (zpk == ZP_NONE) return launch_gemm_fused_for<ZP_NONE>(L, st);
+    if (zpk == ZP_FLOAT) return launch_gemm_fused_for<ZP_FLOAT>(L, st);
+    return launch_gemm_fused_for<ZP_PACKED>(L, st);
   }
   if (k == K_GEMM_Q4) {
     if (zpk == ZP_NONE) return launch_gemm1<ZP_NONE>(L, st);
