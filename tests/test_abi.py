@@ -88,7 +88,8 @@ def test_qkv_requires_norm_scale():
     (0, 128, 4096, 14336, 32, nat.F16, nat.F16, "gemm_q4_mfma"),      # float zero points: the same tile rule
     (0, 2048, 4096, 14336, 32, nat.F16, nat.F32, "gemm_q4_big"),
     (0, 127, 4096, 14336, 32, nat.F16, nat.U8, "gemm_q4_mfma"),
-    (0, 64, 4096, 14336, 32, nat.F16, nat.F16, "gemm_q4_mfma"),
+    (0, 64, 4096, 14336, 32, nat.F16, nat.F16, "gemv_q4_splitk"),    # four row chunks of 16
+    (0, 65, 4096, 14336, 32, nat.F16, nat.F16, "gemm_q4_mfma"),
     (1, 4, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_mq"),
     (1, 4, 4096, 4096, 64, nat.F16, nat.F16, "gemv_q4_dot"),      # float zero points
     (1, 2, 8192, 4096, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_dot"),  # K beyond the MFMA GEMV's 4096
@@ -98,7 +99,8 @@ def test_qkv_requires_norm_scale():
     (2, 16, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),
     (2, 17, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemm_q4_fused"),   # Mlp prefill
     (2, 2048, 4096, 14336, 64, nat.F16, nat.U8, "gemm_q4_fused"),
-    (1, 64, 2048, 512, 32, nat.F16, nat.U8, "gemm_q4_fused"),           # Qkv prefill
+    (1, 64, 2048, 512, 32, nat.F16, nat.U8, "gemv_q4_splitk"),          # Qkv, four row chunks
+    (1, 65, 2048, 512, 32, nat.F16, nat.U8, "gemm_q4_fused"),           # Qkv prefill
     (1, 17, 4096, 4096, 16, nat.F16, nat.F16, "gemm_q4_fused"),
     (1, 32, 96, 16, 32, nat.F32, nat.UNSPECIFIED, "generic"),           # float32 prefill
     (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),       # the CPU-oracle workload, float32

@@ -31,6 +31,7 @@ LIMIT_CASES = [
     # M, N, kernel: K = 4096, block 32, 4-bit, packed zero points (2 KB of codes per column)
     (1, 524287, "gemv_q4_dot"),     # codes 1 GiB - 2 KB: the largest fast geometry
     (4, 524287, "gemv_q4_splitk"),
+    (40, 524287, "gemv_q4_splitk"),  # three row chunks at the largest geometry
     (1, 524288, "generic"),         # codes exactly 1 GiB
     (2, 1048577, "generic"),        # codes 2 GiB + 2 KB: offsets past 2^31
     (256, 524287, "gemm_q4_big"),   # 2048 tiles of 256 x 256, then 256 x 192

@@ -179,7 +179,8 @@ def test_gemv_fp32_parity(gpu, M, K, N, bs, zp, bias, zdt):
 
 
 GEMM_CASES = [
-    # M, K, N, bs, zp, bias: 17 <= M < 128 runs the 128 x 128 GEMM
+    # M, K, N, bs, zp, bias: 17 <= M < 128 runs the 128 x 128 GEMM (K of
+    # neither 64 nor 128 chunks: the split-K GEMV takes no row chunks)
     (17, 256, 64, 32, None, False),
     (64, 512, 130, 32, "packed", True),
     (96, 288, 40, 32, "packed", True),   # K tail
@@ -575,7 +576,7 @@ QKV_GEMM_CASES = [
     # M, K, Nq, Nkv, bs, zp, skip on the fused 128 x 128 GEMM (M > 16): row
     # tiles full and partial, projections narrower than one column tile, K
     # tails inside a K step, every zero-point kind, bs 16..128
-    (64, 2048, 512, 128, 32, "packed", True),   # GQA prefill layout, narrower
+    (80, 2048, 512, 128, 32, "packed", True),   # GQA prefill layout, narrower
     (17, 1024, 40, 24, 64, None, False),       # one row past the GEMVs, odd widths
     (200, 4096, 256, 64, 128, "float", True),  # two row tiles, the second partial
     (130, 512, 130, 3, 16, "packed", True),    # bs = 16; a 3-column projection
@@ -608,10 +609,10 @@ def test_qkv_gemm_parity(gpu, M, K, Nq, Nkv, bs, zp, skip):
 
 MLP_GEMM_CASES = [
     # M, K, N, bs, zp, skip, norm, biases, act, residual on the fused GEMM
-    (64, 2048, 5632, 32, None, False, True, False, "silu", True),   # the SwiGLU prefill layout (M = 64)
+    (72, 2048, 5632, 32, None, False, True, False, "silu", True),   # the SwiGLU prefill layout
     (17, 1024, 72, 64, "packed", True, True, True, "silu", True),
     (130, 512, 33, 32, None, True, False, True, "gelu", True),       # N below one 64-output tile
-    (40, 4096, 100, 128, "float", False, False, False, "relu", False),
+    (70, 4096, 100, 128, "float", False, False, False, "relu", False),
     (256, 992, 64, 16, "packed", True, True, True, "tanh", True),    # bs = 16; K ends half way into a step
     (24, 256, 96, 32, None, False, True, True, "sigmoid", False),
     (24, 256, 96, 32, "float_int", True, False, True, "none", True),
@@ -638,6 +639,65 @@ def test_mlp_gemm_parity(gpu, M, K, N, bs, zp, skip, norm, biases, act, res):
     assert_parity(host(Y), ref, dt)
     if res:
         assert np.array_equal(host(R), r)
+
+
+SK_CHUNK_CASES = [
+    # op, M, K, N (Qkv: Nq, Nkv), bs, zp, extras: the split-K GEMV over row
+    # chunks of 16 (17..64 rows, K of 64 or 128 chunks): partial last chunks,
+    # every operator and zero-point kind, prologue and epilogue variants
+    ("mnb", 17, 4096, 100, 32, "packed", dict(bias=True)),
+    ("mnb", 33, 2048, 260, 64, "float", dict(bias=True)),
+    ("mnb", 64, 4096, 1000, 128, None, dict(bias=False)),
+    ("mnb", 48, 2048, 33, 32, "float_int", dict(bias=True)),
+    ("qkv", 40, 4096, (256, 64), 64, "packed", dict(skip=True)),
+    ("qkv", 64, 2048, (100, 36), 32, None, dict(skip=False)),
+    ("mlp", 24, 2048, 96, 32, None, dict(skip=True, norm=True, biases=True, act="silu", res=True)),
+    ("mlp", 64, 4096, 40, 64, "packed", dict(skip=False, norm=True, biases=False, act="gelu", res=False)),
+    ("mlp", 50, 2048, 33, 128, None, dict(skip=True, norm=False, biases=True, act="relu", res=True)),
+]
+
+
+@pytest.mark.parametrize("op,M,K,N,bs,zp,ex", SK_CHUNK_CASES)
+def test_splitk_row_chunks(gpu, op, M, K, N, bs, zp, ex):
+    rng = np.random.default_rng(M * 53 + K + bs + len(op))
+    dt = np.float16
+    o = ops()
+    kind = None if zp is None else ("packed" if zp == "packed" else "float")
+    A = rng.standard_normal((M, K)).astype(dt)
+    if op == "mnb":
+        _, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, dt, zp, ex["bias"])
+        assert o.select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16, kind) == "gemv_q4_splitk"
+        Y = host(o.matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
+        assert_parity(Y, O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs), dt)
+    elif op == "qkv":
+        Nq, Nkv = N
+        sk = rng.standard_normal((M, K)).astype(dt) if ex["skip"] else None
+        g = rng.uniform(0.5, 1.5, K).astype(dt)
+        parts = [rand_case(rng, 1, K, n, 4, bs, dt, zp)[1:4] for n in (Nq, Nkv, Nkv)]
+        assert o.select_kernel("MatMulNBitsQkv", M, K, Nq, 4, bs, torch.float16, kind) == "gemv_q4_splitk"
+        Q, Kk, V, R = o.matmul_nbits_qkv(dev(A), *[dev(x) for p in parts for x in p[:2]], norm_scale=dev(g),
+                                         skip=dev(sk), block_size=bs, q_zero_points=dev(parts[0][2]),
+                                         k_zero_points=dev(parts[1][2]), v_zero_points=dev(parts[2][2]))
+        ref = O.matmul_nbits_qkv(A, parts[0][0], parts[0][1], parts[1][0], parts[1][1], parts[2][0], parts[2][1],
+                                 K=K, Nq=Nq, Nkv=Nkv, norm_scale=g, skip=sk, block_size=bs,
+                                 q_zero_points=parts[0][2], k_zero_points=parts[1][2], v_zero_points=parts[2][2])
+        for got, exp, nm in zip((Q, Kk, V), ref[:3], "qkv"):
+            assert_parity(host(got), exp, dt, nm)
+        assert np.array_equal(host(R), ref[3])  # residual A + skip: bit-exact, every row chunk
+    else:
+        sk = rng.standard_normal((M, K)).astype(dt) if ex["skip"] else None
+        g = rng.uniform(0.5, 1.5, K).astype(dt) if ex["norm"] else None
+        _, gB, gS, gZ, gb = rand_case(rng, 1, K, N, 4, bs, dt, zp, ex["biases"])
+        _, uB, uS, uZ, ub = rand_case(rng, 1, K, N, 4, bs, dt, zp, ex["biases"])
+        assert o.select_kernel("MatMulNBitsMlp", M, K, N, 4, bs, torch.float16, kind) == "gemv_q4_splitk"
+        Y, R = o.matmul_nbits_mlp(dev(A), dev(gB), dev(gS), dev(uB), dev(uS), skip=dev(sk), norm_scale=dev(g),
+                                  gate_bias=dev(gb), up_bias=dev(ub), block_size=bs, activation=ex["act"],
+                                  gate_zero_points=dev(gZ), up_zero_points=dev(uZ), want_residual=ex["res"])
+        ref, r = O.matmul_nbits_mlp(A, gB, gS, uB, uS, K=K, N=N, skip=sk, norm_scale=g, gate_bias=gb, up_bias=ub,
+                                    block_size=bs, activation=ex["act"], gate_zero_points=gZ, up_zero_points=uZ)
+        assert_parity(host(Y), ref, dt)
+        if ex["res"]:
+            assert np.array_equal(host(R), r)
 
 
 def test_gemm_fused_rows_independent(gpu):

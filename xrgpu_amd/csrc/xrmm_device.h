@@ -193,6 +193,55 @@ __device__ __forceinline__ Meta<SPC> ld_meta(const Launch& L, const Proj& P, int
   return m;
 }
 
+// The same metadata as raw bits, loaded together with a chunk's weights so
+// that the loads of a pipeline stage are all in flight at once (ld_meta's
+// conversion would make the load's first use follow it immediately):
+// binary16 scale bits, and the zero point's raw bits (packed: the byte;
+// float: binary16 or float32 bits). Converted by meta_of when consumed.
+template <int SPC>
+struct RawMeta {
+  uint32_t s[SPC];
+  uint32_t z[SPC];
+};
+
+template <int ZPK, int SPC>
+__device__ __forceinline__ RawMeta<SPC> ld_meta_raw(const Launch& L, const Proj& P, int64_t n, int64_t ch, bool valid) {
+  RawMeta<SPC> r;
+#pragma unroll
+  for (int half = 0; half < SPC; ++half) {
+    const int64_t b = (ch * 32 + half * 16) >> L.bs_log2;
+    r.s[half] = 0u;
+    r.z[half] = 0u;
+    if (valid) {
+      r.s[half] = static_cast<const uint16_t*>(P.scales)[n * L.kb + b];
+      if constexpr (ZPK == ZP_PACKED)
+        r.z[half] = static_cast<const uint8_t*>(P.zp)[n * L.zrow + (b >> 1)];
+      else if constexpr (ZPK == ZP_FLOAT)
+        r.z[half] = L.zp_dtype == DT_F32 ? static_cast<const uint32_t*>(P.zp)[n * L.kb + b]
+                                         : static_cast<const uint16_t*>(P.zp)[n * L.kb + b];
+    }
+  }
+  return r;
+}
+
+template <int ZPK, int SPC>
+__device__ __forceinline__ Meta<SPC> meta_of(const Launch& L, const RawMeta<SPC>& r, int64_t ch, bool valid) {
+  Meta<SPC> m;
+#pragma unroll
+  for (int half = 0; half < SPC; ++half) {
+    const int64_t b = (ch * 32 + half * 16) >> L.bs_log2;
+    m.s[half] = __builtin_bit_cast(f16, static_cast<uint16_t>(r.s[half]));
+    float z = 8.f;
+    if constexpr (ZPK == ZP_PACKED)
+      z = static_cast<float>((r.z[half] >> ((b & 1) * 4)) & 15u);
+    else if constexpr (ZPK == ZP_FLOAT)
+      z = L.zp_dtype == DT_F32 ? __builtin_bit_cast(float, r.z[half])
+                               : static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(r.z[half])));
+    m.z[half] = valid ? z : 8.f;
+  }
+  return m;
+}
+
 // Dequantise the chunk's four dwords with its metadata (pair order per dword).
 template <int ZPK, int SPC>
 __device__ __forceinline__ void dq_regs(u32x4 w, const Meta<SPC>& m, f16x8 out[4]) {

@@ -18,11 +18,11 @@
 // outputs by inv in the epilogue. The first column tile writes the residual
 // (r rounded once). The binary16 stage limits |r * gamma| to 65504.
 //
-// Pipeline. K steps of 64; the next step's activations (+ skip, gamma) and
-// weight chunk are loaded into registers while the current step's MFMAs run;
-// weights are dequantised on the way into LDS (the routine and pair order of
-// the other kernels: the staged weight is the reference's float32 weight
-// rounded once to binary16).
+// Pipeline. K steps of 64; each thread's activations (+ skip, gamma), weight
+// chunk and its raw scale / zero point are loaded into registers two steps
+// ahead (two register sets alternate); weights are dequantised on the way into
+// LDS (the routine and pair order of the other kernels: the staged weight is
+// the reference's float32 weight rounded once to binary16).
 #pragma once
 #include "xrmm_device.h"
 
@@ -74,27 +74,33 @@ __global__ __launch_bounds__(256) void k_gemm_fused(Launch L) {
   const uint8_t* Bcol = PB.B + (bnval ? bn : 0) * row_bytes;
 
   // activation staging: thread t stages pieces t + 256 i (row (t >> 3) + 32 i,
-  // k group t & 7): the same k group for all four, so one gamma load per step
+  // k group t & 7): the same k group for all four, so one gamma load per step.
+  // Registers of one step, loaded two steps ahead.
   const int grp = tid & 7;
-  f16x8 ra[4], rs[4], rg;
-  u32x4 rb;
+  struct Regs {
+    f16x8 a[4], s[4], g;
+    u32x4 b;
+    RawMeta<SPC> m;
+  };
   float sq[4] = {0.f, 0.f, 0.f, 0.f};
-  auto gload = [&](int64_t kt) {
+  auto gload = [&](Regs& r, int64_t kt) {
     const int64_t k = kt * GF_BK + grp * 8;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t m = m0 + (tid >> 3) + 32 * i;
       const bool ok = m < M && k < K;  // K % 8 == 0: groups are whole
-      ra[i] = ok ? __builtin_bit_cast(f16x8, ld16(A + m * K + k)) : f16x8{};
-      rs[i] = (ok && skip) ? __builtin_bit_cast(f16x8, ld16(S + m * K + k)) : f16x8{};
+      r.a[i] = ok ? __builtin_bit_cast(f16x8, ld16(A + m * K + k)) : f16x8{};
+      r.s[i] = (ok && skip) ? __builtin_bit_cast(f16x8, ld16(S + m * K + k)) : f16x8{};
     }
-    rg = (norm && k < K) ? __builtin_bit_cast(f16x8, ld16(G + k)) : f16x8{};
+    r.g = (norm && k < K) ? __builtin_bit_cast(f16x8, ld16(G + k)) : f16x8{};
     const int64_t ch = kt * 2 + bh;
-    rb = (bnval && ch < nchunk) ? ld16(Bcol + ch * 16) : u32x4{0u, 0u, 0u, 0u};
+    const bool bok = bnval && ch < nchunk;
+    r.b = bok ? ld16(Bcol + ch * 16) : u32x4{0u, 0u, 0u, 0u};
+    r.m = ld_meta_raw<ZPK, SPC>(L, PB, bn, ch, bok);
   };
   f16* res = static_cast<f16*>(L.residual);
   const bool write_res = res != nullptr && blockIdx.x == 0;
-  auto sstore = [&](int64_t kt) {
+  auto sstore = [&](const Regs& rg, int64_t kt) {
     const int64_t k = kt * GF_BK + grp * 8;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -102,10 +108,10 @@ __global__ __launch_bounds__(256) void k_gemm_fused(Launch L) {
       f16x8 u, r16;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float r = skip ? __fadd_rn(static_cast<float>(ra[i][e]), static_cast<float>(rs[i][e]))
-                             : static_cast<float>(ra[i][e]);
+        const float r = skip ? __fadd_rn(static_cast<float>(rg.a[i][e]), static_cast<float>(rg.s[i][e]))
+                             : static_cast<float>(rg.a[i][e]);
         sq[i] = __builtin_fmaf(r, r, sq[i]);
-        u[e] = static_cast<f16>(norm ? r * static_cast<float>(rg[e]) : r);
+        u[e] = static_cast<f16>(norm ? r * static_cast<float>(rg.g[e]) : r);
         r16[e] = static_cast<f16>(r);
       }
       *reinterpret_cast<f16x8*>(As + row * GF_LDK + grp * 8) = pair_order(u);
@@ -114,7 +120,7 @@ __global__ __launch_bounds__(256) void k_gemm_fused(Launch L) {
     }
     const int64_t ch = kt * 2 + bh;
     f16x8 b[4];
-    dq_chunk<ZPK, SPC>(L, PB, bn, ch, bnval && ch < nchunk, rb, b);
+    dq_regs<ZPK, SPC>(rg.b, meta_of<ZPK, SPC>(L, rg.m, ch, bnval && ch < nchunk), b);
 #pragma unroll
     for (int d = 0; d < 4; ++d) *reinterpret_cast<f16x8*>(Bs + bcol * GF_LDK + bh * 32 + d * 8) = b[d];
   };
@@ -127,12 +133,13 @@ __global__ __launch_bounds__(256) void k_gemm_fused(Launch L) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  gload(0);
-  for (int64_t kt = 0; kt < ktiles; ++kt) {
+  // One K step: stage the registers of step kt, refill them with step kt + 2
+  // (loads past the last step return zeros), multiply.
+  auto step = [&](Regs& r, int64_t kt) {
     __syncthreads();
-    sstore(kt);
+    sstore(r, kt);
     __syncthreads();
-    if (kt + 1 < ktiles) gload(kt + 1);
+    gload(r, kt + 2);
 #pragma unroll
     for (int kk = 0; kk < GF_BK / 16; ++kk) {
       f16x8 a[2], b[2];
@@ -147,7 +154,16 @@ __global__ __launch_bounds__(256) void k_gemm_fused(Launch L) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
+  };
+  Regs r0, r1;
+  gload(r0, 0);
+  gload(r1, 1);
+  int64_t kt = 0;
+  for (; kt + 1 < ktiles; kt += 2) {
+    step(r0, kt);
+    step(r1, kt + 1);
   }
+  if (kt < ktiles) step(r0, kt);
 
   // rows' sums of squares: the eight threads of a row (consecutive lanes) add
   // their partials

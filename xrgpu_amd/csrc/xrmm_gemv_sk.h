@@ -33,6 +33,8 @@
 // order as A[j][k]; the MFMA's 32 k are the four lane groups' dwords. Tile
 // partials accumulate in float32.
 #pragma once
+#include <cstdlib>
+
 #include "xrmm_device.h"
 
 namespace xrmm {
@@ -60,6 +62,7 @@ struct SkArgs {
   uint32_t zesz;      // bytes per float zero point (2 or 4)
   uint32_t tiles;     // tiles of the whole launch
   uint32_t tpw;       // tiles per workgroup (<= sk_tmax(W))
+  uint32_t chunks;    // row chunks of 16 (more than 16 rows: the grid repeats per chunk)
 };
 
 // Tiles per workgroup at most: the LDS holds every wave's partial sum of
@@ -123,11 +126,19 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t j = lane & 15, g = lane >> 4;
-  const uint32_t K = a.K, kb = a.kb, rowb = a.rowb, M = a.M;
+  // Workgroup -> (tile group x, row chunk y). The row chunks of one tile group
+  // are eight workgroups apart: consecutive workgroups go to consecutive XCDs,
+  // so they run on one XCD, close in time, and share its L2 copy of the
+  // weights (one HBM read for up to 64 rows). With one chunk x = blockIdx.x.
+  const uint32_t bid = blockIdx.x, nch = a.chunks;
+  const uint32_t gx = (bid & 7u) + 8u * (bid / (8u * nch)), gy = (bid >> 3) % nch;
+  const uint32_t tb = gx * a.tpw;  // first tile of the workgroup
+  if (tb >= a.tiles) return;       // padding of the grid to whole groups of eight (uniform)
+  const uint32_t m0 = 16u * gy;    // first row of the chunk
+  const uint32_t K = a.K, kb = a.kb, rowb = a.rowb, M = a.M - m0 < 16u ? a.M - m0 : 16u;
   const uint32_t ch0 = (w * 4 + g) * CPL;  // first chunk of this lane
   const uint32_t k0 = ch0 * 32;            // first k of this lane
   const uint32_t b0 = k0 >> a.bsl;         // first block of this lane
-  const uint32_t tb = blockIdx.x * a.tpw;  // first tile of the workgroup
   const uint32_t tpw = a.tpw < a.tiles - tb ? a.tpw : a.tiles - tb;
 
   // ---- activations: the wave's K slice of all 16 rows, loaded coalesced
@@ -136,7 +147,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
   // order directly, every load instruction touched 64 different lines.)
   constexpr int AI = 16 * OPR / 64;  // coalesced loads per lane
   static_assert(AI == 4 * CPL, "activation staging");
-  const rsrc_t rA = mk_rsrc(a.A, M * K * 2u);
+  const rsrc_t rA = mk_rsrc(static_cast<const f16*>(a.A) + m0 * K, M * K * 2u);
   u32x4 craw[AI];
   uint32_t coff[AI];
 #pragma unroll
@@ -148,7 +159,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
   }
   u32x4 csk[NRM ? AI : 1];
   if constexpr (NRM) {
-    const rsrc_t rK = mk_rsrc(a.skip, a.skip ? M * K * 2u : 0u);
+    const rsrc_t rK = mk_rsrc(a.skip ? static_cast<const f16*>(a.skip) + m0 * K : nullptr, a.skip ? M * K * 2u : 0u);
 #pragma unroll
     for (int r = 0; r < AI; ++r) csk[r] = bld16(rK, coff[r], 0);
   }
@@ -301,7 +312,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
       for (int v = 0; v < W; ++v) t += rsq[v][j];
       inv = 1.f / sqrtf(t / static_cast<float>(K) + a.eps);
     }
-    const bool write_res = a.residual != nullptr && blockIdx.x == 0 && j < M;
+    const bool write_res = a.residual != nullptr && gx == 0 && j < M;
     const rsrc_t rG = mk_rsrc(a.gamma, has_gamma ? K * 2u : 0u);
 #pragma unroll
     for (int i = 0; i < CPL; ++i)
@@ -314,7 +325,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = has_gamma ? static_cast<f16>(static_cast<float>(rr[e]) * (inv * static_cast<float>(gv[e]))) : rr[e];
         aop[i][d] = pair_order(x);
-        if (write_res && k < K) *reinterpret_cast<f16x8*>(static_cast<f16*>(a.residual) + j * K + k) = rr;
+        if (write_res && k < K) *reinterpret_cast<f16x8*>(static_cast<f16*>(a.residual) + (m0 + j) * K + k) = rr;
       }
   } else {
 #pragma unroll
@@ -394,7 +405,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_sk(SkArgs a) {
   const uint32_t N = P.N;
   const uint32_t col = MLP ? tt * 8u + jj : (tt - P.t0) * 16u + jj;
   if (col >= N) return;
-  f16* Y = static_cast<f16*>(P.Y);
+  f16* Y = static_cast<f16*>(P.Y) + m0 * N;
   if constexpr (MLP) {
     f32x4 u = part_of(0, t * 64 + l + 8);
 #pragma unroll
@@ -452,10 +463,34 @@ inline int64_t sk_tiles(const Launch& L, int64_t& t1, int64_t& t2) {
   return t2 + (L.p[2].N + 15) / 16;
 }
 
-// Whether the split-K GEMV applies: M <= 16, a column splits evenly over the
-// waves, block_size >= 32, Mlp gate and up of one width.
+// Rows the split-K GEMV takes at most, in chunks of 16 that share the weight
+// stream through L2. Measured against the 128 x 128 GEMMs (K = 4096,
+// N = 14336 unless noted): MatMulNBits at 32 / 64 rows 19 / 37 us against
+// 57 / 58 us, at 128 rows 65 against 61 us; Mlp (K = 2048, N = 5632) at
+// 32 / 64 rows 21 / 39 against 59 / 64 us, at 128 rows 77 against 67 us; Qkv
+// (Nq = 4096, Nkv = 1024) at 64 rows 47 against 100 us. Each chunk
+// dequantises the weights again, so the cost grows with the chunks.
+// XRMM_SK_MAX_ROWS overrides the limit (measurement).
+#ifndef XRMM_SK_MAX_ROWS
+#define XRMM_SK_MAX_ROWS 64
+#endif
+inline int64_t sk_max_rows() {
+  static const int64_t v = [] {
+    const char* e = std::getenv("XRMM_SK_MAX_ROWS");
+    if (e != nullptr && *e != 0) {
+      char* end = nullptr;
+      const long long r = std::strtoll(e, &end, 10);
+      if (end != nullptr && *end == 0 && r >= 16 && r <= 256) return static_cast<int64_t>(r);
+    }
+    return static_cast<int64_t>(XRMM_SK_MAX_ROWS);
+  }();
+  return v;
+}
+
+// Whether the split-K GEMV applies: M <= sk_max_rows(), a column splits evenly
+// over the waves, block_size >= 32, Mlp gate and up of one width.
 inline bool sk_fits(const Launch& L) {
-  if (L.M < 1 || L.M > 16 || sk_shape(L).w == 0 || L.block_size < 32 || L.bs_log2 < 5) return false;
+  if (L.M < 1 || L.M > sk_max_rows() || sk_shape(L).w == 0 || L.block_size < 32 || L.bs_log2 < 5) return false;
   if (L.op == OP_MLP && L.p[0].N != L.p[1].N) return false;
   return true;
 }
@@ -499,7 +534,10 @@ inline hipError_t launch_sk5(const Launch& L, hipStream_t st) {
   int64_t tpw = (tiles + cus - 1) / cus;
   tpw = tpw < 1 ? 1 : tpw > sk_tmax(W) ? sk_tmax(W) : tpw;
   a.tpw = static_cast<uint32_t>(tpw);
-  const uint32_t grid = static_cast<uint32_t>((tiles + tpw - 1) / tpw);
+  a.chunks = static_cast<uint32_t>((L.M + 15) / 16);
+  int64_t groups = (tiles + tpw - 1) / tpw;
+  if (a.chunks > 1) groups = (groups + 7) / 8 * 8;  // whole groups of eight workgroups per chunk
+  const uint32_t grid = static_cast<uint32_t>(groups * a.chunks);
   hipLaunchKernelGGL((k_gemv_sk<ZPK, OPK, W, CPL, SPL, NRM>), dim3(grid), dim3(W * 64), 0, st, a);
   return hipGetLastError();
 }

@@ -156,33 +156,39 @@ __global__ __launch_bounds__(256) void k_gemm_q4(Launch L) {
   const int64_t ktiles = (Kp + GM_BK - 1) / GM_BK;
   const f16* A = static_cast<const f16*>(L.A);
 
-  // global -> register staging
-  f16x8 ra[4];
-  u32x4 rb;
+  // global -> register staging, two steps ahead: each thread's four 16-byte
+  // activation pieces, one weight chunk and its raw scale / zero point
+  struct Regs {
+    f16x8 a[4];
+    u32x4 b;
+    RawMeta<SPC> m;
+  };
   const int bcol = tid >> 1, bh = tid & 1;
   const int64_t bn = n0 + bcol;
   const bool bnval = bn < N;
   const uint8_t* Bcol = P.B + (bnval ? bn : 0) * row_bytes;
 
-  auto gload = [&](int64_t kt) {
+  auto gload = [&](Regs& r, int64_t kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int idx = tid + 256 * i, row = idx >> 3, grp = idx & 7;
       const int64_t m = m0 + row, k = kt * GM_BK + grp * 8;
-      ra[i] = (m < M && k < K) ? __builtin_bit_cast(f16x8, ld16(A + m * K + k)) : f16x8{};
+      r.a[i] = (m < M && k < K) ? __builtin_bit_cast(f16x8, ld16(A + m * K + k)) : f16x8{};
     }
     const int64_t ch = kt * 2 + bh;
-    rb = (bnval && ch < nchunk) ? ld16(Bcol + ch * 16) : u32x4{0u, 0u, 0u, 0u};
+    const bool ok = bnval && ch < nchunk;
+    r.b = ok ? ld16(Bcol + ch * 16) : u32x4{0u, 0u, 0u, 0u};
+    r.m = ld_meta_raw<ZPK, SPC>(L, P, bn, ch, ok);
   };
-  auto sstore = [&](int64_t kt) {
+  auto sstore = [&](const Regs& r, int64_t kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int idx = tid + 256 * i, row = idx >> 3, grp = idx & 7;
-      *reinterpret_cast<f16x8*>(As + row * GM_LDK + grp * 8) = pair_order(ra[i]);
+      *reinterpret_cast<f16x8*>(As + row * GM_LDK + grp * 8) = pair_order(r.a[i]);
     }
     const int64_t ch = kt * 2 + bh;
     f16x8 b[4];
-    dq_chunk<ZPK, SPC>(L, P, bn, ch, bnval && ch < nchunk, rb, b);
+    dq_regs<ZPK, SPC>(r.b, meta_of<ZPK, SPC>(L, r.m, ch, bnval && ch < nchunk), b);
 #pragma unroll
     for (int d = 0; d < 4; ++d) *reinterpret_cast<f16x8*>(Bs + bcol * GM_LDK + bh * 32 + d * 8) = b[d];
   };
@@ -195,12 +201,13 @@ __global__ __launch_bounds__(256) void k_gemm_q4(Launch L) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  gload(0);
-  for (int64_t kt = 0; kt < ktiles; ++kt) {
+  // One K step: stage the registers of step kt, refill them with step kt + 2
+  // (loads past the last step return zeros), multiply.
+  auto step = [&](Regs& r, int64_t kt) {
     __syncthreads();
-    sstore(kt);
+    sstore(r, kt);
     __syncthreads();
-    if (kt + 1 < ktiles) gload(kt + 1);
+    gload(r, kt + 2);
 #pragma unroll
     for (int kk = 0; kk < GM_BK / 16; ++kk) {
       f16x8 a[2], b[2];
@@ -215,7 +222,16 @@ __global__ __launch_bounds__(256) void k_gemm_q4(Launch L) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
+  };
+  Regs r0, r1;
+  gload(r0, 0);
+  gload(r1, 1);
+  int64_t kt = 0;
+  for (; kt + 1 < ktiles; kt += 2) {
+    step(r0, kt);
+    step(r1, kt + 1);
   }
+  if (kt < ktiles) step(r0, kt);
 
   // epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each 32x32 tile
 #pragma unroll
