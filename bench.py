@@ -511,15 +511,20 @@ def main():
                           "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": FP16_PEAK_TFLOPS,
                                        "unit": "TFLOP/s", "frac": round(tf / FP16_PEAK_TFLOPS, 4),
                                        "flops_per_launch": fl,
-                                       "kernel": ops.select_kernel("MatMulNBits", 2048, 4096, 14336, 4, 128, zp="packed")},
+                                       "kernel": ops.select_kernel("MatMulNBits", 2048, 4096, 14336, 4, 128, zp="packed"),
+                                       "traffic": traffic_of("prefill_m2048_gemm.md", ops.select_kernel(
+                                           "MatMulNBits", 2048, 4096, 14336, 4, 128, zp="packed"))},
                           "dense_fp16_library": dense_fp16_reference(torch)}
-    for name, nbytes in (("qkv_gqa_m4", 13_656_064), ("mlp_swiglu_m16", 66_650_112)):
+    for name, nbytes, summary, kern in (
+            ("qkv_gqa_m4", 13_656_064, "qkv_gqa_m4_gemv.md",
+             ops.select_kernel("MatMulNBitsQkv", 4, 4096, 4096, 4, 64, zp="packed")),
+            ("mlp_swiglu_m16", 66_650_112, "mlp_swiglu_m16_gemv.md", ops.select_kernel("MatMulNBitsMlp", 16, 4096, 14336, 4, 32))):
         if name in results:
             r = results[name]
             gbs = nbytes / (r["ms"] * 1e-3) / 1e9
             out[name] = {"us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                          "bytes_per_launch": nbytes, "replicas": r["replicas"],
-                         "rotated_bytes": nbytes * r["replicas"]}
+                         "rotated_bytes": nbytes * r["replicas"], "kernel": kern, "traffic": traffic_of(summary, kern)}
     if "mlp_prefill_m64" in results:
         r, q = results["mlp_prefill_m64"], MLP64
         fl = 2 * 2 * q["M"] * q["K"] * q["N"]
@@ -531,7 +536,8 @@ def main():
             "us": round(r["ms"] * 1e3, 3), "tflops": round(tf, 2), "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 4),
             "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "flops_per_launch": fl,
             "bytes_per_launch": nbytes, "replicas": r["replicas"],
-            "kernel": ops.select_kernel("MatMulNBitsMlp", q["M"], q["K"], q["N"], 4, q["bs"])}
+            "kernel": ops.select_kernel("MatMulNBitsMlp", q["M"], q["K"], q["N"], 4, q["bs"]),
+            "traffic": traffic_of("mlp_prefill_m64_splitk.md", ops.select_kernel("MatMulNBitsMlp", q["M"], q["K"], q["N"], 4, q["bs"]))}
     if "f32_k2048_m1" in results:
         r, q = results["f32_k2048_m1"], F32
         nbytes = 2_703_360
@@ -540,7 +546,9 @@ def main():
             "workload": "MatMulNBits float32 M=1 K=2048 N=2048 bs=32 packed zp (the CPU-oracle workload, on the GPU)",
             "us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
             "bytes_per_launch": nbytes, "replicas": r["replicas"],
-            "kernel": ops.select_kernel("MatMulNBits", q["M"], q["K"], q["N"], 4, q["bs"], torch.float32, zp="packed")}
+            "kernel": ops.select_kernel("MatMulNBits", q["M"], q["K"], q["N"], 4, q["bs"], torch.float32, zp="packed"),
+            "traffic": traffic_of("f32_k2048_m1_gemv.md", ops.select_kernel("MatMulNBits", q["M"], q["K"], q["N"], 4, q["bs"],
+                                                                              torch.float32, zp="packed"))}
     if "qmoe_mixtral_t1" in results:
         r, q = results["qmoe_mixtral_t1"], QMOE
         nbytes = qmoe_algorithmic_bytes(**q)

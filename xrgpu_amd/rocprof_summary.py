@@ -65,6 +65,8 @@ def main(argv=None):
                     help="*_counter_collection.csv of a further --pmc run (repeatable): every counter recorded "
                          "for the kernel is listed as its per-dispatch mean")
     ap.add_argument("--cus", type=int, default=256, help="compute units, for the MFMA busy fraction")
+    ap.add_argument("--xcds", type=int, default=8,
+                    help="GRBM_GUI_ACTIVE instances summed by rocprofv3 (one per XCD on MI355X)")
     ap.add_argument("--command", required=True, help="the command line that produced the CSVs")
     ap.add_argument("--out", required=True)
     a = ap.parse_args(argv)
@@ -98,12 +100,22 @@ def main(argv=None):
         lines += [""] + [f"{k}_per_dispatch: {statistics.fmean(v):.1f} (n={len(v)})" for k, v in sorted(vals.items())]
         mean = {k: statistics.fmean(v) for k, v in vals.items()}
         if "GRBM_GUI_ACTIVE" in mean:
-            lines.append(f"GRBM_GUI_ACTIVE_per_ns: {mean['GRBM_GUI_ACTIVE'] / st['avg_ns']:.3f}")
-        if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and "GRBM_GUI_ACTIVE" in mean:
-            lines.append(f"mfma_busy_fraction: {mean['SQ_VALU_MFMA_BUSY_CYCLES'] / (mean['GRBM_GUI_ACTIVE'] * a.cus * 4):.4f}"
-                         f"  (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x {a.cus} CUs x 4 SIMDs))")
+            # rocprofv3 sums GRBM_GUI_ACTIVE over the XCDs: the kernel's cycles
+            # are the sum divided by their number
+            cyc = mean["GRBM_GUI_ACTIVE"] / a.xcds
+            lines.append(f"gpu_cycles_per_dispatch: {cyc:.1f}  (GRBM_GUI_ACTIVE / {a.xcds} XCDs)")
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
+                lines.append(f"mfma_busy_fraction: {mean['SQ_VALU_MFMA_BUSY_CYCLES'] / (cyc * a.cus * 4):.4f}"
+                             f"  (SQ_VALU_MFMA_BUSY_CYCLES / (cycles x {a.cus} CUs x 4 SIMDs))")
+        if "SQ_WAVE_CYCLES" in mean and mean["SQ_WAVE_CYCLES"]:
+            for k in ("SQ_WAIT_INST_ANY", "SQ_WAIT_ANY", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_LDS"):
+                if k in mean:
+                    lines.append(f"{k.lower()}_over_wave_cycles: {mean[k] / mean['SQ_WAVE_CYCLES']:.4f}")
         if "SQ_LDS_BANK_CONFLICT" in mean and "SQ_LDS_IDX_ACTIVE" in mean and mean["SQ_LDS_IDX_ACTIVE"]:
             lines.append(f"lds_bank_conflict_over_active: {mean['SQ_LDS_BANK_CONFLICT'] / mean['SQ_LDS_IDX_ACTIVE']:.4f}")
+        if "SQ_INSTS_LDS" in mean and "SQ_VALU_MFMA_BUSY_CYCLES" in mean and mean["SQ_VALU_MFMA_BUSY_CYCLES"]:
+            lines.append(f"lds_instructions_per_mfma: {mean['SQ_INSTS_LDS'] * 32 / mean['SQ_VALU_MFMA_BUSY_CYCLES']:.3f}"
+                         "  (one 32x32x16 fp16 MFMA = 32 busy cycles)")
     lines += ["", "command:", a.command, ""]
     with open(a.out, "w") as f:
         f.write("\n".join(lines))
