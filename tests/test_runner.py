@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-RUNNER = os.path.join(ROOT, "xrgpu_amd", "lib", "xrmm_execute")
+# XRMM_EXECUTE selects another build of the runner (the host-sanitizer build)
+RUNNER = os.environ.get("XRMM_EXECUTE") or os.path.join(ROOT, "xrgpu_amd", "lib", "xrmm_execute")
 
 
 def run_job(tmp_path, job, name="job.json"):
@@ -96,3 +97,45 @@ def test_malformed_json(tmp_path):
     assert r.returncode == 1 and "Invalid invocation JSON" in json.loads(r.stderr)["error"]
     r = subprocess.run([RUNNER], capture_output=True, text=True, timeout=60)
     assert r.returncode == 1 and "Usage" in json.loads(r.stderr)["error"]
+
+
+def _fuzz_cases():
+    """Seeded malformed job files: every truncation point of a valid job (every
+    7th byte), single-byte substitutions with JSON-significant characters,
+    and hand-picked hostile inputs (deep nesting, huge numbers, bad escapes,
+    bytes that are not UTF-8, oversized shapes)."""
+    base = json.dumps(mnb_job(M=1, K=32, N=2, bs=32)).encode()
+    rng = np.random.default_rng(20261202)
+    cases = [base[:n] for n in range(0, len(base), 7)]
+    subs = b'{}[]",:\\0-eE.+ \x00\xff'
+    for _ in range(60):
+        b = bytearray(base)
+        i = int(rng.integers(len(b)))
+        b[i] = subs[int(rng.integers(len(subs)))]
+        cases.append(bytes(b))
+    cases += [
+        b"[" * 200000, b"{\"a\":" * 100000, b"\"" + b"\\" * 99999, b"1e99999", b"-", b"-0e-99999",
+        b"{\"operation\": \"\\ud800\"}", b"{\"operation\": \"\\u00zz\"}", b"{\"operation\": \"\x80\xfe\"}",
+        b"{\"operation\": 1e400, \"inputs\": [], \"attrs\": {}}",
+        base.replace(b"[1, 64]", b"[4294967297, 4294967297]").replace(b"\"shape\": [1, 32]",
+                                                                       b"\"shape\": [9223372036854775807, 3]"),
+        base.replace(b"\"N\": 2", b"\"N\": -1"), base.replace(b"\"N\": 2", b"\"N\": 1.5e300"),
+        base.replace(b"\"block_size\": 32", b"\"block_size\": 0"),
+        base + b" trailing", b"\xef\xbb\xbf" + base, b"",
+    ]
+    return cases
+
+
+def test_parser_fuzz_never_crashes(tmp_path):
+    """The runner reads untrusted job files: every malformed input ends in exit
+    status 0 or 1 with a JSON error object, never in a signal (the same test
+    runs against the AddressSanitizer / UBSan build of the runner)."""
+    if not os.path.exists(RUNNER):
+        pytest.fail("xrmm_execute is not built (python -m xrgpu_amd.build)")
+    path = tmp_path / "fuzz.json"
+    for i, data in enumerate(_fuzz_cases()):
+        path.write_bytes(data)
+        r = subprocess.run([RUNNER, str(path)], capture_output=True, timeout=60)
+        assert r.returncode in (0, 1), (i, data[:80], r.returncode, r.stderr[-400:])
+        if r.returncode == 1:
+            assert "error" in json.loads(r.stderr.decode("utf-8", "replace")), (i, r.stderr[-200:])

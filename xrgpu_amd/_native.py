@@ -10,7 +10,9 @@ import os
 import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libxrmm.so")
+# XRMM_LIB_PATH selects another build of the same ABI (the host-sanitizer
+# build of xrgpu_amd/build_sanitized.py)
+LIB_PATH = os.environ.get("XRMM_LIB_PATH") or os.path.join(HERE, "lib", "libxrmm.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "xrmm.h")
 
 XRMM_OK, XRMM_EINVAL, XRMM_EDEVICE = 0, 1, 2

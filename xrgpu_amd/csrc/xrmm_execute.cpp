@@ -71,6 +71,18 @@ struct Json {
 struct Parser {
   const std::string& s;
   size_t p = 0;
+  // Nesting depth of the value being parsed. value() recurses per level, so
+  // unbounded nesting in an untrusted file would overflow the stack; job
+  // files nest four levels deep.
+  int depth = 0;
+  static constexpr int kMaxDepth = 64;
+  struct Nest {
+    Parser& q;
+    explicit Nest(Parser& p_) : q(p_) {
+      if (++q.depth > kMaxDepth) q.bad("nesting too deep");
+    }
+    ~Nest() { --q.depth; }
+  };
 
   [[noreturn]] void bad(const char* what) const {
     throw std::invalid_argument(std::string("Invalid invocation JSON: ") + what + " at offset " + std::to_string(p));
@@ -149,6 +161,7 @@ struct Parser {
     Json v;
     const char c = s[p];
     if (c == '{') {
+      const Nest nest(*this);
       v.kind = Json::Object;
       ++p;
       ws();
@@ -172,6 +185,7 @@ struct Parser {
       }
     }
     if (c == '[') {
+      const Nest nest(*this);
       v.kind = Json::Array;
       ++p;
       ws();
