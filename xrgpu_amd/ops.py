@@ -23,23 +23,33 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
-def _stream(stream=None):
-    s = stream if stream is not None else torch.cuda.current_stream()
-    return s.cuda_stream
+# The current stream's raw handle without building a torch.cuda.Stream object
+# (a per-call cost of several microseconds on the eager path).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream(stream=None, device=None):
+    if stream is not None:
+        return stream.cuda_stream
+    if _raw_stream is not None:
+        return _raw_stream(device if device is not None and device >= 0 else torch.cuda.current_device())
+    return torch.cuda.current_stream().cuda_stream
 
 
 def _check_dev(*ts):
-    dev = None
+    """Every tensor on one GPU and contiguous; returns the device index."""
+    dev = -2
     for t in ts:
         if t is None:
             continue
-        if not t.is_cuda:
+        d = t.get_device()  # -1 on the CPU
+        if d < 0:
             raise nat.XrmmInvalid("tensors must be on the GPU")
         if not t.is_contiguous():
             raise nat.XrmmInvalid("tensors must be contiguous")
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
+        if dev == -2:
+            dev = d
+        elif d != dev:
             raise nat.XrmmInvalid("tensors must share one device")
     return dev
 
@@ -117,12 +127,12 @@ def matmul_nbits(A, B, scales, zero_points=None, bias=None, *, K=None, N=None, b
         raise nat.XrmmInvalid("bias must be [N] of A's dtype")
     M = A.numel() // K
     _check_out(out, tuple(A.shape[:-1]) + (N,), A.dtype)
-    _check_dev(A, B, scales, zero_points, bias, out)
+    dev = _check_dev(A, B, scales, zero_points, bias, out)
     if out is None:
         out = torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
     nat.check(nat.lib().xrmm_matmul_nbits(_ptr(A), _ptr(B), _ptr(scales), _ptr(zero_points),
                                           _zp_dtype(zero_points), _ptr(bias), _ptr(out), M, K, N,
-                                          bits, block_size, _t1(A), _stream(stream)))
+                                          bits, block_size, _t1(A), _stream(stream, dev)))
     return out
 
 
@@ -146,7 +156,7 @@ def matmul_nbits_qkv(A, q_B, q_scales, k_B, k_scales, v_B, v_scales, *, norm_sca
     if norm_scale is None:
         raise nat.XrmmInvalid("Missing complex input: normScaleT")
     _check_aux(norm_scale, (K,), A.dtype, "norm_scale")
-    _check_dev(A, skip, norm_scale, q_B, q_scales, k_B, k_scales, v_B, v_scales, *zps)
+    dev = _check_dev(A, skip, norm_scale, q_B, q_scales, k_B, k_scales, v_B, v_scales, *zps)
     lead = tuple(A.shape[:-1])
     Q = torch.empty(lead + (Nq,), dtype=A.dtype, device=A.device)
     Ko = torch.empty(lead + (Nkv,), dtype=A.dtype, device=A.device)
@@ -155,7 +165,7 @@ def matmul_nbits_qkv(A, q_B, q_scales, k_B, k_scales, v_B, v_scales, *, norm_sca
     nat.check(nat.lib().xrmm_matmul_nbits_qkv(
         _ptr(A), _ptr(skip), _ptr(norm_scale), _ptr(q_B), _ptr(q_scales), _ptr(zps[0]), _ptr(k_B),
         _ptr(k_scales), _ptr(zps[1]), _ptr(v_B), _ptr(v_scales), _ptr(zps[2]), zdt, _ptr(Q), _ptr(Ko),
-        _ptr(V), _ptr(R), M, K, Nq, Nkv, bits, block_size, float(epsilon), _t1(A), _stream(stream)))
+        _ptr(V), _ptr(R), M, K, Nq, Nkv, bits, block_size, float(epsilon), _t1(A), _stream(stream, dev)))
     return Q, Ko, V, R
 
 
@@ -178,14 +188,14 @@ def matmul_nbits_mlp(A, gate_B, gate_scales, up_B, up_scales, *, skip=None, norm
     _check_aux(norm_scale, (K,), A.dtype, "norm_scale")
     _check_aux(gate_bias, (N,), A.dtype, "gate_bias")
     _check_aux(up_bias, (N,), A.dtype, "up_bias")
-    _check_dev(A, skip, norm_scale, gate_B, gate_scales, up_B, up_scales, gate_bias, up_bias,
+    dev = _check_dev(A, skip, norm_scale, gate_B, gate_scales, up_B, up_scales, gate_bias, up_bias,
                gate_zero_points, up_zero_points)
     Y = torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
     R = torch.empty_like(A) if want_residual else None
     nat.check(nat.lib().xrmm_matmul_nbits_mlp(
         _ptr(A), _ptr(skip), _ptr(norm_scale), _ptr(gate_B), _ptr(gate_scales), _ptr(gate_zero_points),
         _ptr(gate_bias), _ptr(up_B), _ptr(up_scales), _ptr(up_zero_points), _ptr(up_bias), zdt, _ptr(Y),
-        _ptr(R), M, K, N, bits, block_size, float(epsilon), nat.ACT[activation], _t1(A), _stream(stream)))
+        _ptr(R), M, K, N, bits, block_size, float(epsilon), nat.ACT[activation], _t1(A), _stream(stream, dev)))
     return Y, R
 
 
@@ -193,12 +203,12 @@ def dequantize(B, scales, zero_points=None, *, K, bits=4, block_size=32, out_dty
                stream=None):
     """Dequantized ``W[N, K]``: float32 reference value or its one-rounding fp16."""
     N = int(B.shape[0])
-    _check_dev(B, scales, zero_points)
+    dev = _check_dev(B, scales, zero_points)
     _check_weights(B, scales, zero_points, N, K, bits, block_size, scales.dtype)
     W = torch.empty((N, K), dtype=out_dtype, device=B.device)
     nat.check(nat.lib().xrmm_dequantize(_ptr(B), _ptr(scales), _ptr(zero_points), _zp_dtype(zero_points),
                                         _ptr(W), N, K, bits, block_size, _T1[scales.dtype], _T1[out_dtype],
-                                        _stream(stream)))
+                                        _stream(stream, dev)))
     return W
 
 
@@ -223,7 +233,7 @@ def qmoe(x, router, fc1, fc1_scales, fc2, fc2_scales, *, k=1, activation="relu",
     """
     if activation not in ("relu", "swiglu"):
         raise nat.XrmmInvalid("Invalid quantized SwiGLU fusion")
-    _check_dev(x, router, fc1, fc1_scales, fc2, fc2_scales, workspace)
+    dev = _check_dev(x, router, fc1, fc1_scales, fc2, fc2_scales, workspace)
     for t, dt, nm in ((x, torch.float32, "input"), (router, torch.float32, "router"), (fc1, torch.uint8, "fc1"),
                       (fc2, torch.uint8, "fc2"), (fc1_scales, torch.float32, "fc1 scales"),
                       (fc2_scales, torch.float32, "fc2 scales")):
@@ -252,7 +262,7 @@ def qmoe(x, router, fc1, fc1_scales, fc2, fc2_scales, *, k=1, activation="relu",
         _ptr(x), _ptr(router), _ptr(fc1), _ptr(fc1_scales), _ptr(fc2), _ptr(fc2_scales), _ptr(y), _ptr(workspace),
         workspace.numel(), T, H, E, F1, int(k), int(expert_weight_bits), int(block_size), act, int(swiglu_fusion),
         float(activation_alpha), float(activation_beta), float(swiglu_limit or 0.0), int(swiglu_limit is not None),
-        _stream(stream)))
+        _stream(stream, dev)))
     return y
 
 
@@ -297,14 +307,14 @@ def gather_block_quantized(data, indices, scales, zero_points=None, *, bits=4, b
         raise nat.XrmmInvalid("Unsupported GatherBlockQuantized geometry")
     if zero_points is not None and tuple(zero_points.shape) != (rows, (blocks * bits + 7) // 8):
         raise nat.XrmmInvalid("Unsupported GatherBlockQuantized geometry")
-    _check_dev(data, indices, scales, zero_points, status)
+    dev = _check_dev(data, indices, scales, zero_points, status)
     data, indices, scales = data.contiguous(), indices.contiguous(), scales.contiguous()
     out = torch.empty((int(indices.shape[0]), width), dtype=torch.float32, device=data.device)
     if status is None:
         status = torch.zeros(1, dtype=torch.int32, device=data.device)
     nat.check(nat.lib().xrmm_gather_block_quantized(
         _ptr(data), _ptr(indices), _IDX[indices.dtype], _ptr(scales), _ptr(zero_points), _ptr(out), _ptr(status),
-        rows, pcols, int(indices.shape[0]), int(bits), int(block_size), _stream(stream)))
+        rows, pcols, int(indices.shape[0]), int(bits), int(block_size), _stream(stream, dev)))
     if check:
         code = int(status.item())
         if code:
@@ -328,11 +338,11 @@ def matmul_bnb4(A, B, absmax, *, K, N, block_size=32, quant_type=1, trans_b=1, o
         raise nat.XrmmInvalid("Invalid packed matmul geometry")
     M = int(A.shape[0])
     _check_out(out, (M, N), A.dtype)
-    _check_dev(A, B, absmax, out)
+    dev = _check_dev(A, B, absmax, out)
     A, B, absmax = A.contiguous(), B.contiguous(), absmax.contiguous()
     Y = out if out is not None else torch.empty((M, N), dtype=A.dtype, device=A.device)
     nat.check(nat.lib().xrmm_matmul_bnb4(_ptr(A), _ptr(B), _ptr(absmax), _ptr(Y), M, K, N, int(block_size),
-                                         int(quant_type), int(trans_b), _T1[A.dtype], _stream(stream)))
+                                         int(quant_type), int(trans_b), _T1[A.dtype], _stream(stream, dev)))
     return Y
 
 
@@ -361,7 +371,7 @@ def matmul_nbits_int8a(A, B, scales, zero_points=None, bias=None, *, K, N, bits=
     A2 = A.reshape(-1, K).contiguous()
     M = int(A2.shape[0])
     _check_out(out, tuple(A.shape[:-1]) + (N,), A.dtype)
-    _check_dev(A, B, scales, zero_points, bias, out, workspace)
+    dev = _check_dev(A, B, scales, zero_points, bias, out, workspace)
     Y = out if out is not None else torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
     need = int(nat.lib().xrmm_matmul_nbits_int8a_workspace_bytes(M, K))
     if need < 0:
@@ -371,7 +381,7 @@ def matmul_nbits_int8a(A, B, scales, zero_points=None, bias=None, *, K, N, bits=
     nat.check(nat.lib().xrmm_matmul_nbits_int8a(
         _ptr(A2), _ptr(B), _ptr(scales), _ptr(zero_points), nat.U8 if zero_points is not None else nat.UNSPECIFIED,
         _ptr(bias), _ptr(Y), _ptr(workspace), workspace.numel(), M, K, N, bits, block_size, _T1[A.dtype],
-        _stream(stream)))
+        _stream(stream, dev)))
     return Y
 
 
@@ -392,11 +402,11 @@ def matmul_nbits_int8a_noalloc(A, B, scales, zero_points=None, bias=None, *, K, 
         raise nat.XrmmInvalid("bias must be [N] of A's dtype")
     M = A.numel() // K
     _check_out(out, tuple(A.shape[:-1]) + (N,), A.dtype)
-    _check_dev(A, B, scales, zero_points, bias, out)
+    dev = _check_dev(A, B, scales, zero_points, bias, out)
     Y = out if out is not None else torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
     nat.check(nat.lib().xrmm_matmul_nbits_int8a_noalloc(
         _ptr(A), _ptr(B), _ptr(scales), _ptr(zero_points), nat.U8 if zero_points is not None else nat.UNSPECIFIED,
-        _ptr(bias), _ptr(Y), M, K, N, bits, block_size, _T1[A.dtype], _stream(stream)))
+        _ptr(bias), _ptr(Y), M, K, N, bits, block_size, _T1[A.dtype], _stream(stream, dev)))
     return Y
 
 
@@ -411,9 +421,9 @@ def int8a_workspace_bytes(M, K) -> int:
 def stream_read(buf, *, loads_per_lane=4, sink=None, stream=None):
     """Read ``buf`` (a device tensor of a multiple of 16 bytes) once on the GPU
     with 16-byte loads: the plain read rate a decode GEMV is compared with."""
-    _check_dev(buf, sink)
+    dev = _check_dev(buf, sink)
     if sink is None:
         sink = torch.zeros(1, dtype=torch.int32, device=buf.device)
     nat.check(nat.lib().xrmm_stream_read(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink),
-                                         int(loads_per_lane), _stream(stream)))
+                                         int(loads_per_lane), _stream(stream, dev)))
     return sink
