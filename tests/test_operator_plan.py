@@ -200,7 +200,9 @@ def gbq_ins(rows=10, pcols=32, n=5, bits=4, bs=16, idx="int64", zp=False):
 def test_gbq_plan_and_checks():
     outs = op.plan(op.Request(GBQ, gbq_ins(), attrs={"bits": 4, "block_size": 16}))
     assert [(t.name, t.shape, t.dtype) for t in outs] == [("outputT", (5, 64), "float32")]
-    assert op.plan(op.Request(GBQ, gbq_ins(idx="int32", zp=True), attrs={"bits": 4, "block_size": 16}))[0].shape == (5, 64)
+    assert op.plan(op.Request(GBQ, gbq_ins(zp=True), attrs={"bits": 4, "block_size": 16}))[0].shape == (5, 64)
+    with pytest.raises(op.XrmmInvalid, match="Logical dtype outside frozen contract: indicesT"):
+        op.plan(op.Request(GBQ, gbq_ins(idx="int32"), attrs={"block_size": 16}))  # Tind = int64 (contract_data.h:660)
     assert op.plan(op.Request(GBQ, gbq_ins(bs=128, bits=8), attrs={"bits": 8}))[0].shape == (5, 32)  # defaults
     for attrs in ({"bits": 2, "block_size": 16}, {"block_size": 8}, {"block_size": 48}, {"block_size": 16, "gather_axis": 1},
                   {"block_size": 16, "quantize_axis": 0}):

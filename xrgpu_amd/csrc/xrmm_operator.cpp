@@ -103,7 +103,10 @@ constexpr uint32_t kU8 = 1u << XRMM_U8;
 constexpr uint32_t kT3 = kT1 | kU8;  // float zero points (reference) or packed uint8 (extension)
 constexpr uint32_t kF32 = 1u << XRMM_F32;
 // int64 indices (the reference contract) and int32 / uint32 (read as int32 by controlIndex)
-constexpr uint32_t kIdx = (1u << XRMM_I64) | (1u << XRMM_I32) | (1u << XRMM_U32);
+// GatherBlockQuantized indices: Tind = int64 in the reference contract
+// (contract_data.h:660); int32 / uint32 indices are taken only by the
+// zero-copy entry point.
+constexpr uint32_t kIdx = 1u << XRMM_I64;
 // operators outside the MatMulNBits family (xrmm::Op covers that family)
 constexpr int OP_BNB4 = 10, OP_QMOE = 11, OP_GBQ = 12;
 
