@@ -531,12 +531,13 @@ inline hipError_t launch_sk5(const Launch& L, hipStream_t st) {
   a.zesz = L.zp_dtype == DT_F32 ? 4u : 2u;
   a.tiles = static_cast<uint32_t>(tiles);
   const int64_t cus = sk_num_cus();
-  // Tiles per workgroup: spread over the CUs, but at least four with several
-  // row chunks, whose workgroups each stage their chunk's activations (Mlp,
-  // 64 rows, K = 2048, N = 5632: 32.5 us at four tiles against 40.3 us at
-  // three; fewer tiles per workgroup measured slower on every shape).
-  int64_t tpw = (tiles + cus - 1) / cus;
-  if (L.M > 16 && tpw < 4) tpw = 4;
+  // Tiles per workgroup: one workgroup per CU at a time (its LDS holds every
+  // wave's partial tiles), so the grid of tile groups x row chunks is sized
+  // to one round of the CUs; every workgroup stages its chunk's activations,
+  // so fewer, larger groups also stage less (Mlp, K = 2048, N = 5632, 32
+  // rows: 13.4 us with 240 workgroups against 21.7 us with 352; Qkv, 64 rows:
+  // 23.2 against 37.5 us).
+  int64_t tpw = ((tiles * ((L.M + 15) / 16)) + cus - 1) / cus;
   tpw = tpw < 1 ? 1 : tpw > sk_tmax(W) ? sk_tmax(W) : tpw;
   a.tpw = static_cast<uint32_t>(tpw);
   a.chunks = static_cast<uint32_t>((L.M + 15) / 16);
