@@ -35,9 +35,9 @@
 // and the factor multiplies the row totals at the end. The workgroup's one
 // barrier before the MFMAs publishes the tile's scales / zero points.
 //
-// End. The four k-group lanes of a column add their sums (two exchanges), the
-// W waves' partial tiles meet in LDS after one barrier, and 16 x M threads add
-// them, add the bias and store.
+// End. Every lane's partial sums (its column, its k-group, four rows) meet in
+// LDS after one barrier, and 16 x M threads add the 4 W of them, add the bias
+// (or apply the RMS factor) and store.
 #pragma once
 #include "xrmm_gemv_dot.h"
 
@@ -47,6 +47,15 @@ namespace xrmm {
 __device__ __forceinline__ float mq_wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Sum over each row of 16 lanes; every lane of the row receives it.
+__device__ __forceinline__ float mq_row16_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));  // row_mirror
   return v;
 }
 
@@ -98,8 +107,12 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
   constexpr uint32_t SLICE = mq_slice_bytes<J>();
   constexpr uint32_t ROWB = mq_row_stride<J>();  // LDS row stride of the slice
   __shared__ __align__(16) unsigned char act[W][SLICE];
-  __shared__ float part[W][4][16];
-  __shared__ float red[QKV ? W : 1][4];
+  // partial sums: [row i][column n][wave w, k-group g] with a padded column
+  // stride, so the 16 columns' writes spread over the banks and an output
+  // thread reads its 4 W values as 16-byte pieces
+  constexpr int PST = ((4 * W + 3) / 4) * 4 + 4;
+  __shared__ __align__(16) float part[4][16][PST];
+  __shared__ float red[QKV ? W : 1][4][4];  // per wave, row and 16-lane row of the wave
   __shared__ __align__(16) unsigned char meta_s[MQ_META_LOADS * W * 64 * 16];
   __shared__ __align__(16) unsigned char meta_z[ZPK == ZP_PACKED ? MQ_META_LOADS * W * 64 * 16 : 16];
 
@@ -230,14 +243,18 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
       if (SK && write_res && static_cast<int>(r) < M && k < K) *reinterpret_cast<f16x8*>(res + r * K + k) = rv;
       if (!SK && write_res && static_cast<int>(r) < M && k < K) *reinterpret_cast<u32x4*>(res + r * K + k) = ar[q];
     }
+    // the rows' partial sums of squares, one per 16-lane row of the wave (the
+    // end adds them up with the waves')
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const float t = wave_total(sq[rr]);
-      if (lane == 0) red[wave][rr] = t;
+      const float t = mq_row16_sum(sq[rr]);
+      if ((lane & 15) == 0) red[wave][rr][lane >> 4] = t;
     }
-    // (NaN compares false: a NaN row stays NaN through the unscaled path)
-    const float wmx = mq_wave_max(mx);
-    if (wmx > 32768.f) {
+    // Rescale only when some |u| exceeds 32768 (a ballot; the wave-wide
+    // maximum is taken only then). NaN compares false: a NaN row stays NaN
+    // through the unscaled path.
+    if (__builtin_amdgcn_ballot_w64(mx > 32768.f) != 0) {
+      const float wmx = mq_wave_max(mx);
       int e = 0;
       (void)__builtin_frexpf(wmx / 32768.f, &e);
       escale = __builtin_ldexpf(1.f, e);
@@ -319,26 +336,24 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
 
   // ---- the four k-group lanes of a column, then the waves
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    y[i] += __shfl_xor(y[i], 16, 64);
-    y[i] += __shfl_xor(y[i], 32, 64);
-  }
-  if (g == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) part[wave][i][n] = y[i] * escale;
-  }
+  for (int i = 0; i < 4; ++i) part[i][n][wave * 4 + g] = y[i] * escale;
   __syncthreads();
   if (tid < 64) {
     const uint32_t i = static_cast<uint32_t>(tid) >> 4, nn = static_cast<uint32_t>(tid) & 15u;
     const uint32_t c = col0 + nn;
     if (static_cast<int>(i) < M && c < N) {
-      float t = 0.f;
+      float t4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int w = 0; w < W; ++w) t += part[w][i][nn];
+      for (int w = 0; w < W; ++w) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(&part[i][nn][w * 4]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) t4[q] += v[q];
+      }
+      float t = (t4[0] + t4[1]) + (t4[2] + t4[3]);
       if constexpr (QKV) {
         float sq = 0.f;
 #pragma unroll
-        for (int w = 0; w < W; ++w) sq += red[w][i];
+        for (int w = 0; w < W; ++w) sq += (red[w][i][0] + red[w][i][1]) + (red[w][i][2] + red[w][i][3]);
         t *= __builtin_amdgcn_rsqf(sq / static_cast<float>(K) + a.eps);
       } else {
         if (a.bias) t += static_cast<float>(static_cast<const f16*>(a.bias)[c]);
