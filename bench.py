@@ -30,7 +30,7 @@ FP16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, published
 PROFILES = os.path.join(ROOT, "profiles")
 SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048": 4, "qmoe_mixtral_t1": 6,
          "bnb4_nf4_m1": 7, "gbq_embed_t2048": 8, "int8a_decode_m1": 1, "f32_k2048_m1": 0,
-         "mlp_prefill_m64": 9}
+         "mlp_prefill_m64": 9, "prefill_m2048_prepacked": 4}
 # The CPU-oracle workload on the GPU: MatMulNBits float32, M=1, K=N=2048,
 # block_size 32, packed zero points (2,703,360 algorithmic bytes per call)
 F32 = dict(M=1, K=2048, N=2048, bs=32)
@@ -85,7 +85,7 @@ def make_replicas(torch, name, R, dev, seed):
                              S=torch.rand((N, kb), device=dev, generator=g) * 0.019 + 0.001,
                              Z=torch.randint(0, 256, (N, (kb + 1) // 2), dtype=torch.uint8, device=dev, generator=g)))
         return dict(A=A, reps=reps, K=K, N=N, bs=bs)
-    if name == "prefill_m2048":
+    if name in ("prefill_m2048", "prefill_m2048_prepacked"):
         M, K, N, bs = 2048, 4096, 14336, 128
         kb = K // bs
         A = torch.randn((M, K), device=dev, generator=g).half()
@@ -176,6 +176,19 @@ def step_fn(ops, name, w):
         def f(i):
             r = reps[i % len(reps)]
             return ops.matmul_nbits(A, r["B"], r["S"], r["Z"], r["bias"], block_size=w["bs"], out=Y)
+        return f
+    if name == "prefill_m2048_prepacked":
+        # the weights are prepacked once, before any timing (the request
+        # lifecycle does the same at prepare)
+        Y = torch.empty((w["M"], w["N"]), dtype=torch.float16, device=A.device)
+        packed = [ops.prepack_weights(r["B"], K=w["K"], block_size=w["bs"]) for r in reps]
+        for r in reps:
+            del r["B"]
+
+        def f(i):
+            r = reps[i % len(reps)]
+            return ops.matmul_nbits_prepacked(A, packed[i % len(reps)], r["S"], r["Z"], r["bias"], K=w["K"],
+                                              N=w["N"], block_size=w["bs"], out=Y)
         return f
     if name == "qkv_gqa_m4":
         def f(i):
@@ -451,18 +464,18 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     results = {}
-    names = ["decode_up_m1", "prefill_m2048", "qkv_gqa_m4", "mlp_swiglu_m16", "mlp_prefill_m64", "f32_k2048_m1",
+    names = ["decode_up_m1", "prefill_m2048", "prefill_m2048_prepacked", "qkv_gqa_m4", "mlp_swiglu_m16", "mlp_prefill_m64", "f32_k2048_m1",
              "qmoe_mixtral_t1", "bnb4_nf4_m1", "gbq_embed_t2048", "int8a_decode_m1"]
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
     for name in names:
         # every leg rotates more weight bytes than the 256 MB Infinity Cache
         # holds (Qkv: 24 x 13.7 MB = 328 MB)
-        R = {"prefill_m2048": 2, "qmoe_mixtral_t1": 2, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24,
+        R = {"prefill_m2048": 2, "prefill_m2048_prepacked": 2, "qmoe_mixtral_t1": 2, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24,
              "f32_k2048_m1": 100, "mlp_prefill_m64": 24}.get(name, args.replicas)
         w = make_replicas(torch, name, R, dev, seed=SEEDS[name])
         fn = step_fn(ops, name, w)
-        steps = args.steps if name != "prefill_m2048" else max(10, args.steps // 10)
+        steps = args.steps if not name.startswith("prefill_m2048") else max(10, args.steps // 10)
         ms, eager_ms, wall_ms = time_steps(torch, fn, steps, args.warmup)
         p10, p50, p90 = per_launch_percentiles(torch, fn, min(100, steps), 5)
         wl = workloads.make(name, scale_down=1) if name == "decode_up_m1" else None
@@ -521,6 +534,15 @@ def main():
                                        "traffic": traffic_of("prefill_m2048_gemm.md", ops.select_kernel(
                                            "MatMulNBits", 2048, 4096, 14336, 4, 128, zp="packed"))},
                           "dense_fp16_library": dense_fp16_reference(torch)}
+    if "prefill_m2048_prepacked" in results:
+        r = results["prefill_m2048_prepacked"]
+        fl = 2 * 2048 * 4096 * 14336
+        tf = fl / (r["ms"] * 1e-3) / 1e12
+        out.setdefault("prefill", {})["prepacked"] = {
+            "workload": "the same call on weights prepacked once by xrmm_prepack_weights (what the request "
+                        "lifecycle does at prepare)",
+            "us": round(r["ms"] * 1e3, 2), "tflops": round(tf, 2), "frac": round(tf / FP16_PEAK_TFLOPS, 4),
+            "kernel": "gemm_q4_big (prepacked weights)"}
     for name, nbytes, summary, kern in (
             ("qkv_gqa_m4", 13_656_064, "qkv_gqa_m4_gemv.md",
              ops.select_kernel("MatMulNBitsQkv", 4, 4096, 4096, 4, 64, zp="packed")),

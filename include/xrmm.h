@@ -83,6 +83,30 @@ int xrmm_matmul_nbits(const void* A, const void* B, const void* scales, const vo
                       int32_t zp_dtype, const void* bias, void* Y, int64_t M, int64_t K,
                       int64_t N, int32_t bits, int32_t block_size, int32_t dtype, void* stream);
 
+/* Offline weight prepack for the prefill GEMM. The reference has no
+ * counterpart in code; it is the "prepare = upload / prepack" step of its
+ * Operator lifecycle (kernels/_shared/extended/vulkan.cpp:119) for callers
+ * that hold their weights on the device. The 4-bit codes of B [N,kb,blob]
+ * are rewritten K-step-major ([ceil(kb*block_size/64)][N][32 bytes], a K step
+ * being 64 codes) with the codes of each 32-bit word reordered so that the
+ * GEMM dequantises in natural k order; scales and zero points keep their
+ * layout. xrmm_prepacked_bytes returns the packed size, 0 when the geometry
+ * has none (bits other than 4, or columns not of whole 32-code chunks).
+ * Both pointers 16-byte aligned. */
+int64_t xrmm_prepacked_bytes(int64_t N, int64_t K, int32_t bits, int32_t block_size);
+int xrmm_prepack_weights(const void* B, void* packed, int64_t N, int64_t K, int32_t bits,
+                         int32_t block_size, void* stream);
+
+/* xrmm_matmul_nbits with B prepacked by xrmm_prepack_weights (float16 A and
+ * outputs, 4-bit codes, power-of-two block_size >= 16, K a multiple of 8,
+ * 16-byte aligned tensors; other geometries return XRMM_EINVAL). Runs the
+ * 256 x 256 prefill GEMM for every M. The request lifecycle (xrmm_prepare)
+ * prepacks by itself for MatMulNBits requests that reach that GEMM. */
+int xrmm_matmul_nbits_prepacked(const void* A, const void* packed, const void* scales,
+                                const void* zero_points, int32_t zp_dtype, const void* bias, void* Y,
+                                int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size,
+                                int32_t dtype, void* stream);
+
 /* com.microsoft.MatMulNBitsQkv, opcode 1028 (complex_kernel.glsl:81,83;
  * complex_plan.cpp:37,119). x = RMSNorm(A + skip) * norm_scale (eps), then
  * Q = x Wq^T [M,Nq], K = x Wk^T [M,Nkv], V = x Wv^T [M,Nkv]; residual

@@ -114,3 +114,19 @@ def test_qkv_requires_norm_scale():
 def test_kernel_selection(op, M, K, N, bs, dtype, zp, expect):
     r = nat.lib().xrmm_select_kernel(op, M, K, N, 4, bs, dtype, zp)
     assert r.decode() == expect
+
+
+def test_prepack_sizes_and_validation_without_device():
+    lib = nat.lib()
+    assert lib.xrmm_prepacked_bytes(14336, 4096, 4, 128) == 14336 * 4096 // 2
+    assert lib.xrmm_prepacked_bytes(100, 96, 4, 32) == 2 * 100 * 32      # a K step and a half: the half is padded
+    assert lib.xrmm_prepacked_bytes(100, 20, 4, 16) == 100 * 32          # one chunk of 32 codes
+    assert lib.xrmm_prepacked_bytes(8, 64, 8, 32) == 0                   # 8-bit codes have no packed layout
+    assert lib.xrmm_prepacked_bytes(8, 64, 4, 8) == 0                    # 16-code columns are not whole chunks
+    rc = lib.xrmm_prepack_weights(None, None, 8, 64, 8, 32, None)
+    assert rc == nat.XRMM_EINVAL and "4-bit" in nat.last_error()
+    rc = lib.xrmm_prepack_weights(None, None, 8, 64, 4, 32, None)
+    assert rc == nat.XRMM_EINVAL and "null" in nat.last_error()
+    rc = lib.xrmm_matmul_nbits_prepacked(None, None, None, None, nat.UNSPECIFIED, None, None, 0, 64, 8, 4, 32,
+                                         nat.F16, None)
+    assert rc == nat.XRMM_OK  # M = 0: nothing to do

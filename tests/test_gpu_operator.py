@@ -49,6 +49,27 @@ def test_matmul_lifecycle_matches_oracle(gpu, M, K, N, bs):
     assert "gfx950" in info["device"]
 
 
+def test_prefill_lifecycle_prepacks_the_weights(gpu):
+    """A request that reaches the 256 x 256 GEMM (512 rows, 128 tiles) gets
+    its weights prepacked at prepare; the result meets the oracle, and a
+    memory limit that leaves no room for the packed copy runs the unpacked
+    GEMM with the same tolerance."""
+    rng = np.random.default_rng(77)
+    M, K, N, bs = 512, 128, 16384, 64
+    ins = rand_mnb(rng, M, K, N, bs)
+    ref = O.matmul_nbits(ins["aT"], ins["bT"], ins["scalesT"], ins["zeroPointsT"], ins["biasT"], K=K, N=N,
+                         block_size=bs)
+    arena = sum(v.nbytes for v in ins.values()) + M * N * 2
+    for limit, kernel in ((256 << 20, "gemm_q4_big_prepacked"), (arena + (64 << 10), "gemm_q4_big")):
+        with op.Operator.prepare("", request(MNB, ins, {"N": N, "block_size": bs}),
+                                 op.Options(memory_limit_bytes=limit)) as o:
+            o.run()
+            (y,) = o.read_outputs()
+            assert o.info()["kernel"] == kernel
+        ok, err, lim = O.tolerance_ok(y.data, ref, np.float16)
+        assert ok, (kernel, err, lim)
+
+
 def test_requested_float32_storage_holds_the_float16_values(gpu):
     rng = np.random.default_rng(1)
     ins = rand_mnb(rng, 2, 256, 64, 32)

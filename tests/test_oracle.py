@@ -372,3 +372,32 @@ def test_nonfinite_policy_matches_serial_order(zp):
     assert np.isnan(y).any() and np.isposinf(y).any() and np.isneginf(y).any()
     assert np.all(np.isfinite(y[4:]))
     assert O.tolerance_ok(ys, y, np.float32)[0]
+
+
+@pytest.mark.parametrize("N,K,bs", [(37, 96, 32), (5, 20, 16), (16, 256, 128), (3, 4096, 64), (7, 200, 32)])
+def test_prepack_layout_decodes_to_the_codes(N, K, bs):
+    """The prefill GEMM's prepacked layout, decoded the way the GEMM reads it
+    (per word, exponent-bias pairs from nibble slots 0/4, 1/5, 2/6, 3/7 in
+    k order; K step s of column n at bytes (s N + n) 32 .. + 31), gives back
+    oracle.unpack_codes; the padding half past the last chunk is zero."""
+    from oracle import prepack as PK
+    rng = np.random.default_rng(N * 7 + K + bs)
+    kb = O.k_blocks(K, bs)
+    B = rng.integers(0, 256, size=(N, kb, O.blob_bytes(bs, 4)), dtype=np.uint8)
+    flat = PK.prepack_q4(B, K, bs)
+    assert flat.size == PK.packed_bytes(N, K, bs)
+    Kp = kb * bs
+    ksteps = (Kp + 63) // 64
+    codes = np.zeros((N, ksteps * 64), dtype=np.uint8)
+    for s in range(ksteps):
+        for n in range(N):
+            piece = flat[(s * N + n) * 32:(s * N + n) * 32 + 32]
+            for w in range(8):
+                word = int.from_bytes(bytes(piece[4 * w:4 * w + 4]), "little")
+                slots = [(word >> (4 * j)) & 15 for j in range(8)]
+                for pair in range(4):  # the GEMM's pair p yields k = 2p, 2p + 1
+                    codes[n, s * 64 + 8 * w + 2 * pair] = slots[pair]
+                    codes[n, s * 64 + 8 * w + 2 * pair + 1] = slots[pair + 4]
+    assert np.array_equal(codes[:, :K], O.unpack_codes(B, K, 4, bs))
+    assert not codes[:, Kp:].any()  # the zero half past the last chunk
+    assert PK.packed_bytes(N, K, bs, bits=8) == 0

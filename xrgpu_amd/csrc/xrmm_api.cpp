@@ -113,6 +113,48 @@ int xrmm_matmul_nbits(const void* A, const void* B, const void* scales, const vo
   return run(L, stream);
 }
 
+int64_t xrmm_prepacked_bytes(int64_t N, int64_t K, int32_t bits, int32_t block_size) {
+  if (N <= 0 || K <= 0 || block_size <= 0) return 0;
+  return xrmm::prepacked_bytes(N, (K + block_size - 1) / block_size, block_size, bits);
+}
+
+int xrmm_prepack_weights(const void* B, void* packed, int64_t N, int64_t K, int32_t bits, int32_t block_size,
+                         void* stream) {
+  xrmm::Launch L;
+  if (int rc = geometry(L, xrmm::OP_MATMUL, 1, K, bits, block_size, XRMM_F16, XRMM_UNSPECIFIED)) return rc;
+  if (N <= 0) return fail(XRMM_EINVAL, "Packed matmul N required");
+  if (xrmm::prepacked_bytes(N, L.kb, block_size, bits) == 0)
+    return fail(XRMM_EINVAL, "prepacked weights need 4-bit codes and whole 32-code chunks per column");
+  if (!B || !packed) return fail(XRMM_EINVAL, "null tensor pointer");
+  if ((reinterpret_cast<uintptr_t>(B) & 15u) || (reinterpret_cast<uintptr_t>(packed) & 15u))
+    return fail(XRMM_EINVAL, "prepack: B and the packed buffer must be 16-byte aligned");
+  L.nproj = 1;
+  L.p[0] = xrmm::Proj{static_cast<const uint8_t*>(B), nullptr, nullptr, nullptr, nullptr, N};
+  const hipError_t e = xrmm::launch_prepack(L, packed, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return dev_fail(e, "prepack launch");
+  return ok();
+}
+
+int xrmm_matmul_nbits_prepacked(const void* A, const void* packed, const void* scales, const void* zero_points,
+                                int32_t zp_dtype, const void* bias, void* Y, int64_t M, int64_t K, int64_t N,
+                                int32_t bits, int32_t block_size, int32_t dtype, void* stream) {
+  xrmm::Launch L;
+  if (int rc = geometry(L, xrmm::OP_MATMUL, M, K, bits, block_size, dtype, zp_dtype)) return rc;
+  if (N <= 0) return fail(XRMM_EINVAL, "Packed matmul N required");
+  if (zp_dtype != XRMM_UNSPECIFIED && !zero_points) return fail(XRMM_EINVAL, "zero-point dtype given without zero points");
+  if (M == 0) return ok();
+  if (!A || !packed || !scales || !Y) return fail(XRMM_EINVAL, "null tensor pointer");
+  L.nproj = 1;
+  L.A = A;
+  L.p[0] = xrmm::Proj{static_cast<const uint8_t*>(packed), scales, zero_points, bias, Y, N};
+  if (!xrmm::prepacked_ok(L))
+    return fail(XRMM_EINVAL, "prepacked weights run float16 activations with 4-bit codes, a power-of-two block_size "
+                             ">= 16, K a multiple of 8 and 16-byte aligned tensors");
+  const hipError_t e = xrmm::launch_prepacked(L, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return dev_fail(e, "kernel launch");
+  return ok();
+}
+
 int xrmm_matmul_nbits_qkv(const void* A, const void* skip, const void* norm_scale, const void* q_B,
                           const void* q_scales, const void* q_zero_points, const void* k_B,
                           const void* k_scales, const void* k_zero_points, const void* v_B,

@@ -75,7 +75,7 @@ struct GbRegs {
 };
 
 // One output tile: rows m0 .. m0 + 255, columns n0 .. n0 + 64 TN - 1.
-template <int ZPK, int SPC, int TN>
+template <int ZPK, int SPC, int TN, bool PK>
 __device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const int n0) {
   extern __shared__ __align__(16) unsigned char smem[];
   f16* lds = reinterpret_cast<f16*>(smem);
@@ -100,7 +100,9 @@ __device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const i
   const int bn = n0 + bc;
   const bool bnval = bc < 64 * TN && bn < N;  // narrow tiles: threads past the tile load nothing
   const uint32_t zrow = ZPK == ZP_PACKED ? static_cast<uint32_t>(L.zrow) : kb * (L.zp_dtype == DT_F32 ? 4u : 2u);
-  const rsrc_t rB = mk_rsrc(P.B, static_cast<uint32_t>(N) * rowb);
+  // PK: B in the prepacked layout [K step][column][32 bytes] (prepack_q4)
+  const uint32_t ksteps_b = static_cast<uint32_t>(ksteps);
+  const rsrc_t rB = mk_rsrc(P.B, PK ? ksteps_b * static_cast<uint32_t>(N) * 32u : static_cast<uint32_t>(N) * rowb);
   // scale / zero-point bounds rounded to 16 bytes: the range check zeroes a
   // whole dword straddling the bound, and 16-byte aligned tensors keep the
   // rounded bound inside the block holding their last byte
@@ -120,7 +122,10 @@ __device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const i
     }
     const int ch = ks * 2 + bh;
     const uint32_t past = ch < nchunk ? 0u : OOB;
-    r.b = bld16(rB, bcol + past + static_cast<uint32_t>(ch) * 16u, 0);
+    if constexpr (PK)
+      r.b = bld16(rB, (bnval && ks < ksteps) ? (static_cast<uint32_t>(ks) * static_cast<uint32_t>(N) + static_cast<uint32_t>(bn)) * 32u + static_cast<uint32_t>(bh) * 16u : OOB, 0);
+    else
+      r.b = bld16(rB, bcol + past + static_cast<uint32_t>(ch) * 16u, 0);
 #pragma unroll
     for (int q = 0; q < SPC; ++q) {
       const uint32_t b = static_cast<uint32_t>(ch * 32 + q * 16) >> L.bs_log2;  // block of this half-chunk
@@ -163,7 +168,9 @@ __device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const i
     f16* As = lds + stage * GB_STAGE;
     f16* Bs = As + GB_M * GB_LD;
     const int p = tid + GB_T * d, row = p >> 3, grp = p & 7;
-    *reinterpret_cast<f16x8*>(As + row * GB_LD + grp * 8) = pair_order(__builtin_bit_cast(f16x8, r.a[d]));
+    // prepacked codes dequantise in natural k order, the others in pair order
+    *reinterpret_cast<f16x8*>(As + row * GB_LD + grp * 8) =
+        PK ? __builtin_bit_cast(f16x8, r.a[d]) : pair_order(__builtin_bit_cast(f16x8, r.a[d]));
     const int q = d / (4 / SPC);
     f16x8 b;
     if constexpr (ZPK == ZP_FLOAT) b = dq8_f32z(r.b[d], mt.z[q], mt.s[q]);
@@ -297,26 +304,26 @@ __device__ __forceinline__ void tile_of(uint32_t b, uint32_t mt, uint32_t nc, ui
 
 // The grid is one dimension: workgroup bid takes a wide tile when bid < nbig
 // (a scalar, uniform branch), else a narrow one.
-template <int ZPK, int SPC>
+template <int ZPK, int SPC, bool PK = false>
 __global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big(Launch L, GemmTiles t) {
   const uint32_t bid = blockIdx.x;
   const uint32_t mt = static_cast<uint32_t>((L.M + GB_M - 1) / GB_M);
   uint32_t row, col;
   if (bid < t.nbig) {
     tile_of(bid, mt, t.nb, row, col);
-    gemm_tile<ZPK, SPC, 4>(L, static_cast<int>(row) * GB_M, static_cast<int>(col) * 256);
+    gemm_tile<ZPK, SPC, 4, PK>(L, static_cast<int>(row) * GB_M, static_cast<int>(col) * 256);
   } else {
     tile_of(bid - t.nbig, mt, t.ns, row, col);
-    gemm_tile<ZPK, SPC, 3>(L, static_cast<int>(row) * GB_M, static_cast<int>(t.nb * 256u + col * 192u));
+    gemm_tile<ZPK, SPC, 3, PK>(L, static_cast<int>(row) * GB_M, static_cast<int>(t.nb * 256u + col * 192u));
   }
 }
 
 // Compute units of the current device (cached per device ordinal).
 int device_cus();
 
-template <int ZPK, int SPC>
+template <int ZPK, int SPC, bool PK = false>
 inline hipError_t launch_gemm_big(const Launch& L, hipStream_t st) {
-  auto kern = k_gemm_q4_big<ZPK, SPC>;
+  auto kern = k_gemm_q4_big<ZPK, SPC, PK>;
   // more than 64 KB of dynamic LDS needs the attribute; set once per instantiation
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -332,5 +339,8 @@ inline hipError_t launch_gemm_big(const Launch& L, hipStream_t st) {
 // Defined once per zero-point kind (xrmm_gemm_zp.hip).
 template <int ZPK>
 hipError_t launch_gemm_big_for(const Launch& L, hipStream_t st);
+// The same GEMM on prepacked weights (L.p[0].B in the prepack_q4 layout).
+template <int ZPK>
+hipError_t launch_gemm_big_pk_for(const Launch& L, hipStream_t st);
 
 }  // namespace xrmm

@@ -13,4 +13,9 @@ hipError_t launch_gemm_big_for<XRMM_ZPK>(const Launch& L, hipStream_t st) {
   return L.block_size >= 32 ? launch_gemm_big<XRMM_ZPK, 1>(L, st) : launch_gemm_big<XRMM_ZPK, 2>(L, st);
 }
 
+template <>
+hipError_t launch_gemm_big_pk_for<XRMM_ZPK>(const Launch& L, hipStream_t st) {
+  return L.block_size >= 32 ? launch_gemm_big<XRMM_ZPK, 1, true>(L, st) : launch_gemm_big<XRMM_ZPK, 2, true>(L, st);
+}
+
 }  // namespace xrmm

@@ -80,4 +80,16 @@ int set_status(int code, const std::string& msg);
 // W [N, K] in out_dtype (see xrmm_dequantize).
 hipError_t launch_dequantize(const Launch& L, void* W, int out_dtype, hipStream_t stream);
 
+// Prepacked 4-bit weights (xrmm_prepack_weights): bytes of the layout, 0 when
+// the geometry has none (the layout needs 4-bit codes and whole 32-code
+// chunks per column).
+int64_t prepacked_bytes(int64_t N, int64_t kb, int64_t block_size, int bits);
+// Write L.p[0].B (N x kb x blob) to `out` in the prepacked layout.
+hipError_t launch_prepack(const Launch& L, void* out, hipStream_t stream);
+// Whether the prepacked GEMM runs this geometry (float16, 4-bit, the fast
+// kernels' alignment and block conditions, 32-bit index ranges).
+bool prepacked_ok(const Launch& L);
+// MatMulNBits with L.p[0].B prepacked (prepacked_ok must hold).
+hipError_t launch_prepacked(const Launch& L, hipStream_t stream);
+
 }  // namespace xrmm

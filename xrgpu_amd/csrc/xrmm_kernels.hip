@@ -466,6 +466,75 @@ hipError_t launch(const Launch& L, hipStream_t st) {
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// offline weight prepack for the prefill GEMM (xrmm_prepack_weights)
+//
+// Layout: [K step s][column n][32 bytes], a K step being 64 codes, so the
+// 256 columns of a GEMM tile read one K step as one contiguous 8 KB block
+// (whole 1 KB pieces per wave load instead of 32-byte pieces of 32 column
+// rows). Inside each dword the eight codes c0..c7 of eight consecutive k are
+// reordered to nibble slots (c0 c2 c4 c6 c1 c3 c5 c7): the dequantisation's
+// exponent-bias pairs (slots 0/4, 1/5, 2/6, 3/7) then come out in natural k
+// order, so the GEMM stages the activations as they are, without the pair
+// permutation. Codes, scales and zero points are otherwise unchanged; a
+// second 16-byte half past the column's last chunk is zero.
+
+// Reorder the nibbles of x (c_i at bits 4i) to slots (c0 c2 c4 c6 c1 c3 c5 c7).
+__device__ __forceinline__ uint32_t prepack_dword(uint32_t x) {
+  auto squeeze = [](uint32_t b) {  // low nibbles of the four bytes -> one 16-bit value
+    const uint32_t t = (b | (b >> 4)) & 0x00FF00FFu;
+    return (t & 0xFFu) | ((t >> 8) & 0xFF00u);
+  };
+  return squeeze(x & 0x0F0F0F0Fu) | (squeeze((x >> 4) & 0x0F0F0F0Fu) << 16);
+}
+
+// One thread per 16-byte half (s, n, h): consecutive threads write
+// consecutive 16 bytes.
+__global__ __launch_bounds__(256) void k_prepack_q4(const uint8_t* __restrict__ B, uint8_t* __restrict__ out,
+                                                    uint32_t N, uint32_t nchunk, uint64_t pieces) {
+  const uint64_t t = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+  if (t >= pieces) return;
+  const uint32_t h = static_cast<uint32_t>(t & 1u);
+  const uint64_t sn = t >> 1;
+  const uint32_t n = static_cast<uint32_t>(sn % N), s = static_cast<uint32_t>(sn / N);
+  const uint32_t ch = 2u * s + h;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (ch < nchunk) v = ld16(B + (static_cast<uint64_t>(n) * nchunk + ch) * 16u);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) v[d] = prepack_dword(v[d]);
+  *reinterpret_cast<u32x4*>(out + t * 16u) = v;
+}
+
+int64_t prepacked_bytes(int64_t N, int64_t kb, int64_t block_size, int bits) {
+  const int64_t Kp = kb * block_size;
+  if (bits != 4 || N <= 0 || Kp <= 0 || Kp % 32 != 0) return 0;
+  return (Kp + 63) / 64 * N * 32;
+}
+
+hipError_t launch_prepack(const Launch& L, void* out, hipStream_t st) {
+  const Proj& P = L.p[0];
+  const int64_t bytes = prepacked_bytes(P.N, L.kb, L.block_size, L.bits);
+  if (bytes == 0) return hipErrorInvalidValue;
+  const uint64_t pieces = static_cast<uint64_t>(bytes / 16);
+  const uint64_t grid = (pieces + 255) / 256;
+  if (grid > 0x7FFFFFFFu || P.N > 0xFFFFFFFFLL) return hipErrorInvalidValue;  // launch limits
+  hipLaunchKernelGGL(k_prepack_q4, dim3(static_cast<uint32_t>(grid)), dim3(256), 0, st, P.B, static_cast<uint8_t*>(out),
+                     static_cast<uint32_t>(P.N), static_cast<uint32_t>(L.kb * L.blob / 16), pieces);
+  return hipGetLastError();
+}
+
+bool prepacked_ok(const Launch& L) {
+  return L.op == OP_MATMUL && L.M >= 1 && q4_fast_ok(L) && fits_i32(L) &&
+         prepacked_bytes(L.p[0].N, L.kb, L.block_size, L.bits) != 0;
+}
+
+hipError_t launch_prepacked(const Launch& L, hipStream_t st) {
+  const int zpk = L.zp_kind == ZP_NONE || !L.p[0].zp ? ZP_NONE : L.zp_kind;
+  if (zpk == ZP_NONE) return launch_gemm_big_pk_for<ZP_NONE>(L, st);
+  if (zpk == ZP_PACKED) return launch_gemm_big_pk_for<ZP_PACKED>(L, st);
+  return launch_gemm_big_pk_for<ZP_FLOAT>(L, st);
+}
+
 hipError_t launch_dequantize(const Launch& L, void* W, int out_dtype, hipStream_t st) {
   const Proj& P = L.p[0];
   if (P.N == 0 || L.K == 0) return hipSuccess;

@@ -616,6 +616,7 @@ struct xrmm_op {
   std::map<std::string, void*> in_dev;  // device copies of present inputs
   std::vector<void*> out_dev;           // device outputs in plan order
   void* workspace = nullptr;            // QMoE workspace / GatherBlockQuantized status word
+  void* packed = nullptr;               // MatMulNBits prefill: B prepacked at prepare (xrmm_prepack_weights)
   uint64_t workspace_bytes = 0;
   bool closed = false, executed = false, poisoned = false, has_gpu = false;
   bool exact_weights = false;  // weights_need_float32 at prepare
@@ -630,6 +631,8 @@ struct xrmm_op {
   void release() noexcept {
     if (stream) (void)hipStreamSynchronize(stream);
     if (arena) (void)hipFree(arena);
+    if (packed) (void)hipFree(packed);
+    packed = nullptr;
     if (ev_start) (void)hipEventDestroy(ev_start);
     if (ev_end) (void)hipEventDestroy(ev_end);
     if (stream) (void)hipStreamDestroy(stream);
@@ -674,6 +677,10 @@ struct xrmm_op {
                                            p.bits, p.block_size, s);
       }
       case xrmm::OP_MATMUL:
+        if (packed)
+          return xrmm_matmul_nbits_prepacked(dptr("aT"), packed, dptr("scalesT"), dptr("zeroPointsT"),
+                                             dptr("zeroPointsT") ? zd : XRMM_UNSPECIFIED, dptr("biasT"), optr("yT"), p.M,
+                                             p.K, p.N, p.bits, p.block_size, p.dtype, s);
         return xrmm_matmul_nbits(dptr("aT"), dptr("bT"), dptr("scalesT"), dptr("zeroPointsT"), dptr("zeroPointsT") ? zd : XRMM_UNSPECIFIED,
                                  dptr("biasT"), optr("yT"), p.M, p.K, p.N, p.bits, p.block_size, p.dtype, s);
       case xrmm::OP_MLP: {
@@ -822,6 +829,18 @@ int xrmm_prepare(const xrmm_request* request, const xrmm_options* options, xrmm_
       const xrmm::ExactWeightsScope exact(op->exact_weights);
       const int64_t n0 = code == xrmm::OP_QKV ? p.Nq : p.N;
       k = xrmm_select_kernel(code, p.M, p.K, n0, p.bits, p.block_size, p.dtype, zk);
+      // prepare = upload / prepack: MatMulNBits requests that reach the 256 x
+      // 256 prefill GEMM get their weights prepacked once, here, when the
+      // copy fits the memory limit beside the arena
+      const int64_t pk = code == xrmm::OP_MATMUL && k && std::strcmp(k, "gemm_q4_big") == 0
+                             ? xrmm_prepacked_bytes(p.N, p.K, p.bits, p.block_size) : 0;
+      if (pk > 0 && total + uint64_t(pk) <= o.memory_limit_bytes) {
+        hip_check(hipMalloc(&op->packed, size_t(pk)), "hipMalloc (prepacked weights)");
+        if (xrmm_prepack_weights(op->dptr("bT"), op->packed, p.N, p.K, p.bits, p.block_size, op->stream) != XRMM_OK)
+          throw Device(std::string("prepack: ") + xrmm_last_error());
+        hip_check(hipStreamSynchronize(op->stream), "hipStreamSynchronize");
+        k = "gemm_q4_big_prepacked";
+      }
     }
     op->kernel = k ? k : "generic";
     *out = op.release();

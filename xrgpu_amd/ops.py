@@ -136,6 +136,57 @@ def matmul_nbits(A, B, scales, zero_points=None, bias=None, *, K=None, N=None, b
     return out
 
 
+def prepacked_bytes(N, K, bits=4, block_size=32):
+    """Bytes of B prepacked for the prefill GEMM (0: the geometry has no prepacked layout)."""
+    return int(nat.lib().xrmm_prepacked_bytes(int(N), int(K), int(bits), int(block_size)))
+
+
+def prepack_weights(B, *, K, N=None, bits=4, block_size=32, stream=None):
+    """B [N, ceil(K/bs), bs/2] uint8 -> the prepacked layout (a flat uint8 tensor) that
+    matmul_nbits_prepacked reads: K-step-major, codes reordered inside each word."""
+    N = int(N if N is not None else B.shape[0])
+    K = int(K)
+    kb, blob, _ = _geometry(K, bits, block_size)
+    if B.dtype != torch.uint8 or tuple(B.shape) != (N, kb, blob):
+        raise nat.XrmmInvalid(f"B must be uint8 [{N}, {kb}, {blob}], got {B.dtype} {tuple(B.shape)}")
+    nbytes = prepacked_bytes(N, K, bits, block_size)
+    if nbytes == 0:
+        raise nat.XrmmInvalid("prepacked weights need 4-bit codes and whole 32-code chunks per column")
+    out = torch.empty(nbytes, dtype=torch.uint8, device=B.device)
+    dev = _check_dev(B, out)
+    nat.check(nat.lib().xrmm_prepack_weights(_ptr(B), _ptr(out), N, K, bits, block_size, _stream(stream, dev)))
+    return out
+
+
+def matmul_nbits_prepacked(A, packed, scales, zero_points=None, bias=None, *, K=None, N, bits=4, block_size=32,
+                           out=None, stream=None):
+    """MatMulNBits with B prepacked by prepack_weights (the prefill GEMM for every M)."""
+    K = int(K if K is not None else A.shape[-1])
+    N = int(N)
+    if A.shape[-1] != K:
+        raise nat.XrmmInvalid("A's last dimension must equal K")
+    if packed.dtype != torch.uint8 or packed.numel() != prepacked_bytes(N, K, bits, block_size):
+        raise nat.XrmmInvalid("packed must be the uint8 output of prepack_weights for this N, K and block_size")
+    kb, _, zrow = _geometry(K, bits, block_size)
+    if scales.dtype != A.dtype or tuple(scales.shape) != (N, kb):
+        raise nat.XrmmInvalid(f"scales must be {A.dtype} [{N}, {kb}], got {scales.dtype} {tuple(scales.shape)}")
+    if zero_points is not None:
+        want = (N, zrow) if zero_points.dtype == torch.uint8 else (N, kb)
+        if tuple(zero_points.shape) != want:
+            raise nat.XrmmInvalid(f"zero points must have shape {list(want)}, got {tuple(zero_points.shape)}")
+    if bias is not None and (bias.dtype != A.dtype or tuple(bias.shape) != (N,)):
+        raise nat.XrmmInvalid("bias must be [N] of A's dtype")
+    M = A.numel() // K
+    _check_out(out, tuple(A.shape[:-1]) + (N,), A.dtype)
+    dev = _check_dev(A, packed, scales, zero_points, bias, out)
+    if out is None:
+        out = torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
+    nat.check(nat.lib().xrmm_matmul_nbits_prepacked(_ptr(A), _ptr(packed), _ptr(scales), _ptr(zero_points),
+                                                    _zp_dtype(zero_points), _ptr(bias), _ptr(out), M, K, N, bits,
+                                                    block_size, _t1(A), _stream(stream, dev)))
+    return out
+
+
 def matmul_nbits_qkv(A, q_B, q_scales, k_B, k_scales, v_B, v_scales, *, norm_scale, skip=None,
                      K=None, Nq=None, Nkv=None, bits=4, block_size=32, epsilon=1e-6,
                      q_zero_points=None, k_zero_points=None, v_zero_points=None,
