@@ -122,7 +122,7 @@ def test_prepack_sizes_and_validation_without_device():
     assert lib.xrmm_prepacked_bytes(100, 96, 4, 32) == 2 * 100 * 32      # a K step and a half: the half is padded
     assert lib.xrmm_prepacked_bytes(100, 20, 4, 16) == 100 * 32          # one chunk of 32 codes
     assert lib.xrmm_prepacked_bytes(8, 64, 8, 32) == 0                   # 8-bit codes have no packed layout
-    assert lib.xrmm_prepacked_bytes(8, 64, 4, 8) == 0                    # 16-code columns are not whole chunks
+    assert lib.xrmm_prepacked_bytes(8, 40, 4, 8) == 0                    # 40-code columns are not whole 32-code chunks
     rc = lib.xrmm_prepack_weights(None, None, 8, 64, 8, 32, None)
     assert rc == nat.XRMM_EINVAL and "4-bit" in nat.last_error()
     rc = lib.xrmm_prepack_weights(None, None, 8, 64, 4, 32, None)
