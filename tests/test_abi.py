@@ -130,3 +130,24 @@ def test_prepack_sizes_and_validation_without_device():
     rc = lib.xrmm_matmul_nbits_prepacked(None, None, None, None, nat.UNSPECIFIED, None, None, 0, 64, 8, 4, 32,
                                          nat.F16, None)
     assert rc == nat.XRMM_OK  # M = 0: nothing to do
+
+
+def test_fuzz_reaches_every_kernel_family():
+    """The seeded GPU fuzz draws (tests/test_gpu_fuzz.py) must dispatch to every
+    MatMulNBits-family kernel, so every family meets shapes nobody picked
+    (checked here, without a device, through the dispatcher)."""
+    import torch
+    from tests import test_gpu_fuzz as F
+    from xrgpu_amd import ops
+    kind = {"none": None, "packed": "packed", "float_int": "float", "float": "float"}
+    seen = set()
+    for M, K, N, bits, bs, zp, _, dt in F.MM + F.MMF32:
+        seen.add(ops.select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float16 if dt == "f16" else torch.float32,
+                                   kind[zp]))
+    for M, K, Nq, _, bs, zp, _ in F.QKV + F.QKV2:
+        seen.add(ops.select_kernel("MatMulNBitsQkv", M, K, Nq, 4, bs, torch.float16, kind[zp]))
+    for M, K, N, bs, *_ in F.MLP + F.MLP2:
+        seen.add(ops.select_kernel("MatMulNBitsMlp", M, K, N, 4, bs, torch.float16))
+    want = {"gemv_q4_dot", "gemv_q4_mq", "gemv_q4_splitk", "gemv_q4_mfma", "gemv_q4_f32", "gemm_q4_mfma",
+            "gemm_q4_fused", "generic"}
+    assert want <= seen, f"not reached: {sorted(want - seen)}"

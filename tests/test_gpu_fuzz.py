@@ -175,6 +175,99 @@ def test_mlp_random(gpu, M, K, N, bs, skip, norm, biases, act, res):
         assert np.array_equal(host(R), r)
 
 
+def _qkv_prefill_cases(n=10):
+    """More than 16 rows: the split-K GEMV's row chunks (up to 64 rows, columns
+    of 64 or 128 chunks) and the fused GEMM."""
+    rng = np.random.default_rng(SEED + 11)
+    out = []
+    for _ in range(n):
+        bs = int(rng.choice([16, 32, 64, 128]))
+        K = int(rng.choice([2048, 4096])) if rng.random() < 0.5 else int(bs * rng.integers(1, max(2, 1024 // bs + 1)))
+        out.append((int(rng.choice([17, 24, 33, 48, 64, 65, 100, 130, 200])), K, int(rng.integers(1, 300)),
+                    int(rng.integers(1, 150)), bs, str(rng.choice(["none", "packed", "float_int"])),
+                    bool(rng.integers(0, 2))))
+    return out
+
+
+QKV2 = _qkv_prefill_cases()
+
+
+@pytest.mark.parametrize("M,K,Nq,Nkv,bs,zp,skip", QKV2, ids=ids(QKV2))
+def test_qkv_prefill_random(gpu, M, K, Nq, Nkv, bs, zp, skip):
+    test_qkv_random(gpu, M, K, Nq, Nkv, bs, zp, skip)
+
+
+def _mlp_prefill_cases(n=10):
+    rng = np.random.default_rng(SEED + 12)
+    out = []
+    for _ in range(n):
+        bs = int(rng.choice([16, 32, 64, 128]))
+        K = int(rng.choice([2048, 4096])) if rng.random() < 0.5 else int(bs * rng.integers(1, max(2, 1024 // bs + 1)))
+        out.append((int(rng.choice([17, 24, 33, 48, 64, 65, 100, 130, 200])), K, int(rng.integers(1, 300)), bs,
+                    bool(rng.integers(0, 2)), bool(rng.integers(0, 2)), bool(rng.integers(0, 2)),
+                    str(rng.choice(["silu", "gelu", "relu", "tanh"])), bool(rng.integers(0, 2))))
+    return out
+
+
+MLP2 = _mlp_prefill_cases()
+
+
+@pytest.mark.parametrize("M,K,N,bs,skip,norm,biases,act,res", MLP2, ids=ids(MLP2))
+def test_mlp_prefill_random(gpu, M, K, N, bs, skip, norm, biases, act, res):
+    test_mlp_random(gpu, M, K, N, bs, skip, norm, biases, act, res)
+
+
+def _f32_cases(n=10):
+    """Float32 activations, 4-bit, up to four rows: the float32 GEMV (K tails,
+    every zero-point kind)."""
+    rng = np.random.default_rng(SEED + 13)
+    out = []
+    for _ in range(n):
+        bs = int(rng.choice([16, 32, 64, 128]))
+        out.append((int(rng.integers(1, 5)), int(8 * rng.integers(1, 1025)), int(rng.integers(1, 600)), 4, bs,
+                    str(rng.choice(["none", "packed", "float_int", "float"])), bool(rng.integers(0, 2)), "f32"))
+    return out
+
+
+MMF32 = _f32_cases()
+
+
+@pytest.mark.parametrize("M,K,N,bits,bs,zp,bias,dt", MMF32, ids=ids(MMF32))
+def test_matmul_nbits_f32_random(gpu, M, K, N, bits, bs, zp, bias, dt):
+    test_matmul_nbits_random(gpu, M, K, N, bits, bs, zp, bias, dt)
+
+
+def _prepacked_cases(n=10):
+    """Prepacked weights: the prefill GEMM at any row count, K of whole 32-code
+    chunks (tails inside a block), every zero-point kind."""
+    rng = np.random.default_rng(SEED + 14)
+    out = []
+    for _ in range(n):
+        bs = int(rng.choice([16, 32, 64, 128]))
+        while True:
+            K = int(8 * rng.integers(1, 129))
+            if (-(-K // bs) * bs) % 32 == 0:
+                break
+        out.append((int(rng.choice([1, 7, 64, 128, 129, 300, 513])), K, int(rng.integers(1, 600)), bs,
+                    str(rng.choice(["none", "packed", "float_int", "float"])), bool(rng.integers(0, 2))))
+    return out
+
+
+PKC = _prepacked_cases()
+
+
+@pytest.mark.parametrize("M,K,N,bs,zp,bias", PKC, ids=ids(PKC))
+def test_prepacked_random(gpu, M, K, N, bs, zp, bias):
+    rng = np.random.default_rng([SEED, 14, M, K, N, bs])
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    B, S, Z = weights(rng, K, N, 4, bs, np.float16, None if zp == "none" else zp)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float16) if bias else None
+    o = ops()
+    packed = o.prepack_weights(dev(B), K=K, block_size=bs)
+    Y = host(o.matmul_nbits_prepacked(dev(A), packed, dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
+    check(Y, O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs), np.float16)
+
+
 # --------------------------------------------------------------------------- GatherBlockQuantized / MatMulBnb4
 
 def _gbq_cases(n=16):
