@@ -142,12 +142,20 @@ __global__ __launch_bounds__(64) void k_generic(Launch L) {
 
 constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 64, GM_LDK = GM_BK + 8;
 
-template <int ZPK, int SPC>
-__global__ __launch_bounds__(256) void k_gemm_q4(Launch L) {
-  __shared__ __align__(16) f16 As[GM_BM * GM_LDK];
-  __shared__ __align__(16) f16 Bs[GM_BN * GM_LDK];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// KG groups of four waves split the K steps (step kt goes to group kt % KG):
+// with few output tiles (N / 128 x M / 128 workgroups against 256 CUs) one
+// group's serial K loop is the critical path, and a second group halves it
+// and fills a second wave per SIMD. The groups' partial tiles meet in LDS.
+template <int ZPK, int SPC, int KG>
+__global__ __launch_bounds__(256 * KG) void k_gemm_q4(Launch L) {
+  static_assert(KG == 1 || KG == 2, "K groups");
+  __shared__ __align__(16) f16 As_[KG][GM_BM * GM_LDK];
+  __shared__ __align__(16) f16 Bs_[KG][GM_BN * GM_LDK];
+  const int tid_all = threadIdx.x, kg = tid_all >> 8, tid = tid_all & 255;
+  const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
+  f16* As = As_[kg];
+  f16* Bs = Bs_[kg];
   const Proj& P = L.p[0];
   const int64_t M = L.M, N = P.N, K = L.K;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * GM_BM, n0 = static_cast<int64_t>(blockIdx.x) * GM_BN;
@@ -156,29 +164,59 @@ __global__ __launch_bounds__(256) void k_gemm_q4(Launch L) {
   const int64_t ktiles = (Kp + GM_BK - 1) / GM_BK;
   const f16* A = static_cast<const f16*>(L.A);
 
-  // global -> register staging, two steps ahead: each thread's four 16-byte
-  // activation pieces, one weight chunk and its raw scale / zero point
+  // global -> register staging, two of the group's steps ahead: each
+  // thread's four 16-byte activation pieces, one weight chunk and its raw
+  // scale / zero point
   struct Regs {
     f16x8 a[4];
     u32x4 b;
     RawMeta<SPC> m;
   };
+  // Loads go through buffer resources with 32-bit offsets: an offset past the
+  // bound reads zero, so rows past M, k past K and columns past N need no
+  // branch around the load (a divergent select became one, and every later
+  // wait a full drain). The fast path guarantees 32-bit index ranges.
+  constexpr uint32_t OOB = 0x80000000u;
   const int bcol = tid >> 1, bh = tid & 1;
   const int64_t bn = n0 + bcol;
   const bool bnval = bn < N;
-  const uint8_t* Bcol = P.B + (bnval ? bn : 0) * row_bytes;
+  const uint32_t K32 = static_cast<uint32_t>(K), kb = static_cast<uint32_t>(L.kb);
+  const rsrc_t rA = mk_rsrc(A, static_cast<uint32_t>(M) * K32 * 2u);
+  const rsrc_t rB = mk_rsrc(P.B, static_cast<uint32_t>(N) * static_cast<uint32_t>(row_bytes));
+  const uint32_t zrow = ZPK == ZP_PACKED ? static_cast<uint32_t>(L.zrow) : kb * (L.zp_dtype == DT_F32 ? 4u : 2u);
+  // scale / zero-point bounds rounded to 16 bytes (16-byte aligned tensors keep
+  // the rounded bound inside the block holding their last byte)
+  const rsrc_t rS = mk_rsrc(P.scales, (static_cast<uint32_t>(N) * kb * 2u + 15u) & ~15u);
+  const rsrc_t rZ = mk_rsrc(P.zp ? P.zp : P.scales, (static_cast<uint32_t>(N) * zrow + 15u) & ~15u);
+  const uint32_t bcol_off = bnval ? static_cast<uint32_t>(bn) * static_cast<uint32_t>(row_bytes) : OOB;
+  const uint32_t scol = bnval ? static_cast<uint32_t>(bn) * kb * 2u : OOB;
+  const uint32_t zcol = bnval ? static_cast<uint32_t>(bn) * zrow : OOB;
+  uint32_t aoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + 256 * i, row = idx >> 3, grp = idx & 7;
+    const int64_t m = m0 + row;
+    aoff[i] = m < M ? (static_cast<uint32_t>(m) * K32 + static_cast<uint32_t>(grp) * 8u) * 2u : OOB;
+  }
 
   auto gload = [&](Regs& r, int64_t kt) {
+    const uint32_t k = static_cast<uint32_t>(kt) * GM_BK + static_cast<uint32_t>(tid & 7) * 8u;
+    const uint32_t kpast = k < K32 ? 0u : OOB;  // K % 8 == 0: groups are whole
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + 256 * i, row = idx >> 3, grp = idx & 7;
-      const int64_t m = m0 + row, k = kt * GM_BK + grp * 8;
-      r.a[i] = (m < M && k < K) ? __builtin_bit_cast(f16x8, ld16(A + m * K + k)) : f16x8{};
+    for (int i = 0; i < 4; ++i)
+      r.a[i] = __builtin_bit_cast(f16x8, bld16(rA, (aoff[i] | kpast) + static_cast<uint32_t>(kt) * (GM_BK * 2), 0));
+    const uint32_t ch = static_cast<uint32_t>(kt) * 2u + static_cast<uint32_t>(bh);
+    const uint32_t past = ch < static_cast<uint32_t>(nchunk) ? 0u : OOB;
+    r.b = bld16(rB, (bcol_off | past) + ch * 16u, 0);
+#pragma unroll
+    for (int q = 0; q < SPC; ++q) {
+      const uint32_t b = (ch * 32u + q * 16u) >> L.bs_log2;  // block of this half-chunk
+      r.m.s[q] = bld_u16(rS, (scol | past) + b * 2u, 0);
+      r.m.z[q] = 0u;
+      if constexpr (ZPK == ZP_PACKED) r.m.z[q] = bld_u8(rZ, (zcol | past) + (b >> 1), 0);
+      else if constexpr (ZPK == ZP_FLOAT)
+        r.m.z[q] = L.zp_dtype == DT_F32 ? bld_u32(rZ, (zcol | past) + b * 4u, 0) : bld_u16(rZ, (zcol | past) + b * 2u, 0);
     }
-    const int64_t ch = kt * 2 + bh;
-    const bool ok = bnval && ch < nchunk;
-    r.b = ok ? ld16(Bcol + ch * 16) : u32x4{0u, 0u, 0u, 0u};
-    r.m = ld_meta_raw<ZPK, SPC>(L, P, bn, ch, ok);
   };
   auto sstore = [&](const Regs& r, int64_t kt) {
 #pragma unroll
@@ -201,37 +239,71 @@ __global__ __launch_bounds__(256) void k_gemm_q4(Launch L) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // One K step: stage the registers of step kt, refill them with step kt + 2
-  // (loads past the last step return zeros), multiply.
+  // One K step of the group: stage the registers of step kt, refill them
+  // with the group's step after next (loads past the last step return
+  // zeros), multiply. Every group runs the same number of steps (a step past
+  // the end stages zeros), so the workgroup barriers pair up.
+  // fragments of K slice kk (0..3): lane (r, g) = (lane % 32, lane / 32)
+  // reads row / column r, k = 16 kk + 8 g .. + 7; the next slice's are read
+  // before the current slice's MFMAs, so the LDS latency hides behind them
+  f16x8 fa[2][2], fb[2][2];
+  auto read_frags = [&](int kk, int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      fa[buf][i] = *reinterpret_cast<const f16x8*>(As + (wm * 64 + i * 32 + (lane & 31)) * GM_LDK + kk * 16 + (lane >> 5) * 8);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      fb[buf][j] = *reinterpret_cast<const f16x8*>(Bs + (wn * 64 + j * 32 + (lane & 31)) * GM_LDK + kk * 16 + (lane >> 5) * 8);
+  };
   auto step = [&](Regs& r, int64_t kt) {
     __syncthreads();
     sstore(r, kt);
     __syncthreads();
-    gload(r, kt + 2);
+    read_frags(0, 0);
+    gload(r, kt + 2 * KG);
 #pragma unroll
     for (int kk = 0; kk < GM_BK / 16; ++kk) {
-      f16x8 a[2], b[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        a[i] = *reinterpret_cast<const f16x8*>(As + (wm * 64 + i * 32 + (lane & 31)) * GM_LDK + kk * 16 + (lane >> 5) * 8);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        b[j] = *reinterpret_cast<const f16x8*>(Bs + (wn * 64 + j * 32 + (lane & 31)) * GM_LDK + kk * 16 + (lane >> 5) * 8);
+      if (kk + 1 < GM_BK / 16) read_frags(kk + 1, (kk + 1) & 1);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk & 1][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
     }
   };
+  const int64_t gsteps = (ktiles + KG - 1) / KG;  // steps per group
   Regs r0, r1;
-  gload(r0, 0);
-  gload(r1, 1);
-  int64_t kt = 0;
-  for (; kt + 1 < ktiles; kt += 2) {
-    step(r0, kt);
-    step(r1, kt + 1);
+  gload(r0, kg);
+  gload(r1, kg + KG);
+  int64_t i = 0;
+  for (; i + 1 < gsteps; i += 2) {
+    step(r0, i * KG + kg);
+    step(r1, (i + 1) * KG + kg);
   }
-  if (kt < ktiles) step(r0, kt);
+  if (i < gsteps) step(r0, i * KG + kg);
+
+  if constexpr (KG == 2) {
+    // group 1's partial tiles through LDS (the stages are free now) to group 0
+    float* red = reinterpret_cast<float*>(&As_[0][0]);
+    static_assert(sizeof(As_) + sizeof(Bs_) >= 256 * 64 * sizeof(float), "the partial tiles fit the stages");
+    __syncthreads();
+    if (kg == 1) {
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) red[((ii * 2 + j) * 16 + r) * 256 + tid] = acc[ii][j][r];
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[ii][j][r] += red[((ii * 2 + j) * 16 + r) * 256 + tid];
+  }
 
   // epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each 32x32 tile
 #pragma unroll
@@ -240,11 +312,11 @@ __global__ __launch_bounds__(256) void k_gemm_q4(Launch L) {
     if (n >= N) continue;
     const float bias = P.bias ? static_cast<float>(static_cast<const f16*>(P.bias)[n]) : 0.f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int ii = 0; ii < 2; ++ii) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m < M) static_cast<f16*>(P.Y)[m * N + n] = static_cast<f16>(acc[i][j][r] + bias);
+        const int64_t m = m0 + wm * 64 + ii * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < M) static_cast<f16*>(P.Y)[m * N + n] = static_cast<f16>(acc[ii][j][r] + bias);
       }
     }
   }
@@ -396,10 +468,22 @@ const char* kernel_name(Kernel k) {
   }
 }
 
+// Two K groups while the tiles fill less than one round of the CUs
+// (XRMM_GEMM_KG overrides: 1 or 2).
+static int gemm_kgroups(int64_t wgs) {
+  const char* e = std::getenv("XRMM_GEMM_KG");
+  if (e != nullptr && (*e == '1' || *e == '2') && e[1] == 0) return *e - '0';
+  const int cus = device_cus();
+  return wgs < (cus > 0 ? cus : 256) ? 2 : 1;
+}
+
 template <int ZPK, int SPC>
 static hipError_t launch_gemm2(const Launch& L, hipStream_t st) {
   const dim3 grid(static_cast<uint32_t>((L.p[0].N + GM_BN - 1) / GM_BN), static_cast<uint32_t>((L.M + GM_BM - 1) / GM_BM));
-  hipLaunchKernelGGL((k_gemm_q4<ZPK, SPC>), grid, dim3(256), 0, st, L);
+  if (gemm_kgroups(int64_t(grid.x) * grid.y) == 2)
+    hipLaunchKernelGGL((k_gemm_q4<ZPK, SPC, 2>), grid, dim3(512), 0, st, L);
+  else
+    hipLaunchKernelGGL((k_gemm_q4<ZPK, SPC, 1>), grid, dim3(256), 0, st, L);
   return hipGetLastError();
 }
 
