@@ -83,6 +83,27 @@ int xrmm_matmul_nbits(const void* A, const void* B, const void* scales, const vo
                       int32_t zp_dtype, const void* bias, void* Y, int64_t M, int64_t K,
                       int64_t N, int32_t bits, int32_t block_size, int32_t dtype, void* stream);
 
+/* xrmm_matmul_nbits with a caller's workspace, for geometries whose output
+ * tiles leave compute units idle (more than 16 rows with few columns or few
+ * rows; the Llama-style down projection K = 14336, N = 4096 at 17..127 rows
+ * has 32 tiles for 256 CUs): the K range is split over workgroups, each
+ * split writes a float32 partial tile to the workspace and the last split of
+ * a tile adds them in split order (deterministic). No counterpart in the
+ * reference (one serial loop, complex_kernel.glsl:83); same results as
+ * xrmm_matmul_nbits within the float16 bar.
+ * xrmm_matmul_nbits_workspace_bytes gives the bytes (0: no split applies,
+ * and the call runs like xrmm_matmul_nbits). The workspace is 256-byte
+ * aligned; its first 4096 bytes (per-tile arrival counters) are zero before
+ * its first use and every call leaves them zero, so one workspace serves
+ * consecutive calls of any shape on a stream. Calls that may overlap
+ * (different streams) need different workspaces. */
+int64_t xrmm_matmul_nbits_workspace_bytes(int64_t M, int64_t K, int64_t N, int32_t bits,
+                                          int32_t block_size, int32_t dtype);
+int xrmm_matmul_nbits_ws(const void* A, const void* B, const void* scales, const void* zero_points,
+                         int32_t zp_dtype, const void* bias, void* Y, int64_t M, int64_t K, int64_t N,
+                         int32_t bits, int32_t block_size, int32_t dtype, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
 /* Offline weight prepack for the prefill GEMM. The reference has no
  * counterpart in code; it is the "prepare = upload / prepack" step of its
  * Operator lifecycle (kernels/_shared/extended/vulkan.cpp:119) for callers

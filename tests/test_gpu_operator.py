@@ -70,6 +70,27 @@ def test_prefill_lifecycle_prepacks_the_weights(gpu):
         assert ok, (kernel, err, lim)
 
 
+def test_splitk_lifecycle_runs_twice_on_its_workspace(gpu):
+    """A request with few output tiles (40 rows, N = 512: 4 tiles) runs the
+    split-K GEMM on a workspace in the operator's arena; the second run finds
+    the counters zeroed by the first and gives the same bits."""
+    from xrgpu_amd import _native as nat
+    rng = np.random.default_rng(31)
+    M, K, N, bs = 40, 8192, 512, 64
+    assert nat.lib().xrmm_matmul_nbits_workspace_bytes(M, K, N, 4, bs, nat.F16) > 0
+    ins = rand_mnb(rng, M, K, N, bs)
+    with op.Operator.prepare("", request(MNB, ins, {"N": N, "block_size": bs})) as o:
+        o.run()
+        (y1,) = o.read_outputs()
+        o.run()
+        (y2,) = o.read_outputs()
+    ref = O.matmul_nbits(ins["aT"], ins["bT"], ins["scalesT"], ins["zeroPointsT"], ins["biasT"], K=K, N=N,
+                         block_size=bs)
+    ok, err, lim = O.tolerance_ok(y1.data, ref, np.float16)
+    assert ok, (err, lim)
+    assert np.array_equal(y1.data.view(np.uint16), y2.data.view(np.uint16))
+
+
 def test_requested_float32_storage_holds_the_float16_values(gpu):
     rng = np.random.default_rng(1)
     ins = rand_mnb(rng, 2, 256, 64, 32)

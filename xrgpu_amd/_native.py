@@ -72,6 +72,9 @@ def _sig(lib):
     s("xrmm_matmul_nbits_int8a_noalloc", ctypes.c_int, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i32,
       _i32, _i32, _vp)
     s("xrmm_stream_read", ctypes.c_int, _vp, ctypes.c_uint64, _vp, _i32, _vp)
+    s("xrmm_matmul_nbits_workspace_bytes", _i64, _i64, _i64, _i64, _i32, _i32, _i32)
+    s("xrmm_matmul_nbits_ws", ctypes.c_int, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32,
+      _vp, _i64, _vp)
     s("xrmm_prepacked_bytes", _i64, _i64, _i64, _i32, _i32)
     s("xrmm_prepack_weights", ctypes.c_int, _vp, _vp, _i64, _i64, _i32, _i32, _vp)
     s("xrmm_matmul_nbits_prepacked", ctypes.c_int, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i32, _i32,

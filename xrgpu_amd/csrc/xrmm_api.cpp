@@ -113,6 +113,44 @@ int xrmm_matmul_nbits(const void* A, const void* B, const void* scales, const vo
   return run(L, stream);
 }
 
+int64_t xrmm_matmul_nbits_workspace_bytes(int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size,
+                                          int32_t dtype) {
+  xrmm::Launch L;
+  if (N <= 0 || geometry(L, xrmm::OP_MATMUL, M, K, bits, block_size, dtype, XRMM_UNSPECIFIED) != XRMM_OK) {
+    g_error.clear();
+    return 0;
+  }
+  L.nproj = 1;
+  L.p[0].N = N;
+  if (M <= 0 || xrmm::select_kernel(L) != xrmm::K_GEMM_Q4) return 0;
+  return xrmm::gemm_workspace_bytes(L, xrmm::gemm_splits(L));
+}
+
+int xrmm_matmul_nbits_ws(const void* A, const void* B, const void* scales, const void* zero_points, int32_t zp_dtype,
+                         const void* bias, void* Y, int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size,
+                         int32_t dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  xrmm::Launch L;
+  if (int rc = geometry(L, xrmm::OP_MATMUL, M, K, bits, block_size, dtype, zp_dtype)) return rc;
+  if (N <= 0) return fail(XRMM_EINVAL, "Packed matmul N required");
+  if (zp_dtype != XRMM_UNSPECIFIED && !zero_points) return fail(XRMM_EINVAL, "zero-point dtype given without zero points");
+  if (M > 0 && (!A || !B || !scales || !Y)) return fail(XRMM_EINVAL, "null tensor pointer");
+  L.nproj = 1;
+  L.A = A;
+  L.p[0] = xrmm::Proj{static_cast<const uint8_t*>(B), scales, zero_points, bias, Y, N};
+  if (M > 0 && workspace && xrmm::select_kernel(L) == xrmm::K_GEMM_Q4) {
+    const int splits = xrmm::gemm_splits(L);
+    const int64_t need = xrmm::gemm_workspace_bytes(L, splits);
+    if (need > 0) {
+      if (workspace_bytes < need)
+        return fail(XRMM_EINVAL, "workspace smaller than xrmm_matmul_nbits_workspace_bytes: " + std::to_string(need));
+      if (reinterpret_cast<uintptr_t>(workspace) & 255u) return fail(XRMM_EINVAL, "workspace must be 256-byte aligned");
+      L.ws = workspace;
+      L.splits = splits;
+    }
+  }
+  return run(L, stream);
+}
+
 int64_t xrmm_prepacked_bytes(int64_t N, int64_t K, int32_t bits, int32_t block_size) {
   if (N <= 0 || K <= 0 || block_size <= 0) return 0;
   return xrmm::prepacked_bytes(N, (K + block_size - 1) / block_size, block_size, bits);

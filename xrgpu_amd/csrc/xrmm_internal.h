@@ -46,6 +46,11 @@ struct Launch {
   // reference formula): set when a binary16 weight (code - z) * scale could
   // leave the binary16 range.
   bool exact_weights;
+  // MatMulNBits split-K (k_gemm_q4 with more than one split): float32 partial
+  // tiles and per-tile arrival counters (zero-filled before first use; the
+  // kernel leaves them zero-filled). nullptr / 1: no split.
+  void* ws;
+  int32_t splits;
 };
 
 // While alive on the calling thread, launches described on that thread set
@@ -76,6 +81,11 @@ hipError_t launch(const Launch& L, hipStream_t stream);
 
 // Record the status of an ABI call for xrmm_last_error ("" when XRMM_OK).
 int set_status(int code, const std::string& msg);
+
+// MatMulNBits split-K: splits for the geometry (1: none) and the workspace
+// bytes they need (0 when there is no split).
+int gemm_splits(const Launch& L);
+int64_t gemm_workspace_bytes(const Launch& L, int splits);
 
 // W [N, K] in out_dtype (see xrmm_dequantize).
 hipError_t launch_dequantize(const Launch& L, void* W, int out_dtype, hipStream_t stream);

@@ -681,6 +681,10 @@ struct xrmm_op {
           return xrmm_matmul_nbits_prepacked(dptr("aT"), packed, dptr("scalesT"), dptr("zeroPointsT"),
                                              dptr("zeroPointsT") ? zd : XRMM_UNSPECIFIED, dptr("biasT"), optr("yT"), p.M,
                                              p.K, p.N, p.bits, p.block_size, p.dtype, s);
+        if (workspace)
+          return xrmm_matmul_nbits_ws(dptr("aT"), dptr("bT"), dptr("scalesT"), dptr("zeroPointsT"),
+                                      dptr("zeroPointsT") ? zd : XRMM_UNSPECIFIED, dptr("biasT"), optr("yT"), p.M, p.K,
+                                      p.N, p.bits, p.block_size, p.dtype, workspace, int64_t(workspace_bytes), s);
         return xrmm_matmul_nbits(dptr("aT"), dptr("bT"), dptr("scalesT"), dptr("zeroPointsT"), dptr("zeroPointsT") ? zd : XRMM_UNSPECIFIED,
                                  dptr("biasT"), optr("yT"), p.M, p.K, p.N, p.bits, p.block_size, p.dtype, s);
       case xrmm::OP_MLP: {
@@ -772,6 +776,8 @@ int xrmm_prepare(const xrmm_request* request, const xrmm_options* options, xrmm_
     uint64_t ws = 0;
     if (p.contract->op == OP_QMOE) ws = uint64_t(xrmm_qmoe_workspace_bytes(p.T, p.k, p.H, p.I));
     if (p.contract->op == OP_GBQ) ws = 4;
+    if (p.contract->op == xrmm::OP_MATMUL && !weights_need_float32(p))  // split-K over workgroups
+      ws = uint64_t(xrmm_matmul_nbits_workspace_bytes(p.M, p.K, p.N, p.bits, p.block_size, p.dtype));
     total += align256(ws);
     if (total > o.memory_limit_bytes) throw Invalid("Extended heap memory limit exceeded");
 
@@ -810,6 +816,10 @@ int xrmm_prepare(const xrmm_request* request, const xrmm_options* options, xrmm_
     }
     op->workspace = ws ? op->arena + off : nullptr;
     op->workspace_bytes = ws;
+    if (ws && p.contract->op == xrmm::OP_MATMUL) {  // the split-K counters start at zero (and stay there)
+      hip_check(hipMemsetAsync(op->workspace, 0, ws, op->stream), "hipMemsetAsync (workspace)");
+      hip_check(hipStreamSynchronize(op->stream), "hipStreamSynchronize");
+    }
     const int32_t zk = p.zp_dtype;
     const int code = p.contract->op;
     const char* k = nullptr;

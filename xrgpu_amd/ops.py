@@ -130,10 +130,39 @@ def matmul_nbits(A, B, scales, zero_points=None, bias=None, *, K=None, N=None, b
     dev = _check_dev(A, B, scales, zero_points, bias, out)
     if out is None:
         out = torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
-    nat.check(nat.lib().xrmm_matmul_nbits(_ptr(A), _ptr(B), _ptr(scales), _ptr(zero_points),
-                                          _zp_dtype(zero_points), _ptr(bias), _ptr(out), M, K, N,
-                                          bits, block_size, _t1(A), _stream(stream, dev)))
+    lib = nat.lib()
+    s = _stream(stream, dev)
+    need = lib.xrmm_matmul_nbits_workspace_bytes(M, K, N, bits, block_size, _t1(A)) if M > 16 else 0
+    if need > 0:
+        ws = _workspace(A.device, s, need, stream)
+        nat.check(lib.xrmm_matmul_nbits_ws(_ptr(A), _ptr(B), _ptr(scales), _ptr(zero_points), _zp_dtype(zero_points),
+                                           _ptr(bias), _ptr(out), M, K, N, bits, block_size, _t1(A), _ptr(ws),
+                                           ws.numel(), s))
+        return out
+    nat.check(lib.xrmm_matmul_nbits(_ptr(A), _ptr(B), _ptr(scales), _ptr(zero_points),
+                                    _zp_dtype(zero_points), _ptr(bias), _ptr(out), M, K, N,
+                                    bits, block_size, _t1(A), s))
     return out
+
+
+# Split-K workspaces of matmul_nbits, one per (device, stream): zero-filled when
+# allocated, and every call leaves them zero-filled, so consecutive calls on a
+# stream share one; calls on different streams never share.
+_WORKSPACES = {}
+
+
+def _workspace(device, stream_handle, nbytes, stream=None):
+    key = (device.index, stream_handle)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 0 if ws is None else 2 * ws.numel())
+        if stream is None:  # the current stream: the one the call enqueues on
+            ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        else:
+            with torch.cuda.stream(stream):  # zero-filled in the stream that will use it
+                ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
 
 
 def prepacked_bytes(N, K, bits=4, block_size=32):
