@@ -30,13 +30,17 @@ FP16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, published
 PROFILES = os.path.join(ROOT, "profiles")
 SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048": 4, "qmoe_mixtral_t1": 6,
          "bnb4_nf4_m1": 7, "gbq_embed_t2048": 8, "int8a_decode_m1": 1, "f32_k2048_m1": 0,
-         "mlp_prefill_m64": 9, "prefill_m2048_prepacked": 4}
+         "mlp_prefill_m64": 9, "prefill_m2048_prepacked": 4, "down_proj_m64": 10}
 # The CPU-oracle workload on the GPU: MatMulNBits float32, M=1, K=N=2048,
 # block_size 32, packed zero points (2,703,360 algorithmic bytes per call)
 F32 = dict(M=1, K=2048, N=2048, bs=32)
 # MatMulNBitsMlp prefill: 64 rows, K=2048, N=5632 (the TinyLlama-1.1B FFN),
 # block_size 32, normScale, SiLU; 2*2*M*K*N flops per call
 MLP64 = dict(M=64, K=2048, N=5632, bs=32)
+# MatMulNBits down projection of the Llama-3-8B FFN for 64 tokens (K=14336,
+# N=4096, block_size 32, packed zero points): 32 output tiles for 256 CUs, the
+# split-K GEMM's case
+DOWN64 = dict(M=64, K=14336, N=4096, bs=32)
 # com.microsoft.MatMulBnb4 decode: the FFN up-projection shape in NF4, blocks of 64
 BNB4 = dict(M=1, K=4096, N=14336, bs=64)
 # com.microsoft.GatherBlockQuantized: a 128256 x 4096 4-bit embedding table
@@ -137,6 +141,15 @@ def make_replicas(torch, name, R, dev, seed):
         scales = torch.rand((q["rows"], q["width"] // q["bs"]), device=dev, generator=g) * 0.02
         idx = [torch.randint(0, q["rows"], (q["n"],), dtype=torch.int32, device=dev, generator=g) for _ in range(R)]
         return dict(A=data, scales=scales, reps=idx)
+    if name == "down_proj_m64":
+        q = DOWN64
+        K, N, bs = q["K"], q["N"], q["bs"]
+        kb = K // bs
+        A = torch.randn((q["M"], K), device=dev, generator=g).half()
+        for _ in range(R):
+            reps.append(dict(B=_gen_weights(torch, g, N, kb, bs // 2, dev), S=_scales(torch, g, (N, kb), dev),
+                             Z=torch.randint(0, 256, (N, (kb + 1) // 2), dtype=torch.uint8, device=dev, generator=g)))
+        return dict(A=A, reps=reps, K=K, N=N, bs=bs)
     if name == "mlp_prefill_m64":
         q = MLP64
         K, N, bs = q["K"], q["N"], q["bs"]
@@ -196,6 +209,13 @@ def step_fn(ops, name, w):
             return ops.matmul_nbits_qkv(A, r["qB"], r["qS"], r["kB"], r["kS"], r["vB"], r["vS"], norm_scale=w["gamma"],
                                         block_size=w["bs"], q_zero_points=r["qZ"], k_zero_points=r["kZ"],
                                         v_zero_points=r["vZ"], want_residual=False)
+        return f
+    if name == "down_proj_m64":
+        Y = torch.empty((DOWN64["M"], w["N"]), dtype=torch.float16, device=A.device)
+
+        def f(i):
+            r = reps[i % len(reps)]
+            return ops.matmul_nbits(A, r["B"], r["S"], r["Z"], block_size=w["bs"], out=Y)
         return f
     if name == "mlp_prefill_m64":
         def f(i):
@@ -464,7 +484,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     results = {}
-    names = ["decode_up_m1", "prefill_m2048", "prefill_m2048_prepacked", "qkv_gqa_m4", "mlp_swiglu_m16", "mlp_prefill_m64", "f32_k2048_m1",
+    names = ["decode_up_m1", "prefill_m2048", "prefill_m2048_prepacked", "qkv_gqa_m4", "mlp_swiglu_m16", "mlp_prefill_m64", "down_proj_m64", "f32_k2048_m1",
              "qmoe_mixtral_t1", "bnb4_nf4_m1", "gbq_embed_t2048", "int8a_decode_m1"]
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
@@ -472,7 +492,7 @@ def main():
         # every leg rotates more weight bytes than the 256 MB Infinity Cache
         # holds (Qkv: 24 x 13.7 MB = 328 MB)
         R = {"prefill_m2048": 2, "prefill_m2048_prepacked": 2, "qmoe_mixtral_t1": 2, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24,
-             "f32_k2048_m1": 100, "mlp_prefill_m64": 24}.get(name, args.replicas)
+             "f32_k2048_m1": 100, "mlp_prefill_m64": 24, "down_proj_m64": 12}.get(name, args.replicas)
         w = make_replicas(torch, name, R, dev, seed=SEEDS[name])
         fn = step_fn(ops, name, w)
         steps = args.steps if not name.startswith("prefill_m2048") else max(10, args.steps // 10)
@@ -566,6 +586,19 @@ def main():
             "bytes_per_launch": nbytes, "replicas": r["replicas"],
             "kernel": ops.select_kernel("MatMulNBitsMlp", q["M"], q["K"], q["N"], 4, q["bs"]),
             "traffic": traffic_of("mlp_prefill_m64_splitk.md", ops.select_kernel("MatMulNBitsMlp", q["M"], q["K"], q["N"], 4, q["bs"]))}
+    if "down_proj_m64" in results:
+        r, q = results["down_proj_m64"], DOWN64
+        fl = 2 * q["M"] * q["K"] * q["N"]
+        kb = q["K"] // q["bs"]
+        nbytes = q["N"] * (q["K"] // 2 + kb * 2 + (kb + 1) // 2) + q["M"] * (q["K"] + q["N"]) * 2
+        tf = fl / (r["ms"] * 1e-3) / 1e12
+        gbs = nbytes / (r["ms"] * 1e-3) / 1e9
+        out["down_proj_m64"] = {
+            "workload": "MatMulNBits fp16 M=64 K=14336 N=4096 bs=32 packed zp (Llama-3-8B FFN down projection, 64 tokens)",
+            "us": round(r["ms"] * 1e3, 3), "tflops": round(tf, 2), "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 4),
+            "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes,
+            "replicas": r["replicas"],
+            "kernel": ops.select_kernel("MatMulNBits", q["M"], q["K"], q["N"], 4, q["bs"], zp="packed") + " (split-K)"}
     if "f32_k2048_m1" in results:
         r, q = results["f32_k2048_m1"], F32
         nbytes = 2_703_360
