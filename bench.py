@@ -562,7 +562,8 @@ def main():
             "workload": "the same call on weights prepacked once by xrmm_prepack_weights (what the request "
                         "lifecycle does at prepare)",
             "us": round(r["ms"] * 1e3, 2), "tflops": round(tf, 2), "frac": round(tf / FP16_PEAK_TFLOPS, 4),
-            "kernel": "gemm_q4_big (prepacked weights)"}
+            "kernel": "gemm_q4_big (prepacked weights)",
+            "traffic": traffic_of("prefill_m2048_prepacked_gemm.md", "gemm_q4_big_prepacked")}
     for name, nbytes, summary, kern in (
             ("qkv_gqa_m4", 13_656_064, "qkv_gqa_m4_gemv.md",
              ops.select_kernel("MatMulNBitsQkv", 4, 4096, 4096, 4, 64, zp="packed")),
@@ -598,7 +599,8 @@ def main():
             "us": round(r["ms"] * 1e3, 3), "tflops": round(tf, 2), "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 4),
             "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes,
             "replicas": r["replicas"],
-            "kernel": ops.select_kernel("MatMulNBits", q["M"], q["K"], q["N"], 4, q["bs"], zp="packed") + " (split-K)"}
+            "kernel": ops.select_kernel("MatMulNBits", q["M"], q["K"], q["N"], 4, q["bs"], zp="packed") + " (split-K)",
+            "traffic": traffic_of("down_proj_m64_gemm.md", "gemm_q4_mfma")}
     if "f32_k2048_m1" in results:
         r, q = results["f32_k2048_m1"], F32
         nbytes = 2_703_360
