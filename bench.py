@@ -422,25 +422,89 @@ def cpu_baseline():
 def stream_ceiling(torch, ops, steps, warmup, nbytes=33_067_008, R=10):
     """The plain read of the decode workload's bytes: R rotating buffers of
     ``nbytes`` (330 MB, beyond the Infinity Cache), one buffer read per step
-    by xrmm_stream_read, timed like the decode leg; best of 1, 2, 4 and 8
-    loads per lane."""
+    by xrmm_stream_read_ex, timed like the decode leg. Swept over the one-shot
+    grid (every lane issues 1, 2, 4 or 8 loads and retires) and persistent
+    grids of 4 or 8 workgroups per CU walking the buffer, each with
+    non-temporal and default-policy loads; the best is the ceiling."""
     g = torch.Generator(device="cuda")
     g.manual_seed(11)
     bufs = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda", generator=g) for _ in range(R)]
     sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    variants = [("oneshot_nt", u, True, 0) for u in (1, 2, 4, 8)]
+    variants += [("oneshot_default", u, False, 0) for u in (1, 4)]
+    variants += [(f"persistent{wpc}_{'nt' if nt else 'default'}", u, nt, wpc * cus)
+                 for wpc in (4, 8) for nt in (True, False) for u in (2, 4)]
     per = {}
-    for u in (1, 2, 4, 8):
-        ms, _, _ = time_steps(torch, lambda i, u=u: ops.stream_read(bufs[i % R], loads_per_lane=u, sink=sink),
-                              steps, warmup)
-        per[u] = ms
+    for kind, u, nt, wg in variants:
+        ms, _, _ = time_steps(torch, lambda i, u=u, nt=nt, wg=wg: ops.stream_read(
+            bufs[i % R], loads_per_lane=u, sink=sink, nontemporal=nt, workgroups=wg), steps, warmup)
+        per[f"{kind}_u{u}"] = ms
     best = min(per, key=per.get)
     ms = per[best]
     del bufs
     torch.cuda.empty_cache()
-    return {"what": f"plain 16-byte non-temporal read of {nbytes} B (the decode GEMV's bytes), {R} rotating buffers",
+    return {"what": f"plain 16-byte read of {nbytes} B (the decode GEMV's bytes), {R} rotating buffers, "
+                    f"best of one-shot and persistent grids, non-temporal and default loads",
             "us": round(ms * 1e3, 3), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2),
-            "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "loads_per_lane": best,
-            "us_by_loads_per_lane": {str(k): round(v * 1e3, 3) for k, v in per.items()}}
+            "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "best": best,
+            "us_by_variant": {k: round(v * 1e3, 3) for k, v in per.items()}}
+
+
+def mfma_ceiling(torch, ops, launches=6, target_ms=2.0):
+    """The sustained v_mfma_f32_32x32x16_f16 rate on this box: back-to-back
+    MFMAs on random N(0, 1) binary16 operands (a GEMM's switching activity)
+    on every CU, swept over 4, 8 and 16 waves per CU and 4 or 8 independent
+    accumulators, then the best shape again on all-zero operands. Every wave
+    records its loop's shader-clock cycles (s_memtime) and the constant-rate
+    counter (s_memrealtime, 100 MHz) at its start and end, which give the
+    clock the MFMAs ran at and the MFMA issue interval per SIMD. The
+    ceiling is the best random-operand rate."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    nb = ops.mfma_peak_operand_bytes()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(12)
+    rnd = torch.randn(nb // 2, device="cuda", generator=g).half()
+    zero = torch.zeros(nb // 2, device="cuda", dtype=torch.float16)
+
+    def run(opnd, wpc, nacc, iters):
+        wg, waves = cus * wpc // 4, 4
+        clocks = torch.zeros(4 * wg * waves, dtype=torch.int64, device="cuda")
+        for _ in range(2):
+            ops.mfma_peak(opnd, clocks, workgroups=wg, waves=waves, accumulators=nacc, iters=iters)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(launches):
+            ops.mfma_peak(opnd, clocks, workgroups=wg, waves=waves, accumulators=nacc, iters=iters)
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e) / launches
+        c = clocks.view(-1, 4).double()
+        cyc, r0, r1 = c[:, 0], c[:, 1], c[:, 2]
+        span = float(r1.max() - r0.min())            # ticks of 10 ns over all waves of the last launch
+        sclk = float(cyc.sum() / (r1 - r0).sum()) * 0.1  # GHz: shader cycles per 10 ns tick / 10
+        fl = ops.mfma_peak_flops(wg, waves, iters)
+        tf = fl / (ms * 1e-3) / 1e12
+        mfma_per_simd = wg * waves * 16 * iters / (cus * 4)
+        return {"waves_per_cu": wpc, "accumulators": nacc, "iters": iters, "us_per_launch": round(ms * 1e3, 1),
+                "tflops": round(tf, 1), "frac_of_2500": round(tf / FP16_PEAK_TFLOPS, 4), "sclk_ghz": round(sclk, 3),
+                "wave_span_over_launch": round(span * 1e-5 / ms, 3),
+                "mean_wave_loop_over_span": round(float((r1 - r0).mean()) / span, 3),
+                "cycles_per_mfma_per_simd": round(span * sclk * 10 / mfma_per_simd, 2)}
+
+    sweep = []
+    for wpc in (4, 8, 16):
+        for nacc in (4, 8):
+            # about target_ms per launch at 1.3 PFLOP/s
+            iters = max(64, int(target_ms * 1e-3 * 1.3e15 / (cus * wpc * 16 * 32768)))
+            sweep.append(run(rnd, wpc, nacc, iters))
+    best = max(sweep, key=lambda r: r["tflops"])
+    zero_run = run(zero, best["waves_per_cu"], best["accumulators"], best["iters"])
+    del rnd, zero
+    return {"mfma": "v_mfma_f32_32x32x16_f16", "operands": "random N(0,1) binary16", "tflops": best["tflops"],
+            "frac_of_2500": best["frac_of_2500"], "sclk_ghz": best["sclk_ghz"], "best": best,
+            "sweep": sweep, "zero_operands": zero_run}
 
 
 def copy_calibration():
@@ -541,6 +605,7 @@ def main():
             "stream_ceiling": ceiling,
             "decode_over_stream_ceiling": round(ceiling["us"] / (r["ms"] * 1e3), 4),
         }
+    mceil = mfma_ceiling(torch, ops) if any(n.startswith("prefill_m2048") for n in results) else None
     if "prefill_m2048" in results:
         r = results["prefill_m2048"]
         fl = 2 * 2048 * 4096 * 14336
@@ -553,7 +618,9 @@ def main():
                                        "kernel": ops.select_kernel("MatMulNBits", 2048, 4096, 14336, 4, 128, zp="packed"),
                                        "traffic": traffic_of("prefill_m2048_gemm.md", ops.select_kernel(
                                            "MatMulNBits", 2048, 4096, 14336, 4, 128, zp="packed"))},
-                          "dense_fp16_library": dense_fp16_reference(torch)}
+                          "dense_fp16_library": dense_fp16_reference(torch),
+                          "mfma_ceiling": mceil,
+                          "frac_of_mfma_ceiling": round(tf / mceil["tflops"], 4)}
     if "prefill_m2048_prepacked" in results:
         r = results["prefill_m2048_prepacked"]
         fl = 2 * 2048 * 4096 * 14336
@@ -562,6 +629,7 @@ def main():
             "workload": "the same call on weights prepacked once by xrmm_prepack_weights (what the request "
                         "lifecycle does at prepare)",
             "us": round(r["ms"] * 1e3, 2), "tflops": round(tf, 2), "frac": round(tf / FP16_PEAK_TFLOPS, 4),
+            "frac_of_mfma_ceiling": round(tf / mceil["tflops"], 4),
             "kernel": "gemm_q4_big (prepacked weights)",
             "traffic": traffic_of("prefill_m2048_prepacked_gemm.md", "gemm_q4_big_prepacked")}
     for name, nbytes, summary, kern in (

@@ -378,6 +378,31 @@ int xrmm_matmul_nbits_int8a_noalloc(const void* A, const void* B, const void* sc
  * compared with. */
 int xrmm_stream_read(const void* src, uint64_t bytes, void* sink, int32_t loads_per_lane, void* stream);
 
+/* Measurement, as above, with the cache policy and grid chosen: `nontemporal`
+ * 1 reads with non-temporal loads, 0 with the default policy; `workgroups` 0
+ * launches the one-shot grid (every lane issues its loads once and retires),
+ * a positive count launches that many 256-lane workgroups that walk the
+ * buffer in strides of the whole grid (a persistent read). */
+int xrmm_stream_read_ex(const void* src, uint64_t bytes, void* sink, int32_t loads_per_lane, int32_t nontemporal,
+                        int32_t workgroups, void* stream);
+
+/* Measurement (no counterpart in the reference): the sustained rate of
+ * back-to-back v_mfma_f32_32x32x16_f16 on the caller's binary16 operands
+ * (`operands`: xrmm_mfma_peak_operand_bytes() bytes, 16-byte aligned; random
+ * values give a real GEMM's switching activity, hence its clock). Launches
+ * `workgroups` workgroups of `waves` (1..4) waves, each wave issuing
+ * 16 * `iters` MFMAs over `accumulators` (4 or 8) independent accumulators
+ * (xrmm_mfma_peak_flops(workgroups, waves, iters) flops in total). Lane 0 of
+ * global wave w writes four uint64 words to clocks[4w..4w+3]: its loop's
+ * shader-clock cycles (s_memtime), the constant-rate counter (s_memrealtime)
+ * at the loop's start and at its end, and its workgroup index. `sink` (4
+ * bytes) is written only in the practically impossible case that the
+ * accumulators sum to a fixed constant. */
+int64_t xrmm_mfma_peak_operand_bytes(void);
+int64_t xrmm_mfma_peak_flops(int32_t workgroups, int32_t waves, int32_t iters);
+int xrmm_mfma_peak(const void* operands, void* sink, void* clocks, int32_t workgroups, int32_t waves,
+                   int32_t accumulators, int32_t iters, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

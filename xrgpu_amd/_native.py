@@ -72,6 +72,10 @@ def _sig(lib):
     s("xrmm_matmul_nbits_int8a_noalloc", ctypes.c_int, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i32,
       _i32, _i32, _vp)
     s("xrmm_stream_read", ctypes.c_int, _vp, ctypes.c_uint64, _vp, _i32, _vp)
+    s("xrmm_stream_read_ex", ctypes.c_int, _vp, ctypes.c_uint64, _vp, _i32, _i32, _i32, _vp)
+    s("xrmm_mfma_peak_operand_bytes", _i64)
+    s("xrmm_mfma_peak_flops", _i64, _i32, _i32, _i32)
+    s("xrmm_mfma_peak", ctypes.c_int, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp)
     s("xrmm_matmul_nbits_workspace_bytes", _i64, _i64, _i64, _i64, _i32, _i32, _i32)
     s("xrmm_matmul_nbits_ws", ctypes.c_int, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32,
       _vp, _i64, _vp)

@@ -498,12 +498,43 @@ def int8a_workspace_bytes(M, K) -> int:
     return max(n, 16)
 
 
-def stream_read(buf, *, loads_per_lane=4, sink=None, stream=None):
+def stream_read(buf, *, loads_per_lane=4, sink=None, nontemporal=True, workgroups=0, stream=None):
     """Read ``buf`` (a device tensor of a multiple of 16 bytes) once on the GPU
-    with 16-byte loads: the plain read rate a decode GEMV is compared with."""
+    with 16-byte loads: the plain read rate a decode GEMV is compared with.
+    ``nontemporal`` picks the cache policy; ``workgroups`` 0 launches the
+    one-shot grid, a positive count a persistent grid of that many
+    workgroups."""
     dev = _check_dev(buf, sink)
     if sink is None:
         sink = torch.zeros(1, dtype=torch.int32, device=buf.device)
-    nat.check(nat.lib().xrmm_stream_read(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink),
-                                         int(loads_per_lane), _stream(stream, dev)))
+    nat.check(nat.lib().xrmm_stream_read_ex(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink),
+                                            int(loads_per_lane), 1 if nontemporal else 0, int(workgroups),
+                                            _stream(stream, dev)))
     return sink
+
+
+def mfma_peak_operand_bytes():
+    return int(nat.lib().xrmm_mfma_peak_operand_bytes())
+
+
+def mfma_peak_flops(workgroups, waves, iters):
+    return int(nat.lib().xrmm_mfma_peak_flops(int(workgroups), int(waves), int(iters)))
+
+
+def mfma_peak(operands, clocks, *, workgroups, waves=4, accumulators=4, iters, sink=None, stream=None):
+    """Back-to-back v_mfma_f32_32x32x16_f16 on ``operands`` (binary16,
+    mfma_peak_operand_bytes() bytes) from ``workgroups`` workgroups of
+    ``waves`` waves, ``16 * iters`` MFMAs per wave over ``accumulators``
+    independent accumulators; ``clocks`` (int64, 4 per wave) receives each
+    wave's shader-clock cycles, constant-rate counter at its loop's start and
+    end, and workgroup index."""
+    dev = _check_dev(operands, clocks, sink)
+    if operands.numel() * operands.element_size() < mfma_peak_operand_bytes():
+        raise nat.XrmmInvalid("mfma peak: operand buffer too small")
+    if clocks.dtype != torch.int64 or clocks.numel() < 4 * workgroups * waves:
+        raise nat.XrmmInvalid("mfma peak: clocks must be int64 with 4 * workgroups * waves elements")
+    if sink is None:
+        sink = torch.zeros(1, dtype=torch.float32, device=operands.device)
+    nat.check(nat.lib().xrmm_mfma_peak(_ptr(operands), _ptr(sink), _ptr(clocks), int(workgroups), int(waves),
+                                       int(accumulators), int(iters), _stream(stream, dev)))
+    return clocks
