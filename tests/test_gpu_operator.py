@@ -91,6 +91,30 @@ def test_splitk_lifecycle_runs_twice_on_its_workspace(gpu):
     assert np.array_equal(y1.data.view(np.uint16), y2.data.view(np.uint16))
 
 
+def test_splitk_workspace_is_optional_under_the_memory_limit(gpu):
+    """A memory limit just above the request's own bytes leaves no room for
+    the split-K workspace: prepare still succeeds and the run (unsplit)
+    meets the oracle."""
+    from xrgpu_amd import _native as nat
+    rng = np.random.default_rng(32)
+    M, K, N, bs = 40, 8192, 512, 64
+    ws = nat.lib().xrmm_matmul_nbits_workspace_bytes(M, K, N, 4, bs, nat.F16)
+    assert ws > 4096
+    ins = rand_mnb(rng, M, K, N, bs)
+    data = sum((v.nbytes + 255) // 256 * 256 for v in ins.values()) + (M * N * 2 + 255) // 256 * 256
+    with op.Operator.prepare("", request(MNB, ins, {"N": N, "block_size": bs}),
+                             op.Options(memory_limit_bytes=data + 1024)) as o:
+        o.run()
+        (y,) = o.read_outputs()
+    ref = O.matmul_nbits(ins["aT"], ins["bT"], ins["scalesT"], ins["zeroPointsT"], ins["biasT"], K=K, N=N,
+                         block_size=bs)
+    ok, err, lim = O.tolerance_ok(y.data, ref, np.float16)
+    assert ok, (err, lim)
+    with pytest.raises(op.XrmmInvalid, match="Extended heap memory limit exceeded"):
+        op.Operator.prepare("", request(MNB, ins, {"N": N, "block_size": bs}),
+                            op.Options(memory_limit_bytes=data - 256))
+
+
 def test_requested_float32_storage_holds_the_float16_values(gpu):
     rng = np.random.default_rng(1)
     ins = rand_mnb(rng, 2, 256, 64, 32)

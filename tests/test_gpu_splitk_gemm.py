@@ -124,3 +124,56 @@ def test_splitk_rejects_a_short_workspace(gpu):
     rc = nat.lib().xrmm_matmul_nbits_ws(x.data_ptr(), x.data_ptr(), x.data_ptr(), None, nat.UNSPECIFIED, None,
                                         x.data_ptr(), M, K, N, 4, bs, nat.F16, ws.data_ptr(), need - 1, None)
     assert rc == nat.XRMM_EINVAL and "workspace" in nat.last_error()
+
+
+def _check(y, A, B, S, Z, b, K, N, bs):
+    ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs)
+    ok, err, lim = O.tolerance_ok(host(y), ref, np.float16)
+    assert ok, (err, lim)
+
+
+@pytest.mark.parametrize("caller_workspace", [False, True])
+def test_splitk_geometries_under_graph_capture(gpu, caller_workspace):
+    """Two split-K geometries captured into two graphs on torch's shared
+    capture stream, the smaller one replayed first, each replayed several
+    times with eager split-K calls and synchronisations in between; every
+    replay meets the oracle. Without a caller workspace the captured calls
+    run unsplit (nothing captured depends on the front end's own
+    workspaces); with one workspace per graph, allocated and zero-filled
+    outside capture, they run split."""
+    rng = np.random.default_rng(61)
+    shapes = [(40, 8192, 512, 64), (17, 8192, 512, 32)]
+    cases = [case(rng, M, K, N, bs, "packed", True) for M, K, N, bs in shapes]
+    dv = [[dev(x) for x in c] for c in cases]
+    outs = [torch.empty((M, N), dtype=torch.float16, device="cuda") for M, K, N, bs in shapes]
+    ws = [torch.zeros(ops().matmul_nbits_workspace_bytes(M, K, N, 4, bs), dtype=torch.uint8, device="cuda")
+          if caller_workspace else None for M, K, N, bs in shapes]
+    assert all(ops().matmul_nbits_workspace_bytes(M, K, N, 4, bs) > 0 for M, K, N, bs in shapes)
+
+    def call(i):
+        A, B, S, Z, b = dv[i]
+        M, K, N, bs = shapes[i]
+        ops().matmul_nbits(A, B, S, Z, b, block_size=bs, out=outs[i], workspace=ws[i])
+
+    for i in range(2):  # warm-up outside capture
+        call(i)
+    torch.cuda.synchronize()
+    graphs = []
+    for i in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            call(i)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i in (1, 0):  # the smaller graph first
+            outs[i].zero_()
+            graphs[i].replay()
+            torch.cuda.synchronize()
+            _check(outs[i], *cases[i], shapes[i][1], shapes[i][2], shapes[i][3])
+            # eager split-K work on the default stream between replays
+            A, B, S, Z, b = dv[1 - i]
+            M, K, N, bs = shapes[1 - i]
+            y = ops().matmul_nbits(A, B, S, Z, b, block_size=bs)
+            torch.cuda.synchronize()
+            _check(y, *cases[1 - i], K, N, bs)

@@ -324,10 +324,10 @@ int device_cus();
 template <int ZPK, int SPC, bool PK = false>
 inline hipError_t launch_gemm_big(const Launch& L, hipStream_t st) {
   auto kern = k_gemm_q4_big<ZPK, SPC, PK>;
-  // more than 64 KB of dynamic LDS needs the attribute; set once per instantiation
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     static_cast<int>(GB_LDS));
+  // more than 64 KB of dynamic LDS needs the attribute; set once per
+  // instantiation and device
+  static std::atomic<int> done[kMaxDevices];
+  const hipError_t attr = raise_lds_cap(reinterpret_cast<const void*>(kern), static_cast<int>(GB_LDS), done);
   if (attr != hipSuccess) return attr;
   const GemmTiles t = gemm_tiles(L.M, L.p[0].N, device_cus());
   const int64_t mt = (L.M + GB_M - 1) / GB_M;

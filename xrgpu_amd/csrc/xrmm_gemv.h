@@ -493,15 +493,11 @@ inline hipError_t launch_gemv6(const Launch& L, hipStream_t st) {
   const int64_t lds = gemv_lds(L, TILES).total;
   auto kern = k_gemv_q4<ZPK, SPC, OP, TILES, DB, STAGE>;
   if (lds > 64 * 1024) {
-    static bool raised = false;  // per instantiation
-    if (!raised) {
-      // Raises the dynamic-LDS cap where the runtime keeps one; an error here
-      // surfaces from the launch itself if the size is really unsupported.
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(kMaxLds));
-      (void)hipGetLastError();
-      raised = true;
-    }
+    // Raises the dynamic-LDS cap where the runtime keeps one; an error here
+    // surfaces from the launch itself if the size is really unsupported.
+    static std::atomic<int> done[kMaxDevices];  // per instantiation and device
+    (void)raise_lds_cap(reinterpret_cast<const void*>(kern), static_cast<int>(kMaxLds), done);
+    (void)hipGetLastError();
   }
   hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(grid)), dim3(GEMV_NT), static_cast<size_t>(lds), st, L);
   return hipGetLastError();

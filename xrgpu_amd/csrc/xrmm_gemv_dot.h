@@ -651,13 +651,9 @@ inline hipError_t launch_dot6(const Launch& L, hipStream_t st) {
   const size_t lds = dot_lds_bytes(a, W);
   auto kern = k_gemv_dot<ZPK, SPC, CPL, C, dot_p(MR, CPL), MR, W, MP, OPK, SK>;
   if (lds > 64 * 1024) {
-    static bool raised = false;  // per instantiation
-    if (!raised) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(160 * 1024 - 1024));
-      (void)hipGetLastError();
-      raised = true;
-    }
+    static std::atomic<int> done[kMaxDevices];  // per instantiation and device
+    (void)raise_lds_cap(reinterpret_cast<const void*>(kern), static_cast<int>(160 * 1024 - 1024), done);
+    (void)hipGetLastError();
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(W * 64), lds, st, a);
   return hipGetLastError();

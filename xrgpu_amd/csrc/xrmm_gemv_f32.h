@@ -287,8 +287,8 @@ inline hipError_t launch_f32_3(const Launch& L, hipStream_t st) {
   const size_t lds = f32_act_bytes<MR>(nchunk) + size_t(kF32W) * a.meta_bytes;
   auto kern = k_gemv_f32<ZPK, CPL, kF32C, MR, kF32W>;
   if (lds > 64 * 1024) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    static std::atomic<int> done[kMaxDevices];  // per instantiation and device
+    const hipError_t attr = raise_lds_cap(reinterpret_cast<const void*>(kern), 160 * 1024, done);
     if (attr != hipSuccess) return attr;
   }
   const uint32_t waves = static_cast<uint32_t>((P.N + kF32C - 1) / kF32C);

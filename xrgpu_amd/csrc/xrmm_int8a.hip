@@ -127,7 +127,6 @@ hipError_t launch_t(const Int8aArgs& a, hipStream_t st) {
 static __device__ __align__(256) uint8_t scratch[kI8aScratchBytes];
 
 namespace {
-constexpr int kMaxDevices = 64;
 std::atomic<void*> g_scratch_ptr[kMaxDevices];
 std::mutex g_scratch_mu;
 }  // namespace

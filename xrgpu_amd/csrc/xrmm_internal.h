@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <string>
 
 namespace xrmm {
@@ -101,5 +102,22 @@ hipError_t launch_prepack(const Launch& L, void* out, hipStream_t stream);
 bool prepacked_ok(const Launch& L);
 // MatMulNBits with L.p[0].B prepacked (prepacked_ok must hold).
 hipError_t launch_prepacked(const Launch& L, hipStream_t stream);
+
+// Raises a kernel's dynamic-LDS cap to `bytes` once per device. `done` is a
+// per-kernel array of flags the call site owns (a function-local static,
+// zero-initialised at load time); the flags are atomic, so host threads may
+// launch concurrently, and a repeated attribute call from a race is harmless.
+// Device ordinals beyond the table are not cached (the attribute is set on
+// every launch there).
+constexpr int kMaxDevices = 64;
+inline hipError_t raise_lds_cap(const void* kern, int bytes, std::atomic<int> (&done)[kMaxDevices]) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (done[dev].load(std::memory_order_acquire) != 0) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done[dev].store(1, std::memory_order_release);
+  return e;
+}
 
 }  // namespace xrmm

@@ -548,13 +548,9 @@ hipError_t launch_gemv(const MoeArgs& a, int gpw, hipStream_t st) {
   const size_t lds = static_cast<size_t>(fc2 ? a.seg * per_step_lds : moe_kpad(a.H, BITS) + 2 * a.E + MOE_MAX_K) * 4;
   auto kern = k_moe_gemv<BITS, SM, ST>;
   if (lds > 64 * 1024) {
-    static bool raised = false;  // per instantiation
-    if (!raised) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(kMoeMaxLds));
-      (void)hipGetLastError();
-      raised = true;
-    }
+    static std::atomic<int> done[kMaxDevices];  // per instantiation and device
+    (void)raise_lds_cap(reinterpret_cast<const void*>(kern), static_cast<int>(kMoeMaxLds), done);
+    (void)hipGetLastError();
   }
   const int64_t tiles = (Nd + 32 * gpw - 1) / (32 * gpw);
   const int64_t blocks = a.T * a.k * tiles * (fc2 ? a.ks : 1);

@@ -776,10 +776,18 @@ int xrmm_prepare(const xrmm_request* request, const xrmm_options* options, xrmm_
     uint64_t ws = 0;
     if (p.contract->op == OP_QMOE) ws = uint64_t(xrmm_qmoe_workspace_bytes(p.T, p.k, p.H, p.I));
     if (p.contract->op == OP_GBQ) ws = 4;
-    if (p.contract->op == xrmm::OP_MATMUL && !weights_need_float32(p))  // split-K over workgroups
-      ws = uint64_t(xrmm_matmul_nbits_workspace_bytes(p.M, p.K, p.N, p.bits, p.block_size, p.dtype));
     total += align256(ws);
     if (total > o.memory_limit_bytes) throw Invalid("Extended heap memory limit exceeded");
+    // The split-K workspace of MatMulNBits is a performance option, not part of
+    // the request's memory: it is reserved only when it fits the limit beside
+    // the data, and the call runs unsplit otherwise.
+    if (p.contract->op == xrmm::OP_MATMUL && !weights_need_float32(p)) {
+      const uint64_t sk = uint64_t(xrmm_matmul_nbits_workspace_bytes(p.M, p.K, p.N, p.bits, p.block_size, p.dtype));
+      if (sk && total + align256(sk) <= o.memory_limit_bytes) {
+        ws = sk;
+        total += align256(sk);
+      }
+    }
 
     hip_check(hipGetDevice(&op->device), "hipGetDevice");
     hipDeviceProp_t prop;

@@ -330,15 +330,13 @@ hipError_t launch_bnb4_fast(const Bnb4Args& a, hipStream_t st) {
   const dim3 grid(static_cast<uint32_t>(ctiles * groups));
   if (a.bs == 16) {
     auto kern = k_bnb4_gemv<T, MR, 2>;
-    if (lds > 64 * 1024)
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                160 * 1024);
+    static std::atomic<int> done[kMaxDevices];  // per instantiation and device
+    if (lds > 64 * 1024) (void)raise_lds_cap(reinterpret_cast<const void*>(kern), 160 * 1024, done);
     hipLaunchKernelGGL(kern, grid, dim3(QT), lds, st, a, static_cast<int>(ctiles));
   } else {
     auto kern = k_bnb4_gemv<T, MR, 1>;
-    if (lds > 64 * 1024)
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                160 * 1024);
+    static std::atomic<int> done[kMaxDevices];  // per instantiation and device
+    if (lds > 64 * 1024) (void)raise_lds_cap(reinterpret_cast<const void*>(kern), 160 * 1024, done);
     hipLaunchKernelGGL(kern, grid, dim3(QT), lds, st, a, static_cast<int>(ctiles));
   }
   return hipGetLastError();

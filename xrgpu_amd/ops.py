@@ -116,8 +116,17 @@ def _one_zp_dtype(zps, what):
 
 
 def matmul_nbits(A, B, scales, zero_points=None, bias=None, *, K=None, N=None, bits=4,
-                 block_size=32, out=None, stream=None):
-    """com.microsoft.MatMulNBits on the GPU. Returns Y ``A.shape[:-1] + [N]``."""
+                 block_size=32, out=None, workspace=None, stream=None):
+    """com.microsoft.MatMulNBits on the GPU. Returns Y ``A.shape[:-1] + [N]``.
+
+    Geometries with few output tiles split K across workgroups on a workspace
+    (``matmul_nbits_workspace_bytes``). Eager calls use one zero-filled
+    workspace per (device, stream) kept by this module. A caller may pass its
+    own ``workspace`` (uint8, 256-byte aligned, its first 4096 bytes zero
+    before first use; every call leaves them zero); calls that may overlap
+    need different workspaces. Under HIP graph capture without a caller
+    workspace the call runs unsplit, so a captured graph never depends on a
+    workspace this module might replace or share with another graph."""
     K = int(K if K is not None else A.shape[-1])
     N = int(N if N is not None else B.shape[0])
     if A.shape[-1] != K:
@@ -133,8 +142,15 @@ def matmul_nbits(A, B, scales, zero_points=None, bias=None, *, K=None, N=None, b
     lib = nat.lib()
     s = _stream(stream, dev)
     need = lib.xrmm_matmul_nbits_workspace_bytes(M, K, N, bits, block_size, _t1(A)) if M > 16 else 0
-    if need > 0:
+    if need > 0 and workspace is not None:
+        if workspace.dtype != torch.uint8 or workspace.numel() < need or workspace.get_device() != dev:
+            raise nat.XrmmInvalid(f"workspace must be uint8 with at least {need} bytes on A's device")
+        ws = workspace
+    elif need > 0 and not torch.cuda.is_current_stream_capturing():
         ws = _workspace(A.device, s, need, stream)
+    else:
+        need = 0
+    if need > 0:
         nat.check(lib.xrmm_matmul_nbits_ws(_ptr(A), _ptr(B), _ptr(scales), _ptr(zero_points), _zp_dtype(zero_points),
                                            _ptr(bias), _ptr(out), M, K, N, bits, block_size, _t1(A), _ptr(ws),
                                            ws.numel(), s))
@@ -163,6 +179,12 @@ def _workspace(device, stream_handle, nbytes, stream=None):
                 ws = torch.zeros(size, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
+
+
+def matmul_nbits_workspace_bytes(M, K, N, bits=4, block_size=32, dtype=torch.float16):
+    """Bytes of the split-K workspace a MatMulNBits geometry uses (0: none)."""
+    return int(nat.lib().xrmm_matmul_nbits_workspace_bytes(int(M), int(K), int(N), int(bits), int(block_size),
+                                                            nat.F16 if dtype == torch.float16 else nat.F32))
 
 
 def prepacked_bytes(N, K, bits=4, block_size=32):
