@@ -30,13 +30,20 @@ FP16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, published
 PROFILES = os.path.join(ROOT, "profiles")
 SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048": 4, "qmoe_mixtral_t1": 6,
          "bnb4_nf4_m1": 7, "gbq_embed_t2048": 8, "int8a_decode_m1": 1, "f32_k2048_m1": 0,
-         "mlp_prefill_m64": 9, "prefill_m2048_prepacked": 4, "down_proj_m64": 10}
+         "mlp_prefill_m64": 9, "prefill_m2048_prepacked": 4, "down_proj_m64": 10, "mlp_prefill_m2048": 13,
+         "qkv_prefill_m2048": 14}
 # The CPU-oracle workload on the GPU: MatMulNBits float32, M=1, K=N=2048,
 # block_size 32, packed zero points (2,703,360 algorithmic bytes per call)
 F32 = dict(M=1, K=2048, N=2048, bs=32)
 # MatMulNBitsMlp prefill: 64 rows, K=2048, N=5632 (the TinyLlama-1.1B FFN),
 # block_size 32, normScale, SiLU; 2*2*M*K*N flops per call
 MLP64 = dict(M=64, K=2048, N=5632, bs=32)
+# MatMulNBitsMlp prefill of the Llama-3-8B FFN: 2048 rows, K=4096, N=14336,
+# block_size 32, normScale, SiLU (gate and up: 2*2*M*K*N flops per call)
+MLP2K = dict(M=2048, K=4096, N=14336, bs=32)
+# MatMulNBitsQkv prefill, the GQA layout: 2048 rows, K=4096, Nq=4096,
+# Nkv=1024, block_size 64, packed zero points, normScale
+QKV2K = dict(M=2048, K=4096, Nq=4096, Nkv=1024, bs=64)
 # MatMulNBits down projection of the Llama-3-8B FFN for 64 tokens (K=14336,
 # N=4096, block_size 32, packed zero points): 32 output tiles for 256 CUs, the
 # split-K GEMM's case
@@ -159,6 +166,29 @@ def make_replicas(torch, name, R, dev, seed):
             reps.append(dict(gB=_gen_weights(torch, g, N, K // bs, bs // 2, dev), gS=_scales(torch, g, (N, K // bs), dev),
                              uB=_gen_weights(torch, g, N, K // bs, bs // 2, dev), uS=_scales(torch, g, (N, K // bs), dev)))
         return dict(A=A, reps=reps, K=K, N=N, bs=bs, gamma=gamma)
+    if name == "mlp_prefill_m2048":
+        q = MLP2K
+        K, N, bs = q["K"], q["N"], q["bs"]
+        A = torch.randn((q["M"], K), device=dev, generator=g).half()
+        gamma = (torch.rand((K,), device=dev, generator=g) + 0.5).half()
+        for _ in range(R):
+            reps.append(dict(gB=_gen_weights(torch, g, N, K // bs, bs // 2, dev), gS=_scales(torch, g, (N, K // bs), dev),
+                             uB=_gen_weights(torch, g, N, K // bs, bs // 2, dev), uS=_scales(torch, g, (N, K // bs), dev)))
+        return dict(A=A, reps=reps, K=K, N=N, bs=bs, gamma=gamma)
+    if name == "qkv_prefill_m2048":
+        q = QKV2K
+        K, bs = q["K"], q["bs"]
+        kb = K // bs
+        A = torch.randn((q["M"], K), device=dev, generator=g).half()
+        gamma = (torch.rand((K,), device=dev, generator=g) + 0.5).half()
+        for _ in range(R):
+            r = {}
+            for p, n in (("q", q["Nq"]), ("k", q["Nkv"]), ("v", q["Nkv"])):
+                r[p + "B"] = _gen_weights(torch, g, n, kb, bs // 2, dev)
+                r[p + "S"] = _scales(torch, g, (n, kb), dev)
+                r[p + "Z"] = torch.randint(0, 256, (n, (kb + 1) // 2), dtype=torch.uint8, device=dev, generator=g)
+            reps.append(r)
+        return dict(A=A, gamma=gamma, reps=reps)
     if name == "mlp_swiglu_m16":
         K, N, bs = 4096, 14336, 32
         A = torch.randn((16, K), device=dev, generator=g).half()
@@ -222,6 +252,28 @@ def step_fn(ops, name, w):
             r = reps[i % len(reps)]
             return ops.matmul_nbits_mlp(A, r["gB"], r["gS"], r["uB"], r["uS"], norm_scale=w["gamma"],
                                         block_size=w["bs"])
+        return f
+    if name == "mlp_prefill_m2048":
+        # one workspace for the normalised rows, allocated once (the front end
+        # would otherwise take it from torch's caching allocator per call)
+        ws = torch.empty(ops.fused_workspace_bytes("mlp", MLP2K["M"], w["K"], w["N"], block_size=w["bs"]),
+                         dtype=torch.uint8, device=A.device)
+
+        def f(i):
+            r = reps[i % len(reps)]
+            return ops.matmul_nbits_mlp(A, r["gB"], r["gS"], r["uB"], r["uS"], norm_scale=w["gamma"],
+                                        block_size=w["bs"], workspace=ws)
+        return f
+    if name == "qkv_prefill_m2048":
+        q = QKV2K
+        ws = torch.empty(ops.fused_workspace_bytes("qkv", q["M"], q["K"], q["Nq"], q["Nkv"], block_size=q["bs"]),
+                         dtype=torch.uint8, device=A.device)
+
+        def f(i):
+            r = reps[i % len(reps)]
+            return ops.matmul_nbits_qkv(A, r["qB"], r["qS"], r["kB"], r["kS"], r["vB"], r["vS"], norm_scale=w["gamma"],
+                                        block_size=q["bs"], q_zero_points=r["qZ"], k_zero_points=r["kZ"],
+                                        v_zero_points=r["vZ"], want_residual=False, workspace=ws)
         return f
     if name == "mlp_swiglu_m16":
         def f(i):
@@ -548,18 +600,21 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     results = {}
-    names = ["decode_up_m1", "prefill_m2048", "prefill_m2048_prepacked", "qkv_gqa_m4", "mlp_swiglu_m16", "mlp_prefill_m64", "down_proj_m64", "f32_k2048_m1",
+    names = ["decode_up_m1", "prefill_m2048", "prefill_m2048_prepacked", "qkv_gqa_m4", "mlp_swiglu_m16",
+             "mlp_prefill_m64", "down_proj_m64", "mlp_prefill_m2048", "qkv_prefill_m2048", "f32_k2048_m1",
              "qmoe_mixtral_t1", "bnb4_nf4_m1", "gbq_embed_t2048", "int8a_decode_m1"]
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
     for name in names:
         # every leg rotates more weight bytes than the 256 MB Infinity Cache
         # holds (Qkv: 24 x 13.7 MB = 328 MB)
-        R = {"prefill_m2048": 2, "prefill_m2048_prepacked": 2, "qmoe_mixtral_t1": 2, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24,
+        # (prefill legs: 8 replicas, 8 x 30-66 MB of weights and scales)
+        R = {"prefill_m2048": 8, "prefill_m2048_prepacked": 8, "mlp_prefill_m2048": 8, "qkv_prefill_m2048": 24,
+             "qmoe_mixtral_t1": 2, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24,
              "f32_k2048_m1": 100, "mlp_prefill_m64": 24, "down_proj_m64": 12}.get(name, args.replicas)
         w = make_replicas(torch, name, R, dev, seed=SEEDS[name])
         fn = step_fn(ops, name, w)
-        steps = args.steps if not name.startswith("prefill_m2048") else max(10, args.steps // 10)
+        steps = args.steps if "prefill_m2048" not in name else max(10, args.steps // 10)
         ms, eager_ms, wall_ms = time_steps(torch, fn, steps, args.warmup)
         p10, p50, p90 = per_launch_percentiles(torch, fn, min(100, steps), 5)
         wl = workloads.make(name, scale_down=1) if name == "decode_up_m1" else None
@@ -605,7 +660,7 @@ def main():
             "stream_ceiling": ceiling,
             "decode_over_stream_ceiling": round(ceiling["us"] / (r["ms"] * 1e3), 4),
         }
-    mceil = mfma_ceiling(torch, ops) if any(n.startswith("prefill_m2048") for n in results) else None
+    mceil = mfma_ceiling(torch, ops) if any("prefill_m2048" in n for n in results) else None
     if "prefill_m2048" in results:
         r = results["prefill_m2048"]
         fl = 2 * 2048 * 4096 * 14336
@@ -655,6 +710,27 @@ def main():
             "bytes_per_launch": nbytes, "replicas": r["replicas"],
             "kernel": ops.select_kernel("MatMulNBitsMlp", q["M"], q["K"], q["N"], 4, q["bs"]),
             "traffic": traffic_of("mlp_prefill_m64_splitk.md", ops.select_kernel("MatMulNBitsMlp", q["M"], q["K"], q["N"], 4, q["bs"]))}
+    for name, q, kern_args in (("mlp_prefill_m2048", MLP2K, ("MatMulNBitsMlp", MLP2K["M"], MLP2K["K"], MLP2K["N"], 4,
+                                                             MLP2K["bs"])),
+                               ("qkv_prefill_m2048", QKV2K, ("MatMulNBitsQkv", QKV2K["M"], QKV2K["K"], QKV2K["Nq"], 4,
+                                                             QKV2K["bs"]))):
+        if name not in results:
+            continue
+        r = results[name]
+        if name.startswith("mlp"):
+            fl = 2 * 2 * q["M"] * q["K"] * q["N"]
+            what = "MatMulNBitsMlp fp16 M=2048 K=4096 N=14336 bs=32 normScale SiLU (Llama-3-8B FFN gate/up prefill)"
+            kern = ops.select_kernel(*kern_args)
+        else:
+            fl = 2 * q["M"] * q["K"] * (q["Nq"] + 2 * q["Nkv"])
+            what = "MatMulNBitsQkv fp16 M=2048 K=4096 Nq=4096 Nkv=1024 bs=64 packed zp normScale (GQA prefill)"
+            kern = ops.select_kernel(*kern_args, zp="packed")
+        tf = fl / (r["ms"] * 1e-3) / 1e12
+        out[name] = {"workload": what, "us": round(r["ms"] * 1e3, 2), "tflops": round(tf, 2),
+                     "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 4), "flops_per_launch": fl, "replicas": r["replicas"],
+                     "kernel": "rms prologue + " + kern}
+        if mceil:
+            out[name]["frac_of_mfma_ceiling"] = round(tf / mceil["tflops"], 4)
     if "down_proj_m64" in results:
         r, q = results["down_proj_m64"], DOWN64
         fl = 2 * q["M"] * q["K"] * q["N"]

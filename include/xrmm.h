@@ -155,6 +155,38 @@ int xrmm_matmul_nbits_mlp(const void* A, const void* skip, const void* norm_scal
                           int32_t block_size, float epsilon, int32_t activation, int32_t dtype,
                           void* stream);
 
+/* xrmm_matmul_nbits_qkv / xrmm_matmul_nbits_mlp with a caller's workspace for
+ * the prefill GEMMs (more than 16 rows): a prologue kernel computes
+ * x = RMSNorm(A + skip) * norm_scale (or A + skip) once per row into the
+ * workspace as binary16, rounded after the normalisation (packedInput,
+ * complex_kernel.glsl:81), and writes the residual; the GEMM then reads x
+ * (from 128 rows with enough tiles: the 256 x 256 prefill pipeline, the three
+ * Qkv projections on one grid, Mlp gate and up columns interleaved with
+ * act(g) * u in the epilogue). xrmm_matmul_nbits_fused_workspace_bytes gives
+ * the bytes (op: 1 Qkv, 2 Mlp; N = Nq for Qkv; 0 = none needed, the call runs
+ * like the workspace-free entry point). The workspace is 256-byte aligned;
+ * nothing in it needs clearing; calls that may overlap need different
+ * workspaces. No counterpart in the reference (one serial loop); same results
+ * as the entry points above within the float16 bar. */
+int64_t xrmm_matmul_nbits_fused_workspace_bytes(int32_t op, int64_t M, int64_t K, int64_t N, int64_t Nkv,
+                                                int32_t bits, int32_t block_size, int32_t dtype, int32_t has_skip,
+                                                int32_t has_norm_scale);
+int xrmm_matmul_nbits_qkv_ws(const void* A, const void* skip, const void* norm_scale,
+                             const void* q_B, const void* q_scales, const void* q_zero_points,
+                             const void* k_B, const void* k_scales, const void* k_zero_points,
+                             const void* v_B, const void* v_scales, const void* v_zero_points,
+                             int32_t zp_dtype, void* Q, void* Kout, void* V, void* residual,
+                             int64_t M, int64_t K, int64_t Nq, int64_t Nkv, int32_t bits,
+                             int32_t block_size, float epsilon, int32_t dtype, void* workspace,
+                             int64_t workspace_bytes, void* stream);
+int xrmm_matmul_nbits_mlp_ws(const void* A, const void* skip, const void* norm_scale,
+                             const void* gate_B, const void* gate_scales, const void* gate_zero_points,
+                             const void* gate_bias, const void* up_B, const void* up_scales,
+                             const void* up_zero_points, const void* up_bias, int32_t zp_dtype, void* Y,
+                             void* residual, int64_t M, int64_t K, int64_t N, int32_t bits,
+                             int32_t block_size, float epsilon, int32_t activation, int32_t dtype,
+                             void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Dequantized weights W [N,K] (nbitWeight, complex_kernel.glsl:80) in
  * `out_dtype`: XRMM_F32 gives the reference value (float(code) - z) * scale;
  * XRMM_F16 gives that value rounded once to binary16, produced by the same

@@ -98,7 +98,10 @@ def test_qkv_requires_norm_scale():
     (2, 16, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_splitk"),
     (2, 16, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),
     (2, 17, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemm_q4_fused"),   # Mlp prefill
-    (2, 2048, 4096, 14336, 64, nat.F16, nat.U8, "gemm_q4_fused"),
+    (2, 2048, 4096, 14336, 64, nat.F16, nat.U8, "gemm_q4_big_fused"),  # 896 tiles of 256 staged columns
+    (2, 256, 4096, 14336, 64, nat.F16, nat.U8, "gemm_q4_fused"),      # 112 tiles: the 128 x 128 GEMM
+    (1, 2048, 4096, 4096, 64, nat.F16, nat.U8, "gemm_q4_big_fused"),  # Qkv prefill, one grid for Q, K, V
+    (1, 128, 4096, 4096, 64, nat.F16, nat.U8, "gemm_q4_fused"),
     (1, 64, 2048, 512, 32, nat.F16, nat.U8, "gemv_q4_splitk"),          # Qkv, four row chunks
     (1, 65, 2048, 512, 32, nat.F16, nat.U8, "gemm_q4_fused"),           # Qkv prefill
     (1, 17, 4096, 4096, 16, nat.F16, nat.F16, "gemm_q4_fused"),

@@ -56,6 +56,11 @@ def _sig(lib):
       _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _f32, _i32, _vp)
     s("xrmm_matmul_nbits_mlp", ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
       _vp, _vp, _i64, _i64, _i64, _i32, _i32, _f32, _i32, _i32, _vp)
+    s("xrmm_matmul_nbits_qkv_ws", ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
+      _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _f32, _i32, _vp, _i64, _vp)
+    s("xrmm_matmul_nbits_mlp_ws", ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
+      _vp, _vp, _i64, _i64, _i64, _i32, _i32, _f32, _i32, _i32, _vp, _i64, _vp)
+    s("xrmm_matmul_nbits_fused_workspace_bytes", _i64, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32)
     s("xrmm_dequantize", ctypes.c_int, _vp, _vp, _vp, _i32, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp)
     s("xrmm_select_kernel", ctypes.c_char_p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32)
     s("xrmm_qmoe_workspace_bytes", _i64, _i64, _i32, _i64, _i64)

@@ -193,14 +193,15 @@ int xrmm_matmul_nbits_prepacked(const void* A, const void* packed, const void* s
   return ok();
 }
 
-int xrmm_matmul_nbits_qkv(const void* A, const void* skip, const void* norm_scale, const void* q_B,
-                          const void* q_scales, const void* q_zero_points, const void* k_B,
-                          const void* k_scales, const void* k_zero_points, const void* v_B,
-                          const void* v_scales, const void* v_zero_points, int32_t zp_dtype, void* Q,
-                          void* Kout, void* V, void* residual, int64_t M, int64_t K, int64_t Nq,
-                          int64_t Nkv, int32_t bits, int32_t block_size, float epsilon, int32_t dtype,
-                          void* stream) {
-  xrmm::Launch L;
+}  // extern "C"
+
+namespace {
+
+int qkv_launch(xrmm::Launch& L, const void* A, const void* skip, const void* norm_scale, const void* q_B,
+               const void* q_scales, const void* q_zero_points, const void* k_B, const void* k_scales,
+               const void* k_zero_points, const void* v_B, const void* v_scales, const void* v_zero_points,
+               int32_t zp_dtype, void* Q, void* Kout, void* V, void* residual, int64_t M, int64_t K, int64_t Nq,
+               int64_t Nkv, int32_t bits, int32_t block_size, float epsilon, int32_t dtype) {
   if (int rc = geometry(L, xrmm::OP_QKV, M, K, bits, block_size, dtype, zp_dtype)) return rc;
   if (Nq <= 0 || Nkv <= 0) return fail(XRMM_EINVAL, "Nq and Nkv must be positive");
   if (!norm_scale) return fail(XRMM_EINVAL, "Missing complex input: normScaleT");
@@ -217,16 +218,14 @@ int xrmm_matmul_nbits_qkv(const void* A, const void* skip, const void* norm_scal
   L.p[0] = xrmm::Proj{static_cast<const uint8_t*>(q_B), q_scales, q_zero_points, nullptr, Q, Nq};
   L.p[1] = xrmm::Proj{static_cast<const uint8_t*>(k_B), k_scales, k_zero_points, nullptr, Kout, Nkv};
   L.p[2] = xrmm::Proj{static_cast<const uint8_t*>(v_B), v_scales, v_zero_points, nullptr, V, Nkv};
-  return run(L, stream);
+  return XRMM_OK;
 }
 
-int xrmm_matmul_nbits_mlp(const void* A, const void* skip, const void* norm_scale, const void* gate_B,
-                          const void* gate_scales, const void* gate_zero_points, const void* gate_bias,
-                          const void* up_B, const void* up_scales, const void* up_zero_points,
-                          const void* up_bias, int32_t zp_dtype, void* Y, void* residual, int64_t M,
-                          int64_t K, int64_t N, int32_t bits, int32_t block_size, float epsilon,
-                          int32_t activation, int32_t dtype, void* stream) {
-  xrmm::Launch L;
+int mlp_launch(xrmm::Launch& L, const void* A, const void* skip, const void* norm_scale, const void* gate_B,
+               const void* gate_scales, const void* gate_zero_points, const void* gate_bias, const void* up_B,
+               const void* up_scales, const void* up_zero_points, const void* up_bias, int32_t zp_dtype, void* Y,
+               void* residual, int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size, float epsilon,
+               int32_t activation, int32_t dtype) {
   if (int rc = geometry(L, xrmm::OP_MLP, M, K, bits, block_size, dtype, zp_dtype)) return rc;
   if (N <= 0) return fail(XRMM_EINVAL, "Packed matmul N required");
   if (activation < XRMM_ACT_NONE || activation > XRMM_ACT_SWIGLU) return fail(XRMM_EINVAL, "Unknown fused activation");
@@ -243,7 +242,107 @@ int xrmm_matmul_nbits_mlp(const void* A, const void* skip, const void* norm_scal
   L.act = activation;
   L.p[0] = xrmm::Proj{static_cast<const uint8_t*>(gate_B), gate_scales, gate_zero_points, gate_bias, Y, N};
   L.p[1] = xrmm::Proj{static_cast<const uint8_t*>(up_B), up_scales, up_zero_points, up_bias, nullptr, N};
+  return XRMM_OK;
+}
+
+// Bytes of the normalised-activation workspace a Qkv / Mlp launch would use
+// (0: its kernel reads none). The selection looks at the workspace pointer,
+// so it is asked with a placeholder one.
+int64_t xs_need(xrmm::Launch L) {
+  if (L.M <= 0 || !xrmm::fused_prologue(L)) return 0;
+  static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
+  L.xs = const_cast<uint8_t*>(dummy);
+  const xrmm::Kernel k = xrmm::select_kernel(L);
+  return k == xrmm::K_GEMM_FUSED || k == xrmm::K_GEMM_BIG_FUSED ? xrmm::fused_xs_bytes(L) : 0;
+}
+
+// Attach a caller's workspace when the launch uses one.
+int attach_xs(xrmm::Launch& L, void* workspace, int64_t workspace_bytes) {
+  const int64_t need = xs_need(L);
+  if (need == 0 || workspace == nullptr) return XRMM_OK;
+  if (workspace_bytes < need)
+    return fail(XRMM_EINVAL, "workspace smaller than xrmm_matmul_nbits_fused_workspace_bytes: " + std::to_string(need));
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u) return fail(XRMM_EINVAL, "workspace must be 256-byte aligned");
+  L.xs = workspace;
+  return XRMM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int xrmm_matmul_nbits_qkv(const void* A, const void* skip, const void* norm_scale, const void* q_B,
+                          const void* q_scales, const void* q_zero_points, const void* k_B,
+                          const void* k_scales, const void* k_zero_points, const void* v_B,
+                          const void* v_scales, const void* v_zero_points, int32_t zp_dtype, void* Q,
+                          void* Kout, void* V, void* residual, int64_t M, int64_t K, int64_t Nq,
+                          int64_t Nkv, int32_t bits, int32_t block_size, float epsilon, int32_t dtype,
+                          void* stream) {
+  return xrmm_matmul_nbits_qkv_ws(A, skip, norm_scale, q_B, q_scales, q_zero_points, k_B, k_scales, k_zero_points,
+                                  v_B, v_scales, v_zero_points, zp_dtype, Q, Kout, V, residual, M, K, Nq, Nkv, bits,
+                                  block_size, epsilon, dtype, nullptr, 0, stream);
+}
+
+int xrmm_matmul_nbits_qkv_ws(const void* A, const void* skip, const void* norm_scale, const void* q_B,
+                             const void* q_scales, const void* q_zero_points, const void* k_B,
+                             const void* k_scales, const void* k_zero_points, const void* v_B,
+                             const void* v_scales, const void* v_zero_points, int32_t zp_dtype, void* Q,
+                             void* Kout, void* V, void* residual, int64_t M, int64_t K, int64_t Nq,
+                             int64_t Nkv, int32_t bits, int32_t block_size, float epsilon, int32_t dtype,
+                             void* workspace, int64_t workspace_bytes, void* stream) {
+  xrmm::Launch L;
+  if (int rc = qkv_launch(L, A, skip, norm_scale, q_B, q_scales, q_zero_points, k_B, k_scales, k_zero_points, v_B,
+                          v_scales, v_zero_points, zp_dtype, Q, Kout, V, residual, M, K, Nq, Nkv, bits, block_size,
+                          epsilon, dtype))
+    return rc;
+  if (int rc = attach_xs(L, workspace, workspace_bytes)) return rc;
   return run(L, stream);
+}
+
+int xrmm_matmul_nbits_mlp(const void* A, const void* skip, const void* norm_scale, const void* gate_B,
+                          const void* gate_scales, const void* gate_zero_points, const void* gate_bias,
+                          const void* up_B, const void* up_scales, const void* up_zero_points,
+                          const void* up_bias, int32_t zp_dtype, void* Y, void* residual, int64_t M,
+                          int64_t K, int64_t N, int32_t bits, int32_t block_size, float epsilon,
+                          int32_t activation, int32_t dtype, void* stream) {
+  return xrmm_matmul_nbits_mlp_ws(A, skip, norm_scale, gate_B, gate_scales, gate_zero_points, gate_bias, up_B,
+                                  up_scales, up_zero_points, up_bias, zp_dtype, Y, residual, M, K, N, bits, block_size,
+                                  epsilon, activation, dtype, nullptr, 0, stream);
+}
+
+int xrmm_matmul_nbits_mlp_ws(const void* A, const void* skip, const void* norm_scale, const void* gate_B,
+                             const void* gate_scales, const void* gate_zero_points, const void* gate_bias,
+                             const void* up_B, const void* up_scales, const void* up_zero_points,
+                             const void* up_bias, int32_t zp_dtype, void* Y, void* residual, int64_t M,
+                             int64_t K, int64_t N, int32_t bits, int32_t block_size, float epsilon,
+                             int32_t activation, int32_t dtype, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  xrmm::Launch L;
+  if (int rc = mlp_launch(L, A, skip, norm_scale, gate_B, gate_scales, gate_zero_points, gate_bias, up_B, up_scales,
+                          up_zero_points, up_bias, zp_dtype, Y, residual, M, K, N, bits, block_size, epsilon,
+                          activation, dtype))
+    return rc;
+  if (int rc = attach_xs(L, workspace, workspace_bytes)) return rc;
+  return run(L, stream);
+}
+
+int64_t xrmm_matmul_nbits_fused_workspace_bytes(int32_t op, int64_t M, int64_t K, int64_t N, int64_t Nkv,
+                                                int32_t bits, int32_t block_size, int32_t dtype, int32_t has_skip,
+                                                int32_t has_norm_scale) {
+  xrmm::Launch L;
+  if ((op != xrmm::OP_QKV && op != xrmm::OP_MLP) || N <= 0 || (op == xrmm::OP_QKV && Nkv <= 0) ||
+      geometry(L, op, M, K, bits, block_size, dtype, XRMM_UNSPECIFIED) != XRMM_OK) {
+    g_error.clear();
+    return 0;
+  }
+  static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
+  L.nproj = op == xrmm::OP_QKV ? 3 : 2;
+  L.A = dummy;
+  L.skip = has_skip ? dummy : nullptr;
+  L.gamma = (has_norm_scale || op == xrmm::OP_QKV) ? dummy : nullptr;
+  for (int i = 0; i < L.nproj; ++i)
+    L.p[i] = xrmm::Proj{dummy, dummy, nullptr, nullptr, nullptr, (op == xrmm::OP_QKV && i > 0) ? Nkv : N};
+  return xs_need(L);
 }
 
 int xrmm_dequantize(const void* B, const void* scales, const void* zero_points, int32_t zp_dtype, void* W,
@@ -277,6 +376,9 @@ const char* xrmm_select_kernel(int32_t op, int64_t M, int64_t K, int64_t N, int3
   L.A = dummy;
   if (op == xrmm::OP_QKV) L.gamma = dummy;  // normScaleT is required for Qkv
   for (int i = 0; i < L.nproj; ++i) L.p[i] = xrmm::Proj{dummy, dummy, zp_dtype == XRMM_UNSPECIFIED ? nullptr : dummy, nullptr, nullptr, N};
+  // the front ends (ops.py, the request lifecycle) supply the Qkv / Mlp
+  // prefill workspace, so the selection assumes one
+  L.xs = const_cast<uint8_t*>(dummy);
   ok();
   return xrmm::kernel_name(xrmm::select_kernel(L));
 }

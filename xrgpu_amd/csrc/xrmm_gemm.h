@@ -74,16 +74,28 @@ struct GbRegs {
   uint32_t z[SPC];   // raw zero-point bits (packed: the byte)
 };
 
-// One output tile: rows m0 .. m0 + 255, columns n0 .. n0 + 64 TN - 1.
-template <int ZPK, int SPC, int TN, bool PK>
-__device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const int n0) {
+// One output tile: rows m0 .. m0 + 255, staged columns 0 .. 64 TN - 1.
+// MatMulNBits and Qkv: staged column c is output column n0 + c of projection
+// pi. Mlp (TN = 4): staged columns 32 g .. 32 g + 31 are the gate (g even) or
+// up (g odd) projection of outputs n0 + 32 (g / 2) .. + 31, so the tile covers
+// 128 outputs and a wave's MFMA column tiles j = 0, 1 (and 2, 3) hold the gate
+// and up projection of the same 32 outputs; act(g + gate bias) * (u + up
+// bias) forms in registers. A staging wave's 32 columns belong to one
+// projection, so each wave's buffer resources stay uniform.
+template <int ZPK, int SPC, int TN, bool PK, int OPK = OP_MATMUL>
+__device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const int n0, const int pi = 0) {
+  static_assert(OPK != OP_MLP || TN == 4, "Mlp tiles pair gate and up MFMA column tiles");
+  constexpr bool MLP = OPK == OP_MLP;
   extern __shared__ __align__(16) unsigned char smem[];
   f16* lds = reinterpret_cast<f16*>(smem);
   constexpr uint32_t OOB = 0x80000000u;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const Proj& P = L.p[0];
+  // the projection this wave stages B from (Mlp: staged column group
+  // (tid / 2) / 32 = wave, gate for even waves, up for odd)
+  const int bpi = MLP ? (wave & 1) : pi;
+  const Proj& P = L.p[bpi];
   const int M = static_cast<int>(L.M), N = static_cast<int>(P.N), K = static_cast<int>(L.K);
   const int Kp = static_cast<int>(L.kb * L.block_size);
   const uint32_t rowb = static_cast<uint32_t>(Kp / 2);
@@ -97,7 +109,7 @@ __device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const i
   // return zero with no per-step select (a divergent select would become a
   // branch around the load).
   const int bc = tid >> 1, bh = tid & 1;
-  const int bn = n0 + bc;
+  const int bn = MLP ? n0 + 32 * (bc >> 6) + (bc & 31) : n0 + bc;
   const bool bnval = bc < 64 * TN && bn < N;  // narrow tiles: threads past the tile load nothing
   const uint32_t zrow = ZPK == ZP_PACKED ? static_cast<uint32_t>(L.zrow) : kb * (L.zp_dtype == DT_F32 ? 4u : 2u);
   // PK: B in the prepacked layout [K step][column][32 bytes] (prepack_q4)
@@ -246,25 +258,45 @@ __device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const i
   // LDS row-major, so Y is written in whole 16-byte pieces of its rows (a
   // wave stores 1 KB of two rows per instruction) instead of 2-byte scatters
   // that leave partial lines.
-  constexpr int YLD = 64 * TN + 8;  // halfs per staged output row (pad spreads banks)
+  constexpr int OUTW = MLP ? 32 * TN : 64 * TN;  // output columns of the tile
+  constexpr int YLD = OUTW + 8;  // halfs per staged output row (pad spreads banks)
   static_assert(GB_M * YLD * 2 <= static_cast<int>(GB_LDS), "the output tile fits the LDS");
-  const f16* biasp = static_cast<const f16*>(P.bias);
   __syncthreads();  // every wave's last fragment reads are done
+  if constexpr (MLP) {
+    const f16* gbias = static_cast<const f16*>(L.p[0].bias);
+    const f16* ubias = static_cast<const f16*>(L.p[1].bias);
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int c = wn * 32 * TN + j * 32 + (lane & 31);
-    const float bias = (biasp != nullptr && n0 + c < N) ? static_cast<float>(biasp[n0 + c]) : 0.f;
+    for (int jp = 0; jp < TN / 2; ++jp) {
+      const int c = wn * 64 + jp * 32 + (lane & 31);  // output column inside the tile
+      const bool cv = n0 + c < N;
+      const float gb = (gbias != nullptr && cv) ? static_cast<float>(gbias[n0 + c]) : 0.f;
+      const float ub = (ubias != nullptr && cv) ? static_cast<float>(ubias[n0 + c]) : 0.f;
 #pragma unroll
-    for (int i = 0; i < GB_TM; ++i)
+      for (int i = 0; i < GB_TM; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int r = wm * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        lds[r * YLD + c] = static_cast<f16>(acc[i][j][e] + bias);
-      }
+        for (int e = 0; e < 16; ++e) {
+          const int r = wm * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          lds[r * YLD + c] = static_cast<f16>(activate(acc[i][2 * jp][e] + gb, L.act) * (acc[i][2 * jp + 1][e] + ub));
+        }
+    }
+  } else {
+    const f16* biasp = static_cast<const f16*>(P.bias);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int c = wn * 32 * TN + j * 32 + (lane & 31);
+      const float bias = (biasp != nullptr && n0 + c < N) ? static_cast<float>(biasp[n0 + c]) : 0.f;
+#pragma unroll
+      for (int i = 0; i < GB_TM; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = wm * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          lds[r * YLD + c] = static_cast<f16>(acc[i][j][e] + bias);
+        }
+    }
   }
   __syncthreads();
-  f16* Y = static_cast<f16*>(P.Y);
-  constexpr int PPR = 8 * TN;  // 16-byte pieces per tile row
+  f16* Y = static_cast<f16*>(L.p[pi].Y);
+  constexpr int PPR = OUTW / 8;  // 16-byte pieces per tile row
   const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15u) == 0;
   for (int idx = tid; idx < GB_M * PPR; idx += GB_T) {
     const int r = idx / PPR, p = idx % PPR;
@@ -318,6 +350,40 @@ __global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big(Launch L, GemmTiles t) 
   }
 }
 
+// MatMulNBitsQkv / MatMulNBitsMlp on the same pipeline, all tiles 256 wide.
+// L.A holds the normalised activations (the operator's prologue has run, or
+// there is none), so the K loop is the MatMulNBits one. Qkv: the three
+// projections' column tiles (t0, t1 and nc - t0 - t1 of them) sit side by
+// side on one grid, so the GQA geometry fills the CUs with one launch. Mlp:
+// a tile covers 128 outputs of the gate and up projections (256 staged
+// columns).
+template <int ZPK, int SPC, int OPK>
+__global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big_fused(Launch L, uint32_t t0, uint32_t t1, uint32_t nc) {
+  const uint32_t mt = static_cast<uint32_t>((L.M + GB_M - 1) / GB_M);
+  uint32_t row, col;
+  tile_of(blockIdx.x, mt, nc, row, col);
+  if constexpr (OPK == OP_MLP) {
+    gemm_tile<ZPK, SPC, 4, false, OP_MLP>(L, static_cast<int>(row) * GB_M, static_cast<int>(col) * 128, 0);
+  } else {
+    const int pi = col < t0 ? 0 : col < t0 + t1 ? 1 : 2;
+    const uint32_t lc = col - (pi == 0 ? 0u : pi == 1 ? t0 : t0 + t1);
+    gemm_tile<ZPK, SPC, 4, false, OP_QKV>(L, static_cast<int>(row) * GB_M, static_cast<int>(lc) * 256, pi);
+  }
+}
+
+// Column tiles of the fused grid: Qkv per projection (256 outputs each),
+// Mlp 128 outputs per tile.
+inline void gemm_fused_tiles(const Launch& L, uint32_t& t0, uint32_t& t1, uint32_t& nc) {
+  if (L.op == OP_MLP) {
+    t0 = t1 = 0;
+    nc = static_cast<uint32_t>((L.p[0].N + 127) / 128);
+  } else {
+    t0 = static_cast<uint32_t>((L.p[0].N + 255) / 256);
+    t1 = static_cast<uint32_t>((L.p[1].N + 255) / 256);
+    nc = t0 + t1 + static_cast<uint32_t>((L.p[2].N + 255) / 256);
+  }
+}
+
 // Compute units of the current device (cached per device ordinal).
 int device_cus();
 
@@ -336,9 +402,26 @@ inline hipError_t launch_gemm_big(const Launch& L, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int ZPK, int SPC, int OPK>
+inline hipError_t launch_gemm_big_fused(const Launch& L, hipStream_t st) {
+  auto kern = k_gemm_q4_big_fused<ZPK, SPC, OPK>;
+  static std::atomic<int> done[kMaxDevices];
+  const hipError_t attr = raise_lds_cap(reinterpret_cast<const void*>(kern), static_cast<int>(GB_LDS), done);
+  if (attr != hipSuccess) return attr;
+  uint32_t t0, t1, nc;
+  gemm_fused_tiles(L, t0, t1, nc);
+  const int64_t tiles = (L.M + GB_M - 1) / GB_M * static_cast<int64_t>(nc);
+  if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;  // launch limit
+  hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(tiles)), dim3(GB_T), GB_LDS, st, L, t0, t1, nc);
+  return hipGetLastError();
+}
+
 // Defined once per zero-point kind (xrmm_gemm_zp.hip).
 template <int ZPK>
 hipError_t launch_gemm_big_for(const Launch& L, hipStream_t st);
+// Qkv / Mlp on the 256 x 256 pipeline (L.A already normalised).
+template <int ZPK>
+hipError_t launch_gemm_big_fused_for(const Launch& L, hipStream_t st);
 // The same GEMM on prepacked weights (L.p[0].B in the prepack_q4 layout).
 template <int ZPK>
 hipError_t launch_gemm_big_pk_for(const Launch& L, hipStream_t st);

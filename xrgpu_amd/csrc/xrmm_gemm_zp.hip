@@ -14,6 +14,14 @@ hipError_t launch_gemm_big_for<XRMM_ZPK>(const Launch& L, hipStream_t st) {
 }
 
 template <>
+hipError_t launch_gemm_big_fused_for<XRMM_ZPK>(const Launch& L, hipStream_t st) {
+  const bool one = L.block_size >= 32;
+  if (L.op == OP_MLP)
+    return one ? launch_gemm_big_fused<XRMM_ZPK, 1, OP_MLP>(L, st) : launch_gemm_big_fused<XRMM_ZPK, 2, OP_MLP>(L, st);
+  return one ? launch_gemm_big_fused<XRMM_ZPK, 1, OP_QKV>(L, st) : launch_gemm_big_fused<XRMM_ZPK, 2, OP_QKV>(L, st);
+}
+
+template <>
 hipError_t launch_gemm_big_pk_for<XRMM_ZPK>(const Launch& L, hipStream_t st) {
   return L.block_size >= 32 ? launch_gemm_big<XRMM_ZPK, 1, true>(L, st) : launch_gemm_big<XRMM_ZPK, 2, true>(L, st);
 }

@@ -52,6 +52,10 @@ struct Launch {
   // kernel leaves them zero-filled). nullptr / 1: no split.
   void* ws;
   int32_t splits;
+  // Qkv / Mlp prefill: binary16 [M, K] for the normalised activations
+  // x = RMSNorm(A + skip) * gamma (or A + skip), written by the prologue
+  // kernel before the GEMM reads it. nullptr: the GEMM normalises in place.
+  void* xs;
 };
 
 // While alive on the calling thread, launches described on that thread set
@@ -71,7 +75,13 @@ class ExactWeightsScope {
 
 // Kernel families the dispatcher chooses between.
 enum Kernel { K_GENERIC = 0, K_GEMV_Q4 = 1, K_GEMM_Q4 = 2, K_GEMV_DOT = 3, K_GEMM_BIG = 4, K_GEMV_SK = 5, K_GEMV_MQ = 6,
-              K_GEMV_F32 = 7, K_GEMM_FUSED = 8 };
+              K_GEMV_F32 = 7, K_GEMM_FUSED = 8, K_GEMM_BIG_FUSED = 9 };
+
+// Whether a Qkv / Mlp launch has a prologue (skip or normScale) whose
+// normalised activations a prefill GEMM can take from L.xs.
+inline bool fused_prologue(const Launch& L) { return L.op != OP_MATMUL && (L.skip != nullptr || L.gamma != nullptr); }
+// Bytes of L.xs for the geometry (binary16 [M, K], 256-byte multiple).
+inline int64_t fused_xs_bytes(const Launch& L) { return (L.M * L.K * 2 + 255) / 256 * 256; }
 
 // Choose a kernel family for the geometry (host only, no device calls).
 Kernel select_kernel(const Launch& L);

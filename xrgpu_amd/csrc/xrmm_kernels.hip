@@ -336,8 +336,15 @@ __global__ __launch_bounds__(256 * KG) void k_gemm_q4(Launch L) {
     const uint32_t pbase = kGemmCounterBytes;  // the partial tiles follow the counter block
     const uint32_t tile_bytes = 256u * 64u * 4u;
     const rsrc_t rW = mk_rsrc(static_cast<uint8_t*>(L.ws) + pbase, tiles * static_cast<uint32_t>(L.splits) * tile_bytes);
-    // thread tid's 16 float4 of a partial: piece (i j q) at ((i 2 + j) 4 + q) 256 + tid
+    // thread tid's 16 float4 of a partial: piece (i j q) at ((i 2 + j) 4 + q) 256 + tid.
+    // A piece holds rows m0 + wm 64 + i 32 + 8 q + 4 (lane / 32) + 0..3 of one
+    // column; pieces whose rows all lie past M are neither stored nor read
+    // (their offset is past the resource: the store is dropped, the load
+    // returns zero), so a tile with few rows moves only the rows it has.
+    const int64_t prow = m0 + wm * 64 + 4 * (lane >> 5);
     auto poff = [&](uint32_t sp, int piece) {
+      const int ii = piece >> 3, q = piece & 3;
+      if (prow + ii * 32 + 8 * q >= M) return 0x80000000u;
       return (tile * static_cast<uint32_t>(L.splits) + sp) * tile_bytes + (static_cast<uint32_t>(piece) * 256u + tid) * 16u;
     };
     if (kg == 0) {
@@ -398,6 +405,74 @@ __global__ __launch_bounds__(256 * KG) void k_gemm_q4(Launch L) {
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Qkv / Mlp prefill prologue: packedInput (complex_kernel.glsl:81) once per
+// row, for the GEMMs that read the normalised activations from L.xs.
+// r = A + skip in float32; with normScale, inv = 1 / sqrt(sum_k r^2 / K + eps)
+// and x = r * (gamma * inv), without it x = r; x is rounded once to binary16
+// after the normalisation, so it stays in range wherever the normalised value
+// does (|r * gamma| itself may exceed 65504). The residual output receives r
+// rounded once. One workgroup per row, 16-byte pieces (K % 8 == 0 and 16-byte
+// aligned tensors: the fast path's conditions); the row's second pass finds
+// its pieces in the L1/L2.
+__global__ __launch_bounds__(256) void k_rms_rows(Launch L) {
+  const int tid = threadIdx.x;
+  const int64_t m = blockIdx.x, K = L.K;
+  const f16* A = static_cast<const f16*>(L.A) + m * K;
+  const f16* S = L.skip ? static_cast<const f16*>(L.skip) + m * K : nullptr;
+  const f16* G = static_cast<const f16*>(L.gamma);
+  auto row = [&](int64_t k, float r[8]) {
+    const f16x8 a = __builtin_bit_cast(f16x8, ld16(A + k));
+    const f16x8 sk = S ? __builtin_bit_cast(f16x8, ld16(S + k)) : f16x8{};
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      r[e] = S ? __fadd_rn(static_cast<float>(a[e]), static_cast<float>(sk[e])) : static_cast<float>(a[e]);
+  };
+  float inv = 1.f;
+  if (G) {
+    float sq = 0.f;
+    for (int64_t k = int64_t(tid) * 8; k < K; k += 256 * 8) {
+      float r[8];
+      row(k, r);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sq = __builtin_fmaf(r[e], r[e], sq);
+    }
+    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
+    __shared__ float red[4];
+    if ((tid & 63) == 0) red[tid >> 6] = sq;
+    __syncthreads();
+    inv = __builtin_amdgcn_rsqf(((red[0] + red[1]) + (red[2] + red[3])) / static_cast<float>(K) + L.eps);
+  }
+  f16* X = static_cast<f16*>(L.xs) + m * K;
+  f16* R = L.residual ? static_cast<f16*>(L.residual) + m * K : nullptr;
+  for (int64_t k = int64_t(tid) * 8; k < K; k += 256 * 8) {
+    float r[8];
+    row(k, r);
+    const f16x8 g = G ? __builtin_bit_cast(f16x8, ld16(G + k)) : f16x8{};
+    f16x8 x, r16;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = static_cast<f16>(G ? r[e] * __builtin_fmaf(static_cast<float>(g[e]), inv, 0.f) : r[e]);
+      r16[e] = static_cast<f16>(r[e]);
+    }
+    *reinterpret_cast<f16x8*>(X + k) = x;
+    if (R) *reinterpret_cast<f16x8*>(R + k) = r16;
+  }
+}
+
+// The prologue, then the operator's GEMM description on its output: A is the
+// normalised binary16 rows, with no skip, normScale or residual left to do.
+static hipError_t run_prologue(const Launch& L, Launch& Lx, hipStream_t st) {
+  if (L.M > 0x7FFFFFFF) return hipErrorInvalidValue;  // launch limit
+  hipLaunchKernelGGL(k_rms_rows, dim3(static_cast<uint32_t>(L.M)), dim3(256), 0, st, L);
+  Lx = L;
+  Lx.A = L.xs;
+  Lx.skip = nullptr;
+  Lx.gamma = nullptr;
+  Lx.residual = nullptr;
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -492,6 +567,13 @@ static bool gemm_big_fills(const Launch& L) {
   return tiles >= gemm_big_min_tiles();
 }
 
+// The same rule for the Qkv / Mlp grid of the 256 x 256 pipeline.
+static bool gemm_big_fused_fills(const Launch& L) {
+  uint32_t t0, t1, nc;
+  gemm_fused_tiles(L, t0, t1, nc);
+  return (L.M + GB_M - 1) / GB_M * int64_t(nc) >= gemm_big_min_tiles();
+}
+
 // Rows from which the split-K MFMA GEMV takes over from the dot GEMV (up to
 // 16 rows): the dot kernel's VALU work grows with every row, the MFMA's does
 // not. Measured with K = 4096: MatMulNBits at two rows is a tie (10.0 vs
@@ -527,6 +609,11 @@ Kernel select_kernel(const Launch& L) {
     if (L.M >= 1 && L.M <= 16 && gemv_tiles(L) != 0) return K_GEMV_Q4;
     if (L.M >= kGemmBigMinM && L.op == OP_MATMUL && gemm_big_fills(L)) return K_GEMM_BIG;
     if (L.M > 16 && L.op == OP_MATMUL) return K_GEMM_Q4;
+    // Qkv / Mlp prefill on the 256 x 256 pipeline: its K loop is the
+    // MatMulNBits one, so the prologue's normalised rows (L.xs) must exist
+    // unless there is nothing to normalise
+    if (L.M >= kGemmBigMinM && (L.xs != nullptr || !fused_prologue(L)) && gemm_big_fused_fills(L))
+      return K_GEMM_BIG_FUSED;
     if (L.M > 16) return K_GEMM_FUSED;
   }
   return K_GENERIC;
@@ -542,6 +629,7 @@ const char* kernel_name(Kernel k) {
     case K_GEMM_Q4: return "gemm_q4_mfma";
     case K_GEMM_BIG: return "gemm_q4_big";
     case K_GEMM_FUSED: return "gemm_q4_fused";
+    case K_GEMM_BIG_FUSED: return "gemm_q4_big_fused";
     default: return "generic";
   }
 }
@@ -636,10 +724,23 @@ hipError_t launch(const Launch& L, hipStream_t st) {
     if (zpk == ZP_PACKED) return launch_gemm_big_for<ZP_PACKED>(L, st);
     return launch_gemm_big_for<ZP_FLOAT>(L, st);
   }
-  if (k == K_GEMM_FUSED) {
-    if (zpk == ZP_NONE) return launch_gemm_fused_for<ZP_NONE>(L, st);
-    if (zpk == ZP_FLOAT) return launch_gemm_fused_for<ZP_FLOAT>(L, st);
-    return launch_gemm_fused_for<ZP_PACKED>(L, st);
+  if (k == K_GEMM_FUSED || k == K_GEMM_BIG_FUSED) {
+    // with a workspace the prologue normalises once per row and the GEMM
+    // reads its binary16 output; without one only the 128 x 128 GEMM runs,
+    // normalising inside its K loop
+    Launch Lx = L;
+    if (L.xs != nullptr && fused_prologue(L)) {
+      const hipError_t e = run_prologue(L, Lx, st);
+      if (e != hipSuccess) return e;
+    }
+    if (k == K_GEMM_BIG_FUSED) {
+      if (zpk == ZP_NONE) return launch_gemm_big_fused_for<ZP_NONE>(Lx, st);
+      if (zpk == ZP_FLOAT) return launch_gemm_big_fused_for<ZP_FLOAT>(Lx, st);
+      return launch_gemm_big_fused_for<ZP_PACKED>(Lx, st);
+    }
+    if (zpk == ZP_NONE) return launch_gemm_fused_for<ZP_NONE>(Lx, st);
+    if (zpk == ZP_FLOAT) return launch_gemm_fused_for<ZP_FLOAT>(Lx, st);
+    return launch_gemm_fused_for<ZP_PACKED>(Lx, st);
   }
   if (k == K_GEMM_Q4) {
     if (zpk == ZP_NONE) return launch_gemm1<ZP_NONE>(L, st);

@@ -689,18 +689,19 @@ struct xrmm_op {
                                  dptr("biasT"), optr("yT"), p.M, p.K, p.N, p.bits, p.block_size, p.dtype, s);
       case xrmm::OP_MLP: {
         const bool z = dptr("gateZeroPointsT") || dptr("upZeroPointsT");
-        return xrmm_matmul_nbits_mlp(dptr("aT"), dptr("skipT"), dptr("normScaleT"), dptr("gateBT"), dptr("gateScalesT"),
-                                     dptr("gateZeroPointsT"), dptr("gateBiasT"), dptr("upBT"), dptr("upScalesT"),
-                                     dptr("upZeroPointsT"), dptr("upBiasT"), z ? zd : XRMM_UNSPECIFIED, optr("yT"),
-                                     optr("residualT"), p.M, p.K, p.N, p.bits, p.block_size, p.eps, p.act, p.dtype, s);
+        return xrmm_matmul_nbits_mlp_ws(dptr("aT"), dptr("skipT"), dptr("normScaleT"), dptr("gateBT"),
+                                        dptr("gateScalesT"), dptr("gateZeroPointsT"), dptr("gateBiasT"), dptr("upBT"),
+                                        dptr("upScalesT"), dptr("upZeroPointsT"), dptr("upBiasT"),
+                                        z ? zd : XRMM_UNSPECIFIED, optr("yT"), optr("residualT"), p.M, p.K, p.N, p.bits,
+                                        p.block_size, p.eps, p.act, p.dtype, workspace, int64_t(workspace_bytes), s);
       }
       default: {
         const bool z = dptr("qZeroPointsT") || dptr("kZeroPointsT") || dptr("vZeroPointsT");
-        return xrmm_matmul_nbits_qkv(dptr("aT"), dptr("skipT"), dptr("normScaleT"), dptr("qBT"), dptr("qScalesT"),
-                                     dptr("qZeroPointsT"), dptr("kBT"), dptr("kScalesT"), dptr("kZeroPointsT"),
-                                     dptr("vBT"), dptr("vScalesT"), dptr("vZeroPointsT"), z ? zd : XRMM_UNSPECIFIED,
-                                     optr("qT"), optr("kT"), optr("vT"), optr("residualT"), p.M, p.K, p.Nq, p.Nkv,
-                                     p.bits, p.block_size, p.eps, p.dtype, s);
+        return xrmm_matmul_nbits_qkv_ws(dptr("aT"), dptr("skipT"), dptr("normScaleT"), dptr("qBT"), dptr("qScalesT"),
+                                        dptr("qZeroPointsT"), dptr("kBT"), dptr("kScalesT"), dptr("kZeroPointsT"),
+                                        dptr("vBT"), dptr("vScalesT"), dptr("vZeroPointsT"), z ? zd : XRMM_UNSPECIFIED,
+                                        optr("qT"), optr("kT"), optr("vT"), optr("residualT"), p.M, p.K, p.Nq, p.Nkv,
+                                        p.bits, p.block_size, p.eps, p.dtype, workspace, int64_t(workspace_bytes), s);
       }
     }
   }
@@ -778,14 +779,21 @@ int xrmm_prepare(const xrmm_request* request, const xrmm_options* options, xrmm_
     if (p.contract->op == OP_GBQ) ws = 4;
     total += align256(ws);
     if (total > o.memory_limit_bytes) throw Invalid("Extended heap memory limit exceeded");
-    // The split-K workspace of MatMulNBits is a performance option, not part of
-    // the request's memory: it is reserved only when it fits the limit beside
-    // the data, and the call runs unsplit otherwise.
-    if (p.contract->op == xrmm::OP_MATMUL && !weights_need_float32(p)) {
-      const uint64_t sk = uint64_t(xrmm_matmul_nbits_workspace_bytes(p.M, p.K, p.N, p.bits, p.block_size, p.dtype));
-      if (sk && total + align256(sk) <= o.memory_limit_bytes) {
-        ws = sk;
-        total += align256(sk);
+    // The split-K workspace of MatMulNBits and the normalised-activation
+    // workspace of the Qkv / Mlp prefill GEMMs are performance options, not
+    // part of the request's memory: each is reserved only when it fits the
+    // limit beside the data, and the call runs without it otherwise.
+    if (!weights_need_float32(p)) {
+      uint64_t opt = 0;
+      if (p.contract->op == xrmm::OP_MATMUL)
+        opt = uint64_t(xrmm_matmul_nbits_workspace_bytes(p.M, p.K, p.N, p.bits, p.block_size, p.dtype));
+      else if (p.contract->op == xrmm::OP_QKV || p.contract->op == xrmm::OP_MLP)
+        opt = uint64_t(xrmm_matmul_nbits_fused_workspace_bytes(
+            p.contract->op, p.M, p.K, p.contract->op == xrmm::OP_QKV ? p.Nq : p.N, p.Nkv, p.bits, p.block_size,
+            p.dtype, p.in.count("skipT") ? 1 : 0, p.in.count("normScaleT") ? 1 : 0));
+      if (opt && total + align256(opt) <= o.memory_limit_bytes) {
+        ws = opt;
+        total += align256(opt);
       }
     }
 

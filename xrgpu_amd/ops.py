@@ -238,11 +238,40 @@ def matmul_nbits_prepacked(A, packed, scales, zero_points=None, bias=None, *, K=
     return out
 
 
+def _fused_workspace(op, A, M, K, N, Nkv, bits, block_size, skip, norm_scale, workspace):
+    """The normalised-activation workspace of a Qkv / Mlp prefill call: the
+    caller's, checked, or a fresh one from torch's caching allocator (under
+    HIP graph capture it comes from the graph's own pool); (None, 0) when the
+    geometry needs none. Nothing in it needs clearing."""
+    need = int(nat.lib().xrmm_matmul_nbits_fused_workspace_bytes(op, M, K, N, Nkv, bits, block_size, _t1(A),
+                                                                 int(skip is not None), int(norm_scale is not None)))
+    if need <= 0:
+        return None, 0
+    if workspace is not None:
+        if workspace.dtype != torch.uint8 or workspace.numel() < need or workspace.get_device() != A.get_device():
+            raise nat.XrmmInvalid(f"workspace must be uint8 with at least {need} bytes on A's device")
+        return workspace, workspace.numel()
+    return torch.empty(need, dtype=torch.uint8, device=A.device), need
+
+
+def fused_workspace_bytes(op, M, K, N, Nkv=0, bits=4, block_size=32, dtype=torch.float16, skip=False,
+                          norm_scale=True):
+    """Bytes of the Qkv ("qkv") / Mlp ("mlp") prefill workspace (0: none)."""
+    code = {"qkv": 1, "mlp": 2}[op]
+    return int(nat.lib().xrmm_matmul_nbits_fused_workspace_bytes(
+        code, int(M), int(K), int(N), int(Nkv), int(bits), int(block_size),
+        nat.F16 if dtype == torch.float16 else nat.F32, int(bool(skip)), int(bool(norm_scale))))
+
+
 def matmul_nbits_qkv(A, q_B, q_scales, k_B, k_scales, v_B, v_scales, *, norm_scale, skip=None,
                      K=None, Nq=None, Nkv=None, bits=4, block_size=32, epsilon=1e-6,
                      q_zero_points=None, k_zero_points=None, v_zero_points=None,
-                     want_residual=True, stream=None):
-    """com.microsoft.MatMulNBitsQkv. Returns ``(Q, K, V, residual-or-None)``."""
+                     want_residual=True, workspace=None, stream=None):
+    """com.microsoft.MatMulNBitsQkv. Returns ``(Q, K, V, residual-or-None)``.
+
+    Prefill geometries normalise the rows once into a workspace
+    (``fused_workspace_bytes``); pass ``workspace`` to supply it, else one is
+    taken from torch's caching allocator."""
     K = int(K if K is not None else A.shape[-1])
     Nq = int(Nq if Nq is not None else q_B.shape[0])
     Nkv = int(Nkv if Nkv is not None else k_B.shape[0])
@@ -264,18 +293,24 @@ def matmul_nbits_qkv(A, q_B, q_scales, k_B, k_scales, v_B, v_scales, *, norm_sca
     Ko = torch.empty(lead + (Nkv,), dtype=A.dtype, device=A.device)
     V = torch.empty(lead + (Nkv,), dtype=A.dtype, device=A.device)
     R = torch.empty_like(A) if want_residual else None
-    nat.check(nat.lib().xrmm_matmul_nbits_qkv(
+    ws, nws = _fused_workspace(1, A, M, K, Nq, Nkv, bits, block_size, skip, norm_scale, workspace)
+    nat.check(nat.lib().xrmm_matmul_nbits_qkv_ws(
         _ptr(A), _ptr(skip), _ptr(norm_scale), _ptr(q_B), _ptr(q_scales), _ptr(zps[0]), _ptr(k_B),
         _ptr(k_scales), _ptr(zps[1]), _ptr(v_B), _ptr(v_scales), _ptr(zps[2]), zdt, _ptr(Q), _ptr(Ko),
-        _ptr(V), _ptr(R), M, K, Nq, Nkv, bits, block_size, float(epsilon), _t1(A), _stream(stream, dev)))
+        _ptr(V), _ptr(R), M, K, Nq, Nkv, bits, block_size, float(epsilon), _t1(A), _ptr(ws), nws,
+        _stream(stream, dev)))
     return Q, Ko, V, R
 
 
 def matmul_nbits_mlp(A, gate_B, gate_scales, up_B, up_scales, *, skip=None, norm_scale=None,
                      gate_bias=None, up_bias=None, K=None, N=None, bits=4, block_size=32,
                      epsilon=1e-5, activation="silu", gate_zero_points=None, up_zero_points=None,
-                     want_residual=False, stream=None):
-    """com.microsoft.MatMulNBitsMlp. Returns ``(Y, residual-or-None)``."""
+                     want_residual=False, workspace=None, stream=None):
+    """com.microsoft.MatMulNBitsMlp. Returns ``(Y, residual-or-None)``.
+
+    Prefill geometries with skip or norm_scale normalise the rows once into a
+    workspace (``fused_workspace_bytes``); pass ``workspace`` to supply it,
+    else one is taken from torch's caching allocator."""
     K = int(K if K is not None else A.shape[-1])
     N = int(N if N is not None else gate_B.shape[0])
     if activation not in nat.ACT:
@@ -294,10 +329,12 @@ def matmul_nbits_mlp(A, gate_B, gate_scales, up_B, up_scales, *, skip=None, norm
                gate_zero_points, up_zero_points)
     Y = torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
     R = torch.empty_like(A) if want_residual else None
-    nat.check(nat.lib().xrmm_matmul_nbits_mlp(
+    ws, nws = _fused_workspace(2, A, M, K, N, 0, bits, block_size, skip, norm_scale, workspace)
+    nat.check(nat.lib().xrmm_matmul_nbits_mlp_ws(
         _ptr(A), _ptr(skip), _ptr(norm_scale), _ptr(gate_B), _ptr(gate_scales), _ptr(gate_zero_points),
         _ptr(gate_bias), _ptr(up_B), _ptr(up_scales), _ptr(up_zero_points), _ptr(up_bias), zdt, _ptr(Y),
-        _ptr(R), M, K, N, bits, block_size, float(epsilon), nat.ACT[activation], _t1(A), _stream(stream, dev)))
+        _ptr(R), M, K, N, bits, block_size, float(epsilon), nat.ACT[activation], _t1(A), _ptr(ws), nws,
+        _stream(stream, dev)))
     return Y, R
 
 
