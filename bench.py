@@ -242,10 +242,14 @@ def step_fn(ops, name, w):
         return f
     if name == "down_proj_m64":
         Y = torch.empty((DOWN64["M"], w["N"]), dtype=torch.float16, device=A.device)
+        # the split-K workspace, zero-filled once outside the timed graph (a
+        # captured call without one runs unsplit)
+        ws = torch.zeros(ops.matmul_nbits_workspace_bytes(DOWN64["M"], w["K"], w["N"], 4, w["bs"]), dtype=torch.uint8,
+                         device=A.device)
 
         def f(i):
             r = reps[i % len(reps)]
-            return ops.matmul_nbits(A, r["B"], r["S"], r["Z"], block_size=w["bs"], out=Y)
+            return ops.matmul_nbits(A, r["B"], r["S"], r["Z"], block_size=w["bs"], out=Y, workspace=ws)
         return f
     if name == "mlp_prefill_m64":
         def f(i):

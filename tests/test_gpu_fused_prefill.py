@@ -146,6 +146,7 @@ MLP_BIG = [
     (256, 256, 640, 128, None, False, False, False, "none", False),   # no prologue at all
     (200, 256, 136, 32, "packed", False, True, True, "tanh", False),
     (256, 256, 256, 32, None, True, True, False, "sigmoid", True),
+    (256, 256, 40000, 32, "packed", True, True, True, "silu", True),  # 313 tiles: wide and narrow (64-output) tiles
 ]
 
 

@@ -43,20 +43,25 @@ struct GemmTiles {
   uint32_t nb, ns, nbig;
 };
 
-// Shortest-makespan mix of k rounds of 256-wide and j rounds of 192-wide tiles
-// on `cus` CUs (one workgroup per CU); all-wide tiles when no mix is shorter.
+// Shortest-makespan mix of k rounds of wide tiles (`ww` output columns) and j
+// rounds of narrow ones (`nw` columns, costing `ncost` of a wide tile) on
+// `cus` CUs (one workgroup per CU); all-wide tiles when no mix is shorter.
 // For j narrow rounds only the fewest wide rounds that still cover N matter,
-// so the search is over j alone (a few iterations per launch).
-inline GemmTiles gemm_tiles(int64_t M, int64_t N, int cus) {
-  const int64_t mt = (M + GB_M - 1) / GB_M, full = (N + 255) / 256;
+// so the search is over j alone (a few iterations per launch). MatMulNBits:
+// 256 / 192 columns (waves of 2 x 4 / 2 x 3 MFMA tiles, cost 0.75); Mlp:
+// 128 / 64 outputs (gate and up interleaved, 2 x 4 / 2 x 2 MFMA tiles; the
+// narrow tile stages the same activations for half the MFMAs, so it costs
+// more than half).
+inline GemmTiles gemm_tiles(int64_t M, int64_t N, int cus, int64_t ww = 256, int64_t nw = 192, double ncost = 0.75) {
+  const int64_t mt = (M + GB_M - 1) / GB_M, full = (N + ww - 1) / ww;
   GemmTiles best{static_cast<uint32_t>(full), 0u, static_cast<uint32_t>(mt * full)};
   if (cus <= 0 || mt * full <= cus || cus % mt != 0) return best;
   const int64_t per = cus / mt;  // column tiles per row tile in one round
   double best_t = static_cast<double>((mt * full + cus - 1) / cus);
   for (int64_t j = 1; j <= 16; ++j) {
-    const int64_t rest = N - 192 * j * per;  // columns left for the wide tiles
-    const int64_t k = rest > 0 ? (rest + 256 * per - 1) / (256 * per) : 0;
-    const double t = static_cast<double>(k) + 0.75 * static_cast<double>(j);
+    const int64_t rest = N - nw * j * per;  // columns left for the wide tiles
+    const int64_t k = rest > 0 ? (rest + ww * per - 1) / (ww * per) : 0;
+    const double t = static_cast<double>(k) + ncost * static_cast<double>(j);
     if (t < best_t - 0.05) {
       best_t = t;
       best = GemmTiles{static_cast<uint32_t>(k * per), static_cast<uint32_t>(j * per), static_cast<uint32_t>(mt * k * per)};
@@ -64,6 +69,11 @@ inline GemmTiles gemm_tiles(int64_t M, int64_t N, int cus) {
   }
   return best;
 }
+
+// Cost of a narrow (64-output) Mlp tile against a wide (128-output) one.
+#ifndef XRMM_MLP_NARROW_COST
+#define XRMM_MLP_NARROW_COST 0.6
+#endif
 
 // Global-load registers of one K step.
 template <int SPC>
@@ -76,15 +86,15 @@ struct GbRegs {
 
 // One output tile: rows m0 .. m0 + 255, staged columns 0 .. 64 TN - 1.
 // MatMulNBits and Qkv: staged column c is output column n0 + c of projection
-// pi. Mlp (TN = 4): staged columns 32 g .. 32 g + 31 are the gate (g even) or
-// up (g odd) projection of outputs n0 + 32 (g / 2) .. + 31, so the tile covers
-// 128 outputs and a wave's MFMA column tiles j = 0, 1 (and 2, 3) hold the gate
-// and up projection of the same 32 outputs; act(g + gate bias) * (u + up
-// bias) forms in registers. A staging wave's 32 columns belong to one
-// projection, so each wave's buffer resources stay uniform.
+// pi. Mlp (TN = 4 or 2): staged columns 32 g .. 32 g + 31 are the gate (g
+// even) or up (g odd) projection of outputs n0 + 32 (g / 2) .. + 31, so the
+// tile covers 32 TN outputs and a wave's MFMA column tiles j = 0, 1 (and 2, 3)
+// hold the gate and up projection of the same 32 outputs; act(g + gate bias)
+// * (u + up bias) forms in registers. A staging wave's 32 columns belong to
+// one projection, so each wave's buffer resources stay uniform.
 template <int ZPK, int SPC, int TN, bool PK, int OPK = OP_MATMUL>
 __device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const int n0, const int pi = 0) {
-  static_assert(OPK != OP_MLP || TN == 4, "Mlp tiles pair gate and up MFMA column tiles");
+  static_assert(OPK != OP_MLP || TN % 2 == 0, "Mlp tiles pair gate and up MFMA column tiles");
   constexpr bool MLP = OPK == OP_MLP;
   extern __shared__ __align__(16) unsigned char smem[];
   f16* lds = reinterpret_cast<f16*>(smem);
@@ -267,7 +277,7 @@ __device__ __forceinline__ void gemm_tile(const Launch& L, const int m0, const i
     const f16* ubias = static_cast<const f16*>(L.p[1].bias);
 #pragma unroll
     for (int jp = 0; jp < TN / 2; ++jp) {
-      const int c = wn * 64 + jp * 32 + (lane & 31);  // output column inside the tile
+      const int c = wn * 16 * TN + jp * 32 + (lane & 31);  // output column inside the tile
       const bool cv = n0 + c < N;
       const float gb = (gbias != nullptr && cv) ? static_cast<float>(gbias[n0 + c]) : 0.f;
       const float ub = (ubias != nullptr && cv) ? static_cast<float>(ubias[n0 + c]) : 0.f;
@@ -358,13 +368,23 @@ __global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big(Launch L, GemmTiles t) 
 // a tile covers 128 outputs of the gate and up projections (256 staged
 // columns).
 template <int ZPK, int SPC, int OPK>
-__global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big_fused(Launch L, uint32_t t0, uint32_t t1, uint32_t nc) {
+__global__ __launch_bounds__(GB_T, 1) void k_gemm_q4_big_fused(Launch L, uint32_t t0, uint32_t t1, uint32_t nc,
+                                                               GemmTiles t) {
   const uint32_t mt = static_cast<uint32_t>((L.M + GB_M - 1) / GB_M);
   uint32_t row, col;
-  tile_of(blockIdx.x, mt, nc, row, col);
   if constexpr (OPK == OP_MLP) {
-    gemm_tile<ZPK, SPC, 4, false, OP_MLP>(L, static_cast<int>(row) * GB_M, static_cast<int>(col) * 128, 0);
+    // wide tiles (128 outputs) first on the grid, then narrow ones (64)
+    const uint32_t bid = blockIdx.x;
+    if (bid < t.nbig) {
+      tile_of(bid, mt, t.nb, row, col);
+      gemm_tile<ZPK, SPC, 4, false, OP_MLP>(L, static_cast<int>(row) * GB_M, static_cast<int>(col) * 128, 0);
+    } else {
+      tile_of(bid - t.nbig, mt, t.ns, row, col);
+      gemm_tile<ZPK, SPC, 2, false, OP_MLP>(L, static_cast<int>(row) * GB_M,
+                                            static_cast<int>(t.nb * 128u + col * 64u), 0);
+    }
   } else {
+    tile_of(blockIdx.x, mt, nc, row, col);
     const int pi = col < t0 ? 0 : col < t0 + t1 ? 1 : 2;
     const uint32_t lc = col - (pi == 0 ? 0u : pi == 1 ? t0 : t0 + t1);
     gemm_tile<ZPK, SPC, 4, false, OP_QKV>(L, static_cast<int>(row) * GB_M, static_cast<int>(lc) * 256, pi);
@@ -410,9 +430,14 @@ inline hipError_t launch_gemm_big_fused(const Launch& L, hipStream_t st) {
   if (attr != hipSuccess) return attr;
   uint32_t t0, t1, nc;
   gemm_fused_tiles(L, t0, t1, nc);
-  const int64_t tiles = (L.M + GB_M - 1) / GB_M * static_cast<int64_t>(nc);
+  GemmTiles t{nc, 0u, 0u};
+  int64_t tiles = (L.M + GB_M - 1) / GB_M * static_cast<int64_t>(nc);
+  if (OPK == OP_MLP) {
+    t = gemm_tiles(L.M, L.p[0].N, device_cus(), 128, 64, XRMM_MLP_NARROW_COST);
+    tiles = (L.M + GB_M - 1) / GB_M * static_cast<int64_t>(t.nb + t.ns);
+  }
   if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;  // launch limit
-  hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(tiles)), dim3(GB_T), GB_LDS, st, L, t0, t1, nc);
+  hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(tiles)), dim3(GB_T), GB_LDS, st, L, t0, t1, nc, t);
   return hipGetLastError();
 }
 
