@@ -81,7 +81,17 @@ struct MqArgs {
   float eps;
   MqProj p[3];
   uint32_t K, kb, rowb, zrow, M, bsl, nchunk;
+  // log2 of a column's scale row (kb * 2 bytes) and packed zero-point row
+  // (zrow bytes) when they are powers of two of at least 16 bytes: the tile's
+  // rows are then staged with 16 bytes of padding each, so the 16 columns'
+  // per-lane reads fall on different banks. 0: staged unpadded.
+  uint32_t sshift, zshift;
 };
+
+// Padded LDS offset of byte o of the tile's contiguous rows (row bytes 2^sh).
+__device__ __forceinline__ uint32_t mq_pad(uint32_t o, uint32_t sh) {
+  return sh ? o + ((o >> sh) << 4) : o;
+}
 
 // LDS row stride of a wave's activation slice: 4J chunks x 32 halves plus 16
 // bytes, so the 16 diagonal lanes' 16-byte reads (rows r, k-groups g: offsets
@@ -113,8 +123,8 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
   constexpr int PST = ((4 * W + 3) / 4) * 4 + 4;
   __shared__ __align__(16) float part[4][16][PST];
   __shared__ float red[QKV ? W : 1][4][4];  // per wave, row and 16-lane row of the wave
-  __shared__ __align__(16) unsigned char meta_s[MQ_META_LOADS * W * 64 * 16];
-  __shared__ __align__(16) unsigned char meta_z[ZPK == ZP_PACKED ? MQ_META_LOADS * W * 64 * 16 : 16];
+  __shared__ __align__(16) unsigned char meta_s[MQ_META_LOADS * W * 64 * 16 + 16 * 16];
+  __shared__ __align__(16) unsigned char meta_z[ZPK == ZP_PACKED ? MQ_META_LOADS * W * 64 * 16 + 16 * 16 : 16];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -202,8 +212,9 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
 #pragma unroll
   for (int q = 0; q < MQ_META_LOADS; ++q) {
     const uint32_t o = (q * W * 64u + static_cast<uint32_t>(tid)) * 16u;
-    if (o < sbytes) *reinterpret_cast<u32x4*>(meta_s + o) = sv[q];
-    if (ZPK == ZP_PACKED && o < zbytes + zdel) *reinterpret_cast<u32x4*>(meta_z + o) = zv[ZPK == ZP_PACKED ? q : 0];
+    if (o < sbytes) *reinterpret_cast<u32x4*>(meta_s + mq_pad(o, a.sshift)) = sv[q];
+    if (ZPK == ZP_PACKED && o < zbytes + zdel)
+      *reinterpret_cast<u32x4*>(meta_z + mq_pad(o, a.zshift)) = zv[ZPK == ZP_PACKED ? q : 0];
   }
   // Qkv: the RMS factor of a row is common to all its k, so it comes out of
   // the sum: y_r = inv_r * sum_k (r_k gamma_k) W_k with r = A + skip and
@@ -304,8 +315,8 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
     const uint32_t ch = ch0 + 4u * j + g;
     const uint32_t b = ((ch < nchunk ? ch : nchunk - 1u) * 32u) >> a.bsl;
     const uint32_t nn = col < N ? n : 0u;
-    sraw[j] = *reinterpret_cast<const uint16_t*>(meta_s + (nn * a.kb + b) * 2u);
-    zraw[j] = ZPK == ZP_PACKED ? meta_z[zdel + nn * a.zrow + (b >> 1)] >> ((b & 1u) * 4u) : 8u;
+    sraw[j] = *reinterpret_cast<const uint16_t*>(meta_s + mq_pad((nn * a.kb + b) * 2u, a.sshift));
+    zraw[j] = ZPK == ZP_PACKED ? meta_z[mq_pad(zdel + nn * a.zrow + (b >> 1), a.zshift)] >> ((b & 1u) * 4u) : 8u;
   }
   const f16x2 k1024 = {static_cast<f16>(1024.f), static_cast<f16>(1024.f)};
   const f16x2 k64 = {static_cast<f16>(64.f), static_cast<f16>(64.f)};
@@ -409,6 +420,17 @@ inline hipError_t launch_mq4(const Launch& L, hipStream_t st) {
   a.M = static_cast<uint32_t>(L.M);
   a.bsl = static_cast<uint32_t>(L.bs_log2);
   a.nchunk = a.rowb / 16u;
+  // padded staging when a row is a power of two of at least 16 bytes (so no
+  // 16-byte piece straddles two rows) and, for zero points, every tile's
+  // bytes start dword-aligned (zrow a multiple of 16 makes col0 * zrow one)
+  auto pow2_shift = [](int64_t bytes) -> uint32_t {
+    if (bytes < 16 || (bytes & (bytes - 1)) != 0) return 0u;
+    uint32_t sh = 0;
+    while ((int64_t(1) << sh) < bytes) ++sh;
+    return sh;
+  };
+  a.sshift = pow2_shift(L.kb * 2);
+  a.zshift = ZPK == ZP_PACKED ? pow2_shift(L.zrow) : 0u;
   hipLaunchKernelGGL((k_gemv_mq<ZPK, J, kMqWaves, OPK, SK>), dim3(tiles), dim3(kMqWaves * 64), 0, st, a);
   return hipGetLastError();
 }
