@@ -108,7 +108,9 @@ def test_qkv_requires_norm_scale():
     (1, 32, 96, 16, 32, nat.F32, nat.UNSPECIFIED, "generic"),           # float32 prefill
     (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),       # the CPU-oracle workload, float32
     (0, 4, 4096, 14336, 64, nat.F32, nat.F32, "gemv_q4_f32"),
-    (0, 5, 2048, 2048, 32, nat.F32, nat.U8, "generic"),             # float32 beyond four rows
+    (0, 5, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),         # float32 beyond four rows: chunks of four
+    (0, 64, 4096, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),
+    (1, 8, 256, 64, 32, nat.F32, nat.UNSPECIFIED, "generic"),         # float32 Qkv
     (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),
     (0, 4, 16384, 14336, 16, nat.F16, nat.UNSPECIFIED, "generic"),  # dot staging would exceed 160 KB of LDS
     (0, 1, 33, 8, 32, nat.F16, nat.UNSPECIFIED, "generic"),
@@ -154,3 +156,13 @@ def test_fuzz_reaches_every_kernel_family():
     want = {"gemv_q4_dot", "gemv_q4_mq", "gemv_q4_splitk", "gemv_q4_mfma", "gemv_q4_f32", "gemm_q4_mfma",
             "gemm_q4_fused", "generic"}
     assert want <= seen, f"not reached: {sorted(want - seen)}"
+
+
+@pytest.mark.parametrize("op,M,K,N,bits,bs,dtype,zp,expect", [
+    (0, 1, 2560, 4096, 8, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),  # the upstream q8 decode case, float32
+    (0, 512, 2560, 4096, 8, 32, nat.F32, nat.U8, "gemv_q4_f32"),         # float32 8-bit prefill, chunks of four rows
+    (0, 1, 2560, 4096, 8, 32, nat.F16, nat.UNSPECIFIED, "generic"),      # float16 8-bit codes
+    (0, 1, 2048, 2048, 2, 32, nat.F32, nat.UNSPECIFIED, "generic"),      # 2-bit codes
+])
+def test_kernel_selection_bits(op, M, K, N, bits, bs, dtype, zp, expect):
+    assert nat.lib().xrmm_select_kernel(op, M, K, N, bits, bs, dtype, zp).decode() == expect

@@ -69,7 +69,8 @@ MNB_CASES = [
     (48, 512, 128, 32, np.float16, "packed", "gemm_q4_mfma"),
     (128, 512, 256, 64, np.float16, "float", "gemm_q4_mfma"),
     (2048, 256, 4096, 64, np.float16, "packed", "gemm_q4_big"),
-    (5, 96, 40, 32, np.float32, "packed", "generic"),
+    (5, 96, 40, 32, np.float32, "packed", "gemv_q4_f32"),   # float32 rows in chunks of four
+    (5, 98, 40, 32, np.float32, "packed", "generic"),       # K % 4 != 0
     (4, 96, 40, 32, np.float32, "packed", "gemv_q4_f32"),
     (3, 2048, 33, 64, np.float32, "float", "gemv_q4_f32"),
     (1, 4096, 64, 16, np.float32, None, "gemv_q4_f32"),

@@ -1,5 +1,7 @@
 // MatMulNBits GEMV for float32 activations (the contract's T1 = float32),
-// 4-bit weights, up to four rows. Float32 arithmetic throughout, as the
+// 4- or 8-bit weights, any number of rows in chunks of up to four (the grid's
+// second dimension: each chunk reads the weights again, from the L2 / the
+// Infinity Cache for all but the first). Float32 arithmetic throughout, as the
 // reference's serial loop (complex_kernel.glsl:80,83): codes convert exactly
 // to float32 and multiply the activations with fused multiply-adds, so the
 // float32 bar (1e-5 * max|Y|) holds with margin.
@@ -12,10 +14,11 @@
 // codes, and the wave's scale / zero-point block in its own LDS slice; one
 // barrier, then no further synchronisation.
 //
-// Arithmetic. For a dword x of codes c0..c7 (low nibble first),
+// Arithmetic. For a dword x of 4-bit codes c0..c7 (low nibble first),
 // x & 0x0F0F0F0F holds c0, c2, c4, c6 in its bytes and (x >> 4) & 0x0F0F0F0F
-// holds c1, c3, c5, c7; v_cvt_f32_ubyte{0..3} turns each byte into a float.
-// sum_k (c_k - z) a_k = sum_k c_k a_k - z sum_k a_k per block half, with the
+// holds c1, c3, c5, c7; 8-bit codes are the dword's bytes.
+// v_cvt_f32_ubyte{0..3} turns each byte into a float.
+// sum_k (c_k - z) a_k = sum_k c_k a_k - z sum_k a_k per 16 codes, with the
 // activation sums from the staging, then times the block scale.
 #pragma once
 #include "xrmm_gemv_dot.h"
@@ -34,14 +37,18 @@ struct F32Args {
   uint32_t zoff;        // zero points' offset inside the slice
 };
 
-// LDS of the staged activations: [MR][nchunk] chunks of 32 floats at a
-// stride of 36 (the pad puts the 16 lanes of a 16-byte read on distinct
-// banks), then the sums [MR][2 * nchunk] (one per 16 codes).
-constexpr uint32_t kF32ChunkStride = 36;
+// LDS of the staged activations: [MR][nchunk] chunks of 128 / BITS floats
+// (a chunk is 16 bytes of codes) at a stride of 4 more (the pad spreads the
+// lanes of a 16-byte read over the banks), then the sums [MR][nchunk * H],
+// one per 16 codes (H = 2 halves of a 4-bit chunk, 1 for 8-bit).
+template <int BITS>
+__host__ __device__ constexpr uint32_t f32_chunk_stride() {
+  return 128 / BITS + 4;
+}
 
-template <int MR>
+template <int MR, int BITS = 4>
 __host__ __device__ constexpr uint32_t f32_act_bytes(uint32_t nchunk) {
-  return MR * nchunk * kF32ChunkStride * 4u + MR * nchunk * 2u * 4u;
+  return MR * nchunk * f32_chunk_stride<BITS>() * 4u + MR * nchunk * (64u / BITS) / 8u * 4u;
 }
 
 // Byte i of x as a float (the compiler emits v_cvt_f32_ubyte{i}).
@@ -49,20 +56,29 @@ __device__ __forceinline__ float ubyte(uint32_t x, int i) {
   return static_cast<float>((x >> (8 * i)) & 0xFFu);
 }
 
-template <int ZPK, int CPL, int C, int MR, int W>
+template <int ZPK, int CPL, int C, int MR, int W, int BITS = 4>
 __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
+  static_assert(BITS == 4 || BITS == 8, "4- or 8-bit codes");
+  constexpr uint32_t CODES = 128 / BITS;         // codes per 16-byte chunk
+  constexpr uint32_t H = CODES / 16;             // 16-code halves per chunk
+  constexpr uint32_t CS = f32_chunk_stride<BITS>();
+  constexpr float ZMID = BITS == 4 ? 8.f : 128.f;  // implicit zero point 2^(bits - 1)
   extern __shared__ __align__(16) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t N = a.N, K = a.K, kb = a.kb, rowb = a.rowb, zrow = a.zrow;
   const uint32_t nchunk = rowb >> 4;
-  const int M = static_cast<int>(a.M);
+  // this workgroup's chunk of up to MR rows (the grid's second dimension)
+  const uint32_t m0 = blockIdx.y * MR;
+  const int M = static_cast<int>(a.M - m0 < MR ? a.M - m0 : MR);
+  const float* A = a.A + static_cast<size_t>(m0) * K;
+  float* Yo = a.Y + static_cast<size_t>(m0) * N;
   const uint32_t col0 = (blockIdx.x * W + wave) * C;
   auto clampc = [&](uint32_t c) { return c < N ? c : N - 1; };
-  const uint32_t act_floats = MR * nchunk * kF32ChunkStride;
-  float* xs = reinterpret_cast<float*>(smem);        // [MR][nchunk][36]
-  float* sums = xs + act_floats;                     // [MR][2 * nchunk]
-  unsigned char* meta = smem + f32_act_bytes<MR>(nchunk) + wave * a.meta_bytes;
+  const uint32_t act_floats = MR * nchunk * CS;
+  float* xs = reinterpret_cast<float*>(smem);        // [MR][nchunk][CS]
+  float* sums = xs + act_floats;                     // [MR][H * nchunk]
+  unsigned char* meta = smem + f32_act_bytes<MR, BITS>(nchunk) + wave * a.meta_bytes;
 
   // ---- the wave's scale / zero-point block (C consecutive rows), 16-byte
   // pieces; loads start at the dword boundary at or below the block
@@ -92,10 +108,10 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
 
   // ---- activations of the workgroup: 16-byte pieces (4 floats), thread t
   // takes pieces t, t + 64 W, ...
-  const rsrc_t rA = mk_rsrc(a.A, static_cast<uint32_t>(M) * K * 4u);
-  constexpr int PIECES_PER_ROW_MAX = 64 * CPL * 8;  // nchunk * 32 floats / 4
+  const rsrc_t rA = mk_rsrc(A, static_cast<uint32_t>(M) * K * 4u);
+  constexpr int PIECES_PER_ROW_MAX = 64 * CPL * CODES / 4;  // nchunk * CODES floats / 4
   constexpr int PPT = (MR * PIECES_PER_ROW_MAX + W * 64 - 1) / (W * 64);
-  const uint32_t ppr = nchunk * 8u;  // pieces per staged row
+  const uint32_t ppr = nchunk * (CODES / 4);  // pieces per staged row
   u32x4 av[PPT];
 #pragma unroll
   for (int it = 0; it < PPT; ++it) {
@@ -128,12 +144,12 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
 #pragma unroll
   for (int it = 0; it < PPT; ++it) {
     const uint32_t p = static_cast<uint32_t>(tid) + it * W * 64u;
-    if (p < MR * ppr) *reinterpret_cast<u32x4*>(xs + (p >> 3) * kF32ChunkStride + (p & 7u) * 4u) = av[it];
+    if (p < MR * ppr) *reinterpret_cast<u32x4*>(xs + (p / (CODES / 4)) * CS + (p % (CODES / 4)) * 4u) = av[it];
   }
   __syncthreads();
   // sums per 16 codes: thread t sums half h = t, t + 64 W, ...
-  for (uint32_t h = static_cast<uint32_t>(tid); h < MR * nchunk * 2u; h += W * 64u) {
-    const float* x = xs + (h >> 1) * kF32ChunkStride + (h & 1u) * 16u;
+  for (uint32_t h = static_cast<uint32_t>(tid); h < MR * nchunk * H; h += W * 64u) {
+    const float* x = xs + (h / H) * CS + (h % H) * 16u;
     float s0 = 0.f, s1 = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; e += 2) {
@@ -160,30 +176,38 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
       const uint32_t ch = static_cast<uint32_t>(lane + 64 * j);
       const uint32_t chc = ch < nchunk ? ch : nchunk - 1;  // past-the-row lanes: in-range reads, no contribution
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {  // 16-code halves
-        const uint32_t b = (chc * 32u + 16u * h) >> a.bsl;
+      for (int h = 0; h < static_cast<int>(H); ++h) {  // 16-code halves (8-bit: the chunk)
+        const uint32_t b = (chc * CODES + 16u * h) >> a.bsl;
         const float s = *reinterpret_cast<const float*>(meta + (i * kb + b) * 4u);
-        float z = 8.f;
+        float z = ZMID;
         if constexpr (ZPK == ZP_PACKED) {
-          z = static_cast<float>((zmeta[i * zrow + (b >> 1)] >> ((b & 1u) * 4u)) & 15u);
+          if constexpr (BITS == 4) z = static_cast<float>((zmeta[i * zrow + (b >> 1)] >> ((b & 1u) * 4u)) & 15u);
+          else z = static_cast<float>(zmeta[i * zrow + b]);
         } else if constexpr (ZPK == ZP_FLOAT) {
           const unsigned char* zp = zmeta + i * zrow + b * a.zesz;
           z = a.zesz == 4 ? *reinterpret_cast<const float*>(zp) : static_cast<float>(*reinterpret_cast<const f16*>(zp));
         }
         float cv[16];
+        if constexpr (BITS == 4) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const uint32_t x = wv[i][j][2 * h + q];
-          const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+          for (int q = 0; q < 2; ++q) {
+            const uint32_t x = wv[i][j][2 * h + q];
+            const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            cv[8 * q + 2 * e] = ubyte(lo, e);
-            cv[8 * q + 2 * e + 1] = ubyte(hi, e);
+            for (int e = 0; e < 4; ++e) {
+              cv[8 * q + 2 * e] = ubyte(lo, e);
+              cv[8 * q + 2 * e + 1] = ubyte(hi, e);
+            }
           }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cv[4 * q + e] = ubyte(wv[i][j][q], e);
         }
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-          const float* x = xs + (m * nchunk + chc) * kF32ChunkStride + 16u * h;
+          const float* x = xs + (m * nchunk + chc) * CS + 16u * h;
           const f32x4 x0 = *reinterpret_cast<const f32x4*>(x), x1 = *reinterpret_cast<const f32x4*>(x + 4);
           const f32x4 x2 = *reinterpret_cast<const f32x4*>(x + 8), x3 = *reinterpret_cast<const f32x4*>(x + 12);
           const float xv[16] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3],
@@ -194,7 +218,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
             p0 = __builtin_fmaf(cv[e], xv[e], p0);
             p1 = __builtin_fmaf(cv[e + 1], xv[e + 1], p1);
           }
-          const float sa = sums[(m * nchunk + chc) * 2u + h];
+          const float sa = sums[(m * nchunk + chc) * H + h];
           float t = __builtin_fmaf(-z, sa, p0 + p1);
           if (!__builtin_isfinite(sa)) {
             // an infinite activation: the folded form would give Inf - Inf;
@@ -220,7 +244,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
     const float b = a.bias ? a.bias[mycol] : 0.f;
 #pragma unroll
     for (int m = 0; m < MR; ++m)
-      if (m < M) a.Y[static_cast<uint32_t>(m) * N + mycol] = out[m] + b;
+      if (m < M) Yo[static_cast<uint32_t>(m) * N + mycol] = out[m] + b;
   }
 }
 
@@ -234,7 +258,8 @@ inline int f32_cpl(const Launch& L) {
   return 0;
 }
 
-inline int f32_mr(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 0; }
+// Rows per workgroup: 1, 2 or 4 (more rows: chunks of four on the grid's y).
+inline int f32_mr(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
 
 inline uint32_t f32_meta_bytes(const Launch& L, uint32_t& zoff) {
   const uint32_t sb = static_cast<uint32_t>(kF32C * L.kb * 4);
@@ -244,14 +269,17 @@ inline uint32_t f32_meta_bytes(const Launch& L, uint32_t& zoff) {
   return (zoff + zb + 3u + 15u) & ~15u;
 }
 
-// fp32, 4-bit, power-of-two block_size >= 16, K a multiple of 4, 16-byte
-// aligned tensors, up to four rows, rows of at most 256 chunks, the wave's
-// scale / zero-point block within 4 KB and the staging within 160 KB of LDS.
+// fp32, 4- or 8-bit, power-of-two block_size >= 16, K a multiple of 4,
+// 16-byte aligned tensors, rows of at most 256 chunks (whole 16-byte chunks),
+// the wave's scale / zero-point block within 4 KB and the staging within
+// 160 KB of LDS; at most 65535 chunks of four rows (the grid's y).
 inline bool f32_fits(const Launch& L) {
-  if (L.dtype != DT_F32 || L.bits != 4 || L.bs_log2 < 4 || L.op != OP_MATMUL || L.K % 4 != 0) return false;
-  if ((L.kb * L.block_size) % 32 != 0) return false;
+  if (L.dtype != DT_F32 || (L.bits != 4 && L.bits != 8) || L.bs_log2 < 4 || L.op != OP_MATMUL || L.K % 4 != 0)
+    return false;
+  if ((L.kb * L.block_size) % (128 / L.bits) != 0) return false;
+  if (L.M < 1 || (L.M + 3) / 4 > 65535) return false;
   const int mr = f32_mr(L.M), cpl = f32_cpl(L);
-  if (mr == 0 || cpl == 0) return false;
+  if (cpl == 0) return false;
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   if (!al(L.A) || !al(L.p[0].B) || !al(L.p[0].scales) || !al(L.p[0].zp)) return false;
   if (L.zp_kind == ZP_FLOAT && L.p[0].zp == nullptr) return false;
@@ -259,12 +287,13 @@ inline bool f32_fits(const Launch& L) {
   const uint32_t meta = f32_meta_bytes(L, zoff);
   if (kF32C * L.kb * 4 > 4096 || meta - zoff > 4096 + 16) return false;
   const uint32_t nchunk = static_cast<uint32_t>(L.kb * L.blob / 16);
-  if (mr * f32_cpl(L) > 8) return false;  // activation loads per thread (registers)
-  const int64_t lds = int64_t(mr) * nchunk * kF32ChunkStride * 4 + int64_t(mr) * nchunk * 2 * 4 + int64_t(kF32W) * meta;
+  if (mr * f32_cpl(L) * 8 / L.bits > 16) return false;  // activation loads per thread (registers)
+  const int64_t codes = 128 / L.bits;
+  const int64_t lds = int64_t(mr) * nchunk * (codes + 4) * 4 + int64_t(mr) * nchunk * (codes / 16) * 4 + int64_t(kF32W) * meta;
   return lds <= 160 * 1024;
 }
 
-template <int ZPK, int CPL, int MR>
+template <int ZPK, int CPL, int MR, int BITS>
 inline hipError_t launch_f32_3(const Launch& L, hipStream_t st) {
   F32Args a{};
   const Proj& P = L.p[0];
@@ -284,34 +313,40 @@ inline hipError_t launch_f32_3(const Launch& L, hipStream_t st) {
   a.bsl = static_cast<uint32_t>(L.bs_log2);
   a.meta_bytes = f32_meta_bytes(L, a.zoff);
   const uint32_t nchunk = a.rowb / 16u;
-  const size_t lds = f32_act_bytes<MR>(nchunk) + size_t(kF32W) * a.meta_bytes;
-  auto kern = k_gemv_f32<ZPK, CPL, kF32C, MR, kF32W>;
+  const size_t lds = f32_act_bytes<MR, BITS>(nchunk) + size_t(kF32W) * a.meta_bytes;
+  auto kern = k_gemv_f32<ZPK, CPL, kF32C, MR, kF32W, BITS>;
   if (lds > 64 * 1024) {
     static std::atomic<int> done[kMaxDevices];  // per instantiation and device
     const hipError_t attr = raise_lds_cap(reinterpret_cast<const void*>(kern), 160 * 1024, done);
     if (attr != hipSuccess) return attr;
   }
   const uint32_t waves = static_cast<uint32_t>((P.N + kF32C - 1) / kF32C);
-  hipLaunchKernelGGL(kern, dim3((waves + kF32W - 1) / kF32W), dim3(kF32W * 64), lds, st, a);
+  const uint32_t chunks = static_cast<uint32_t>((L.M + MR - 1) / MR);
+  hipLaunchKernelGGL(kern, dim3((waves + kF32W - 1) / kF32W, chunks), dim3(kF32W * 64), lds, st, a);
   return hipGetLastError();
 }
 
-template <int ZPK, int CPL>
+template <int ZPK, int CPL, int BITS>
 inline hipError_t launch_f32_2(const Launch& L, hipStream_t st) {
   switch (f32_mr(L.M)) {
-    case 1: return launch_f32_3<ZPK, CPL, 1>(L, st);
-    case 2: return launch_f32_3<ZPK, CPL, 2>(L, st);
-    default: return launch_f32_3<ZPK, CPL, 4>(L, st);
+    case 1: return launch_f32_3<ZPK, CPL, 1, BITS>(L, st);
+    case 2: return launch_f32_3<ZPK, CPL, 2, BITS>(L, st);
+    default: return launch_f32_3<ZPK, CPL, 4, BITS>(L, st);
+  }
+}
+
+template <int ZPK, int BITS>
+inline hipError_t launch_f32_b(const Launch& L, hipStream_t st) {
+  switch (f32_cpl(L)) {
+    case 1: return launch_f32_2<ZPK, 1, BITS>(L, st);
+    case 2: return launch_f32_2<ZPK, 2, BITS>(L, st);
+    default: return launch_f32_2<ZPK, 4, BITS>(L, st);
   }
 }
 
 template <int ZPK>
 inline hipError_t launch_f32_1(const Launch& L, hipStream_t st) {
-  switch (f32_cpl(L)) {
-    case 1: return launch_f32_2<ZPK, 1>(L, st);
-    case 2: return launch_f32_2<ZPK, 2>(L, st);
-    default: return launch_f32_2<ZPK, 4>(L, st);
-  }
+  return L.bits == 8 ? launch_f32_b<ZPK, 8>(L, st) : launch_f32_b<ZPK, 4>(L, st);
 }
 
 // Entry of one zero-point kind (defined in xrmm_gemv_f32_zp.hip).
