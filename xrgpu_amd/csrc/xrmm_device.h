@@ -305,4 +305,15 @@ __device__ __forceinline__ u32x4 ld16(const void* p) {
   return *static_cast<const u32x4*>(p);
 }
 
+// Logical index of workgroup b on a grid of n. The dispatcher hands
+// consecutive workgroups to consecutive XCDs (eight on gfx950, each with its
+// own L2), so the first 8 floor(n / 8) workgroups are renumbered to make XCD
+// b % 8 walk the contiguous range (b % 8) * (n / 8) ... of the logical order;
+// the remainder keeps its index. Output lines then fill inside one XCD's L2
+// instead of collecting partial writes from all eight.
+__device__ __forceinline__ uint32_t xcd_slot(uint32_t b, uint32_t n) {
+  const uint32_t per = n >> 3;
+  return b < (per << 3) ? (b & 7u) * per + (b >> 3) : b;
+}
+
 }  // namespace xrmm

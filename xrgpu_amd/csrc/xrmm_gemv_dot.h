@@ -122,7 +122,10 @@ __global__ __launch_bounds__(W * 64) void k_gemv_dot(DotArgs a) {
   // the grid (a workgroup may hold waves of two projections: they share the
   // activations). Every projection's fields are loaded with the other
   // arguments and picked with scalar selects, so no load depends on the choice.
-  const uint32_t bid = blockIdx.x;
+#ifndef XRMM_DOT_XCD
+#define XRMM_DOT_XCD 1
+#endif
+  const uint32_t bid = XRMM_DOT_XCD ? xcd_slot(blockIdx.x, gridDim.x) : blockIdx.x;
   const uint32_t gw = bid * W + wave;  // global wave index
   uint32_t pi = 0;
   if constexpr (QKV) pi = (gw >= a.p[1].wg0 ? 1u : 0u) + (gw >= a.p[2].wg0 ? 1u : 0u);

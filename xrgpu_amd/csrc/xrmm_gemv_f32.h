@@ -73,7 +73,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
   const int M = static_cast<int>(a.M - m0 < MR ? a.M - m0 : MR);
   const float* A = a.A + static_cast<size_t>(m0) * K;
   float* Yo = a.Y + static_cast<size_t>(m0) * N;
-  const uint32_t col0 = (blockIdx.x * W + wave) * C;
+  const uint32_t col0 = (xcd_slot(blockIdx.x, gridDim.x) * W + wave) * C;
   auto clampc = [&](uint32_t c) { return c < N ? c : N - 1; };
   const uint32_t act_floats = MR * nchunk * CS;
   float* xs = reinterpret_cast<float*>(smem);        // [MR][nchunk][CS]

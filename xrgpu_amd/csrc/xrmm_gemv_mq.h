@@ -129,7 +129,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t n = lane & 15, g = lane >> 4;
-  const uint32_t tile = blockIdx.x;
+  const uint32_t tile = xcd_slot(blockIdx.x, gridDim.x);
   uint32_t pi = 0;
   if constexpr (QKV) pi = (tile >= a.p[1].t0 ? 1u : 0u) + (tile >= a.p[2].t0 ? 1u : 0u);
   auto pick = [&](auto v0, auto v1, auto v2) { return QKV ? (pi == 0 ? v0 : pi == 1 ? v1 : v2) : v0; };

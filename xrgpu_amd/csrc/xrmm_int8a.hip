@@ -52,7 +52,7 @@ __global__ __launch_bounds__(I8T) void k_i8a_quant(Int8aArgs a) {
 template <typename T, int CPL>
 __global__ __launch_bounds__(I8T) void k_i8a_gemv(Int8aArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * (I8T / 64) + (threadIdx.x >> 6);
+  const int64_t n = static_cast<int64_t>(xcd_slot(blockIdx.x, gridDim.x)) * (I8T / 64) + (threadIdx.x >> 6);
   if (n >= a.N) return;  // whole waves
   const uint32_t chunks = static_cast<uint32_t>(a.K / 32);
   const int64_t kb = a.K >> a.lbs;

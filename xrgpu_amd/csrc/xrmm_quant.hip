@@ -157,8 +157,9 @@ __global__ __launch_bounds__(QT) void k_bnb4_gemv(Bnb4Args a, int ctiles) {
   extern __shared__ __align__(16) float xs[];  // [MR][steps * 64 * 36], then the table
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ctile = static_cast<int>(blockIdx.x % ctiles);
-  const int64_t m0 = static_cast<int64_t>(blockIdx.x / ctiles) * MR;
+  const uint32_t bid = xcd_slot(blockIdx.x, gridDim.x);
+  const int ctile = static_cast<int>(bid % static_cast<uint32_t>(ctiles));
+  const int64_t m0 = static_cast<int64_t>(bid / static_cast<uint32_t>(ctiles)) * MR;
   const int K = static_cast<int>(a.K), N = static_cast<int>(a.N);
   const uint32_t colb = static_cast<uint32_t>(K / 2);  // bytes of one column
   const uint32_t chunks = colb / 16;
