@@ -772,7 +772,8 @@ def main():
             "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes,
             "replicas": r["replicas"],
             "kernel": ops.select_kernel("MatMulNBits", q["M"], q["K"], q["N"], 4, q["bs"], zp="packed") + " (split-K)",
-            "traffic": traffic_of("down_proj_m64_gemm.md", "gemm_q4_mfma")}
+            "traffic": traffic_of("down_proj_m64_gemm.md",
+                                  ops.select_kernel("MatMulNBits", q["M"], q["K"], q["N"], 4, q["bs"], zp="packed"))}
     for name, q, what in (("q8_f32_decode_m1", Q8F32, "MatMulNBits float32 M=1 K=2560 N=4096 bits=8 bs=32 (upstream "
                                                      "qwen3-qproj-decode-m1-q8g32 geometry)"),
                           ("f32_prefill_m64", F32P, "MatMulNBits float32 M=64 K=4096 N=4096 bits=4 bs=32")):

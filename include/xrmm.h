@@ -85,8 +85,9 @@ int xrmm_matmul_nbits(const void* A, const void* B, const void* scales, const vo
 
 /* xrmm_matmul_nbits with a caller's workspace, for geometries whose output
  * tiles leave compute units idle (more than 16 rows with few columns or few
- * rows; the Llama-style down projection K = 14336, N = 4096 at 17..127 rows
- * has 32 tiles for 256 CUs): the K range is split over workgroups, each
+ * rows; the Llama-style down projection K = 14336, N = 4096 has 64 column
+ * tiles on the thin GEMM at 17..64 rows and 32 tiles on the 128 x 128 GEMM
+ * at 65..127 rows, for 256 CUs): the K range is split over workgroups, each
  * split writes a float32 partial tile to the workspace and the last split of
  * a tile adds them in split order (deterministic). No counterpart in the
  * reference (one serial loop, complex_kernel.glsl:83); same results as

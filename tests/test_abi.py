@@ -90,6 +90,8 @@ def test_qkv_requires_norm_scale():
     (0, 127, 4096, 14336, 32, nat.F16, nat.U8, "gemm_q4_mfma"),
     (0, 64, 4096, 14336, 32, nat.F16, nat.F16, "gemv_q4_splitk"),    # four row chunks of 16
     (0, 65, 4096, 14336, 32, nat.F16, nat.F16, "gemm_q4_mfma"),
+    (0, 64, 14336, 4096, 32, nat.F16, nat.U8, "gemm_q4_thin"),       # the down projection at 64 rows
+    (0, 17, 512, 96, 16, nat.F16, nat.F16, "gemm_q4_thin"),          # no split-K GEMV shape for K = 512
     (1, 4, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_mq"),
     (1, 4, 4096, 4096, 64, nat.F16, nat.F16, "gemv_q4_dot"),      # float zero points
     (1, 2, 8192, 4096, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_dot"),  # K beyond the MFMA GEMV's 4096
@@ -154,7 +156,7 @@ def test_fuzz_reaches_every_kernel_family():
     for M, K, N, bs, *_ in F.MLP + F.MLP2:
         seen.add(ops.select_kernel("MatMulNBitsMlp", M, K, N, 4, bs, torch.float16))
     want = {"gemv_q4_dot", "gemv_q4_mq", "gemv_q4_splitk", "gemv_q4_mfma", "gemv_q4_f32", "gemm_q4_mfma",
-            "gemm_q4_fused", "generic"}
+            "gemm_q4_thin", "gemm_q4_fused", "generic"}
     assert want <= seen, f"not reached: {sorted(want - seen)}"
 
 

@@ -66,7 +66,7 @@ MNB_CASES = [
     (5, 2048, 64, 32, np.float16, None, "gemv_q4_splitk"),
     (8, 4096, 40, 64, np.float16, "packed", "gemv_q4_splitk"),
     (5, 512, 48, 16, np.float16, "packed", "gemv_q4_mfma"),
-    (48, 512, 128, 32, np.float16, "packed", "gemm_q4_mfma"),
+    (48, 512, 128, 32, np.float16, "packed", "gemm_q4_thin"),
     (128, 512, 256, 64, np.float16, "float", "gemm_q4_mfma"),
     (2048, 256, 4096, 64, np.float16, "packed", "gemm_q4_big"),
     (5, 96, 40, 32, np.float32, "packed", "gemv_q4_f32"),   # float32 rows in chunks of four
@@ -181,7 +181,7 @@ def test_mlp_nonfinite_activations(gpu, M, K, N, bs, dtype, norm, family):
 
 @pytest.mark.parametrize("M,K,N,bs,zp,family", [(1, 1024, 64, 32, None, "gemv_q4_dot"),
                                                  (5, 2048, 64, 32, "packed", "gemv_q4_splitk"),
-                                                 (48, 512, 128, 32, "packed", "gemm_q4_mfma"),
+                                                 (48, 512, 128, 32, "packed", "gemm_q4_thin"),
                                                  (128, 512, 256, 64, "float", "gemm_q4_mfma"),
                                                  (2048, 256, 4096, 64, "packed", "gemm_q4_big")])
 def test_large_scales_within_binary16_weight_range(gpu, M, K, N, bs, zp, family):

@@ -179,9 +179,12 @@ def test_gemv_fp32_parity(gpu, M, K, N, bs, zp, bias, zdt):
 
 
 GEMM_CASES = [
-    # M, K, N, bs, zp, bias: 17 <= M < 128 runs the 128 x 128 GEMM (K of
-    # neither 64 nor 128 chunks: the split-K GEMV takes no row chunks)
+    # M, K, N, bs, zp, bias: K of neither 64 nor 128 chunks, so the split-K
+    # GEMV takes no row chunks: 17 <= M <= 64 runs the thin GEMM (one or two
+    # 32-row MFMA tiles), 65 <= M < 128 the 128 x 128 GEMM
     (17, 256, 64, 32, None, False),
+    (40, 288, 70, 16, "float", True),       # thin: bs = 16, K tail
+    (32, 1056, 200, 32, "packed", True),    # thin: one row tile, a partial last chunk
     (64, 512, 130, 32, "packed", True),
     (96, 288, 40, 32, "packed", True),   # K tail
     (127, 1024, 256, 128, "packed", True),
@@ -196,7 +199,10 @@ def test_gemm_fp16_parity(gpu, M, K, N, bs, zp, bias):
     rng = np.random.default_rng(M * 7 + K + N + bs)
     A, B, S, Z, b = rand_case(rng, M, K, N, 4, bs, np.float16, zp, bias)
     kind = None if zp is None else ("packed" if zp == "packed" else "float")
-    assert ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16, kind) == "gemm_q4_mfma"
+    # up to 64 rows the thin GEMM (split-K GEMV geometries aside), above it
+    # the 128 x 128 GEMM
+    want = "gemm_q4_thin" if M <= 64 else "gemm_q4_mfma"
+    assert ops().select_kernel("MatMulNBits", M, K, N, 4, bs, torch.float16, kind) == want
     Y = host(ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, block_size=bs))
     ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, block_size=bs)
     assert_parity(Y, ref, np.float16)

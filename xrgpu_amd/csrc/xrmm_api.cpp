@@ -122,7 +122,8 @@ int64_t xrmm_matmul_nbits_workspace_bytes(int64_t M, int64_t K, int64_t N, int32
   }
   L.nproj = 1;
   L.p[0].N = N;
-  if (M <= 0 || xrmm::select_kernel(L) != xrmm::K_GEMM_Q4) return 0;
+  const xrmm::Kernel k = M > 0 ? xrmm::select_kernel(L) : xrmm::K_GENERIC;
+  if (k != xrmm::K_GEMM_Q4 && k != xrmm::K_GEMM_THIN) return 0;
   return xrmm::gemm_workspace_bytes(L, xrmm::gemm_splits(L));
 }
 
@@ -137,7 +138,8 @@ int xrmm_matmul_nbits_ws(const void* A, const void* B, const void* scales, const
   L.nproj = 1;
   L.A = A;
   L.p[0] = xrmm::Proj{static_cast<const uint8_t*>(B), scales, zero_points, bias, Y, N};
-  if (M > 0 && workspace && xrmm::select_kernel(L) == xrmm::K_GEMM_Q4) {
+  const xrmm::Kernel k = M > 0 ? xrmm::select_kernel(L) : xrmm::K_GENERIC;
+  if (workspace && (k == xrmm::K_GEMM_Q4 || k == xrmm::K_GEMM_THIN)) {
     const int splits = xrmm::gemm_splits(L);
     const int64_t need = xrmm::gemm_workspace_bytes(L, splits);
     if (need > 0) {

@@ -1,6 +1,7 @@
 // One zero-point kind of the prefill GEMM; the build compiles this file once
 // per kind with -DXRMM_ZPK=<0|1|2>.
 #include "xrmm_gemm.h"
+#include "xrmm_gemm_thin.h"
 
 #ifndef XRMM_ZPK
 #error "XRMM_ZPK must be defined"
@@ -24,6 +25,11 @@ hipError_t launch_gemm_big_fused_for<XRMM_ZPK>(const Launch& L, hipStream_t st) 
 template <>
 hipError_t launch_gemm_big_pk_for<XRMM_ZPK>(const Launch& L, hipStream_t st) {
   return L.block_size >= 32 ? launch_gemm_big<XRMM_ZPK, 1, true>(L, st) : launch_gemm_big<XRMM_ZPK, 2, true>(L, st);
+}
+
+template <>
+hipError_t launch_gemm_thin_for<XRMM_ZPK>(const Launch& L, hipStream_t st) {
+  return launch_thin<XRMM_ZPK>(L, st);
 }
 
 }  // namespace xrmm

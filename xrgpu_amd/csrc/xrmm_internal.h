@@ -75,7 +75,7 @@ class ExactWeightsScope {
 
 // Kernel families the dispatcher chooses between.
 enum Kernel { K_GENERIC = 0, K_GEMV_Q4 = 1, K_GEMM_Q4 = 2, K_GEMV_DOT = 3, K_GEMM_BIG = 4, K_GEMV_SK = 5, K_GEMV_MQ = 6,
-              K_GEMV_F32 = 7, K_GEMM_FUSED = 8, K_GEMM_BIG_FUSED = 9 };
+              K_GEMV_F32 = 7, K_GEMM_FUSED = 8, K_GEMM_BIG_FUSED = 9, K_GEMM_THIN = 10 };
 
 // Whether a Qkv / Mlp launch has a prologue (skip or normScale) whose
 // normalised activations a prefill GEMM can take from L.xs.

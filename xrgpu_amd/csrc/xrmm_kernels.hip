@@ -41,6 +41,7 @@
 #include "xrmm_gemv_sk.h"
 #include "xrmm_gemm.h"
 #include "xrmm_gemm_fused.h"
+#include "xrmm_gemm_thin.h"
 
 namespace xrmm {
 
@@ -590,6 +591,17 @@ inline int64_t split_k_min_rows(int op) { return op == OP_MATMUL ? 3 : op == OP_
 // N = 14336) and loses to the dot GEMV below.
 inline bool mq_takes(const Launch& L) { return L.op == OP_QKV && L.M <= 4 && mq_fits(L); }
 
+// MatMulNBits with 17..64 rows: the thin GEMM (weights straight into the
+// MFMA operands, activations shared through LDS) where the split-K GEMV does
+// not apply, or everywhere in that range with XRMM_THIN_OVER_SK.
+#ifndef XRMM_THIN_OVER_SK
+#define XRMM_THIN_OVER_SK 0
+#endif
+inline bool thin_takes(const Launch& L) {
+  if (L.op != OP_MATMUL || L.M <= 16 || L.M > 64) return false;
+  return XRMM_THIN_OVER_SK || !sk_fits(L);
+}
+
 Kernel select_kernel(const Launch& L) {
   if (L.exact_weights) {
     // the dot and four-row MFMA GEMVs keep weights out of binary16; every
@@ -604,6 +616,7 @@ Kernel select_kernel(const Launch& L) {
   if (f32_fits(L) && fits_i32(L)) return K_GEMV_F32;
   if (q4_fast_ok(L) && fits_i32(L)) {
     if (mq_takes(L)) return K_GEMV_MQ;
+    if (thin_takes(L)) return K_GEMM_THIN;
     if (L.M >= split_k_min_rows(L.op) && sk_fits(L)) return K_GEMV_SK;
     if ((L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 && dot_fits(L)) return K_GEMV_DOT;
     if (L.M >= 1 && L.M <= 16 && gemv_tiles(L) != 0) return K_GEMV_Q4;
@@ -630,6 +643,7 @@ const char* kernel_name(Kernel k) {
     case K_GEMM_BIG: return "gemm_q4_big";
     case K_GEMM_FUSED: return "gemm_q4_fused";
     case K_GEMM_BIG_FUSED: return "gemm_q4_big_fused";
+    case K_GEMM_THIN: return "gemm_q4_thin";
     default: return "generic";
   }
 }
@@ -649,6 +663,7 @@ static int gemm_kgroups(int64_t wgs) {
 // the workspace traffic). Measured, K = 14336, N = 4096, 64 rows (32 tiles,
 // 8 splits): 39.5 against 153.8 us without the split.
 int gemm_splits(const Launch& L) {
+  if (select_kernel(L) == K_GEMM_THIN) return static_cast<int>(thin_args(L, true).S);
   const int64_t tiles = ((L.p[0].N + GM_BN - 1) / GM_BN) * ((L.M + GM_BM - 1) / GM_BM);
   if (tiles * 4 > kGemmCounterBytes) return 1;
   const int64_t ktiles = (L.kb * L.block_size + GM_BK - 1) / GM_BK;
@@ -661,6 +676,7 @@ int gemm_splits(const Launch& L) {
 
 int64_t gemm_workspace_bytes(const Launch& L, int splits) {
   if (splits < 2) return 0;
+  if (select_kernel(L) == K_GEMM_THIN) return thin_ws_bytes(L);
   const int64_t tiles = ((L.p[0].N + GM_BN - 1) / GM_BN) * ((L.M + GM_BM - 1) / GM_BM);
   return kGemmCounterBytes + tiles * splits * int64_t(256 * 64 * 4);
 }
@@ -741,6 +757,11 @@ hipError_t launch(const Launch& L, hipStream_t st) {
     if (zpk == ZP_NONE) return launch_gemm_fused_for<ZP_NONE>(Lx, st);
     if (zpk == ZP_FLOAT) return launch_gemm_fused_for<ZP_FLOAT>(Lx, st);
     return launch_gemm_fused_for<ZP_PACKED>(Lx, st);
+  }
+  if (k == K_GEMM_THIN) {
+    if (zpk == ZP_NONE) return launch_gemm_thin_for<ZP_NONE>(L, st);
+    if (zpk == ZP_FLOAT) return launch_gemm_thin_for<ZP_FLOAT>(L, st);
+    return launch_gemm_thin_for<ZP_PACKED>(L, st);
   }
   if (k == K_GEMM_Q4) {
     if (zpk == ZP_NONE) return launch_gemm1<ZP_NONE>(L, st);
