@@ -46,15 +46,34 @@ struct ThinArgs {
   uint32_t tiles;   // column tiles
 };
 
-// LDS bytes: two buffers of KQ chunks x rows x (KC + 8) halfs.
-template <int CG, int KC, int MT>
+// Block-metadata slots per column and iteration (the KQ chunks of an
+// iteration span at most KQ KC / 16 blocks of 16 codes, or two blocks when
+// blocks are longer than the iteration).
+template <int CG, int KC>
+__host__ __device__ constexpr int thin_meta_slots() {
+  return (8 / CG) * KC / 16;
+}
+
+// LDS bytes: two buffers of KQ chunks x rows x (KC + 8) halfs, and with
+// staged metadata (integer zero points) two buffers of NT columns x slots of
+// binary16 scales and zero-point nibbles (one byte each).
+template <int CG, int KC, int MT, bool STG>
 __host__ __device__ constexpr int thin_lds_bytes() {
-  return 2 * (8 / CG) * (32 * MT) * (KC + 8) * 2;
+  return 2 * (8 / CG) * (32 * MT) * (KC + 8) * 2 + (STG ? 2 * 32 * CG * thin_meta_slots<CG, KC>() * 3 : 0);
 }
 
 template <int ZPK, int SPC, int CG, int KC, int MT>
 __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
+  // Integer zero points (and none): the iteration's scales and zero points
+  // are staged in LDS with the activations, loaded by consecutive threads
+  // along each column's block row. Float zero points: each lane loads its
+  // pieces' metadata itself.
+  constexpr bool STG = ZPK != ZP_FLOAT;
   constexpr int KQ = 8 / CG, NT = 32 * CG, ROWS = 32 * MT;
+  constexpr int MS = thin_meta_slots<CG, KC>();     // metadata slots per column and iteration
+  constexpr int MPT = NT * MS / GT_T;               // metadata slots per thread
+  static_assert(MPT * GT_T == NT * MS, "metadata slots divide over the threads");
+  constexpr int META = NT * MS * 3;                 // bytes per metadata buffer (scales, then nibbles)
   constexpr int LD = KC + 8;                  // halfs per staged row
   constexpr int CH = ROWS * LD;               // halfs per staged chunk
   constexpr int BUF = KQ * CH;                // halfs per buffer
@@ -65,6 +84,7 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
   constexpr uint32_t OOB = 0x80000000u;
   extern __shared__ __align__(16) unsigned char smem[];
   f16* lds = reinterpret_cast<f16*>(smem);
+  unsigned char* mlds = smem + 2 * BUF * 2;  // metadata buffers
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -94,7 +114,7 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
 
   struct WRegs {
     u32x4 w[PJ];
-    uint32_t s[PJ][SPC], z[PJ][SPC];
+    uint32_t s[STG ? 1 : PJ][SPC], z[STG ? 1 : PJ][SPC];
   };
   // weights of iteration i (chunk c0 + KQ i + kq of this K group); `live`
   // false turns the loads into zero reads instead of branching around them
@@ -110,6 +130,7 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
       // load instructions (two pieces each of two chunks), so it should stay
       // in the caches between them (non-temporal loads measured 10% slower)
       r.w[j] = bld16(rB, (bcol | past) + pc * 16u, 0);
+      if constexpr (!STG) {
 #pragma unroll
       for (int q = 0; q < SPC; ++q) {
         const uint32_t b = (pc * 32u + 16u * q) >> L.bs_log2;
@@ -119,12 +140,47 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
         else if constexpr (ZPK == ZP_FLOAT)
           r.z[j][q] = L.zp_dtype == DT_F32 ? bld_u32(rZ, (zcol | past) + b * 4u, 0) : bld_u16(rZ, (zcol | past) + b * 2u, 0);
       }
+      }
     }
   };
 
   // ---- activations: KQ chunks x ROWS rows of an iteration, APT 16-byte
   // pieces per thread (rows past M and k past K read zero)
   const rsrc_t rA = mk_rsrc(L.A, M * K * 2u);
+  // first block of iteration i's chunks, and how many blocks they span
+  auto blk0 = [&](uint32_t i) { return ((c0 + KQ * i) * KC) >> L.bs_log2; };
+  auto nblk = [&](uint32_t i) { return ((((c0 + KQ * i + KQ) * KC) - 1u) >> L.bs_log2) - blk0(i) + 1u; };
+  struct MRegs {
+    uint32_t s[STG ? MPT : 1], z[STG ? MPT : 1];
+  };
+  // metadata of iteration i: slot e = tid + GT_T x is block blk0 + e % MS of
+  // column n0 + e / MS
+  auto mload = [&](MRegs& mr, uint32_t i, bool live) {
+    if constexpr (STG) {
+      const uint32_t b0 = blk0(i), nb = nblk(i);
+      const bool it = live & (c0 + KQ * i < c1);
+#pragma unroll
+      for (int x = 0; x < MPT; ++x) {
+        const uint32_t e = static_cast<uint32_t>(tid + GT_T * x), col = n0 + e / MS, sl = e % MS, b = b0 + sl;
+        const bool ok = it & (sl < nb) & (col < N) & (b < kb);
+        mr.s[x] = bld_u16(rS, ok ? col * kb * 2u + b * 2u : OOB, 0);
+        mr.z[x] = 0u;
+        if constexpr (ZPK == ZP_PACKED) mr.z[x] = bld_u8(rZ, ok ? col * zrow + (b >> 1) : OOB, 0);
+      }
+    }
+  };
+  auto mstore = [&](const MRegs& mr, int buf, uint32_t i) {
+    if constexpr (STG) {
+      unsigned char* ms = mlds + buf * META;
+      const uint32_t b0 = blk0(i);
+#pragma unroll
+      for (int x = 0; x < MPT; ++x) {
+        const uint32_t e = static_cast<uint32_t>(tid + GT_T * x);
+        *reinterpret_cast<uint16_t*>(ms + e * 2u) = static_cast<uint16_t>(mr.s[x]);
+        if constexpr (ZPK == ZP_PACKED) ms[NT * MS * 2 + e] = static_cast<unsigned char>((mr.z[x] >> (((b0 + e % MS) & 1u) * 4u)) & 15u);
+      }
+    }
+  };
   auto aload = [&](u32x4 (&ra)[APT], uint32_t i, bool live) {
 #pragma unroll
     for (int e = 0; e < APT; ++e) {
@@ -155,23 +211,27 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
   auto compute = [&](const WRegs& r, int buf, uint32_t i) {
     const uint32_t c = c0 + KQ * i + static_cast<uint32_t>(kq);
     const f16* As = lds + buf * BUF + kq * CH + (lane & 31) * LD + g * 32;
+    const unsigned char* ms = mlds + buf * META + (32u * cg + static_cast<uint32_t>(lane & 31)) * MS * 2u;
+    const unsigned char* mz = mlds + buf * META + NT * MS * 2 + (32u * cg + static_cast<uint32_t>(lane & 31)) * MS;
+    const uint32_t b0 = blk0(i);
 #pragma unroll
     for (int j = 0; j < PJ; ++j) {
       Dq dc[SPC];
       float zf[SPC], sf[SPC];
 #pragma unroll
       for (int q = 0; q < SPC; ++q) {
-        const f16 sc = __builtin_bit_cast(f16, static_cast<uint16_t>(r.s[j][q]));
+        const uint32_t pc = c * (KC / 32) + 2u * j + g;
+        const uint32_t b = (pc * 32u + 16u * q) >> L.bs_log2;
+        const uint16_t sbits = STG ? *reinterpret_cast<const uint16_t*>(ms + (b - b0) * 2u) : static_cast<uint16_t>(r.s[STG ? 0 : j][q]);
+        const f16 sc = __builtin_bit_cast(f16, sbits);
         float z;
         if constexpr (ZPK == ZP_NONE) {
           z = 8.f;
         } else if constexpr (ZPK == ZP_PACKED) {
-          const uint32_t pc = c * (KC / 32) + 2u * j + g;
-          const uint32_t b = (pc * 32u + 16u * q) >> L.bs_log2;
-          z = static_cast<float>((r.z[j][q] >> ((b & 1u) * 4u)) & 15u);
+          z = static_cast<float>(mz[b - b0]);
         } else {
-          z = L.zp_dtype == DT_F32 ? __builtin_bit_cast(float, r.z[j][q])
-                                   : static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(r.z[j][q])));
+          z = L.zp_dtype == DT_F32 ? __builtin_bit_cast(float, r.z[STG ? 0 : j][q])
+                                   : static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(r.z[STG ? 0 : j][q])));
         }
         zf[q] = z;
         sf[q] = static_cast<float>(sc);
@@ -199,11 +259,15 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
     const uint32_t nr = t.ni - base < GT_IMAX ? t.ni - base : GT_IMAX;
     WRegs wr[GT_IMAX];
     u32x4 ra[APT];
+    MRegs mr;
     aload(ra, base, true);
+    mload(mr, base, true);
     wload(wr[0], base, true);
     wload(wr[1], base + 1, nr > 1);
     astore(ra, 0);  // buffer 0 was last read before the previous round's final barrier
+    mstore(mr, 0, base);
     aload(ra, base + 1, nr > 1);
+    mload(mr, base + 1, nr > 1);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < GT_IMAX; ++i) {
@@ -213,14 +277,18 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
       // buffer (i + 1) % 2 was last read in iteration i - 1; after the
       // round's last iteration the store lands in a buffer nothing reads
       astore(ra, (i + 1) & 1);
-      if (i + 2 < GT_IMAX) aload(ra, base + i + 2, static_cast<uint32_t>(i + 2) < nr);
+      mstore(mr, (i + 1) & 1, base + i + 1);
+      if (i + 2 < GT_IMAX) {
+        aload(ra, base + i + 2, static_cast<uint32_t>(i + 2) < nr);
+        mload(mr, base + i + 2, static_cast<uint32_t>(i + 2) < nr);
+      }
       __syncthreads();
     }
   }
 
   // ---- K groups meet in LDS (the activation buffers are free now)
   float* red = reinterpret_cast<float*>(smem);
-  static_assert((KQ - 1) * CG * MT * 16 * 64 * 4 <= thin_lds_bytes<CG, KC, MT>(), "the K-group partials fit the LDS");
+  static_assert((KQ - 1) * CG * MT * 16 * 64 * 4 <= thin_lds_bytes<CG, KC, MT, STG>(), "the K-group partials fit the LDS");
   if (kq > 0) {
 #pragma unroll
     for (int r = 0; r < MT; ++r)
@@ -352,7 +420,7 @@ inline int64_t thin_ws_bytes(const Launch& L) {
 template <int ZPK, int SPC, int MT>
 inline hipError_t launch_thin3(const Launch& L, hipStream_t st) {
   auto kern = k_gemm_thin<ZPK, SPC, kThinCG, kThinKC, MT>;
-  constexpr int lds = thin_lds_bytes<kThinCG, kThinKC, MT>();
+  constexpr int lds = thin_lds_bytes<kThinCG, kThinKC, MT, ZPK != ZP_FLOAT>();
   if (lds > 64 * 1024) {
     static std::atomic<int> done[kMaxDevices];
     const hipError_t e = raise_lds_cap(reinterpret_cast<const void*>(kern), lds, done);
