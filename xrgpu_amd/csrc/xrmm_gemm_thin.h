@@ -6,7 +6,8 @@
 // Work split. A workgroup owns NT = 32 CG output columns and one K split
 // (grid = column tiles x splits). Its eight waves are CG column groups of 32
 // columns times KQ = 8 / CG K groups; K advances in chunks of KC, and in
-// iteration i K group q takes chunk c0 + KQ i + q of the split, so the
+// iteration i K group q takes chunk c0 + KQ i + q of the split (the
+// iterations in a rotated order per workgroup, see cfirst), so the
 // workgroup stages KQ consecutive chunks of the activations per iteration
 // (double-buffered) and each wave multiplies all rows (two 32-row MFMA
 // tiles) by its 32 columns.
@@ -98,6 +99,17 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
   const uint32_t nchunk = rowb / 16;
   const uint32_t c0 = sp * t.cps;
   const uint32_t c1 = c0 + t.cps < t.nkc ? c0 + t.cps : t.nkc;
+  // First chunk of loop iteration i. The workgroups of one split (about
+  // one XCD's share, all wanting the same activations) walk its iterations
+  // from different starting points, so each activation chunk is fetched from
+  // memory by one of them and found in the L2 by the others, instead of every
+  // workgroup missing on the same chunk at the same time.
+  const uint32_t rot = t.ni > 1 ? tile % t.ni : 0u;
+  auto cfirst = [&](uint32_t i) {
+    uint32_t ii = i + rot;
+    ii = ii >= t.ni ? ii - t.ni : ii;
+    return c0 + KQ * ii;
+  };
 
   // ---- this lane's weight column
   const uint32_t n0 = tile * NT;
@@ -120,7 +132,7 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
   // false turns the loads into zero reads instead of branching around them
   // (a branch around a load makes every later wait a full drain)
   auto wload = [&](WRegs& r, uint32_t i, bool live) {
-    const uint32_t c = c0 + KQ * i + static_cast<uint32_t>(kq);
+    const uint32_t c = cfirst(i) + static_cast<uint32_t>(kq);
     const bool cv = live & (c < c1);
 #pragma unroll
     for (int j = 0; j < PJ; ++j) {
@@ -148,8 +160,8 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
   // pieces per thread (rows past M and k past K read zero)
   const rsrc_t rA = mk_rsrc(L.A, M * K * 2u);
   // first block of iteration i's chunks, and how many blocks they span
-  auto blk0 = [&](uint32_t i) { return ((c0 + KQ * i) * KC) >> L.bs_log2; };
-  auto nblk = [&](uint32_t i) { return ((((c0 + KQ * i + KQ) * KC) - 1u) >> L.bs_log2) - blk0(i) + 1u; };
+  auto blk0 = [&](uint32_t i) { return (cfirst(i) * KC) >> L.bs_log2; };
+  auto nblk = [&](uint32_t i) { return ((((cfirst(i) + KQ) * KC) - 1u) >> L.bs_log2) - blk0(i) + 1u; };
   struct MRegs {
     uint32_t s[STG ? MPT : 1], z[STG ? MPT : 1];
   };
@@ -158,7 +170,7 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
   auto mload = [&](MRegs& mr, uint32_t i, bool live) {
     if constexpr (STG) {
       const uint32_t b0 = blk0(i), nb = nblk(i);
-      const bool it = live & (c0 + KQ * i < c1);
+      const bool it = live & (cfirst(i) < c1);
 #pragma unroll
       for (int x = 0; x < MPT; ++x) {
         const uint32_t e = static_cast<uint32_t>(tid + GT_T * x), col = n0 + e / MS, sl = e % MS, b = b0 + sl;
@@ -186,7 +198,7 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
     for (int e = 0; e < APT; ++e) {
       const int p = tid + GT_T * e;
       const int q = p / (ROWS * GPR), rem = p % (ROWS * GPR), row = rem / GPR, grp = rem % GPR;
-      const uint32_t c = c0 + KQ * i + static_cast<uint32_t>(q);
+      const uint32_t c = cfirst(i) + static_cast<uint32_t>(q);
       const uint32_t k = c * KC + static_cast<uint32_t>(grp) * 8u;
       const bool ok = live & (c < c1) & (static_cast<uint32_t>(row) < M) & (k < K);  // K % 8 == 0
       ra[e] = bld16(rA, ok ? (static_cast<uint32_t>(row) * K + k) * 2u : OOB, 0);
@@ -209,7 +221,7 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
 
   // one iteration's MFMAs on buffer `buf` with the weights of `r`
   auto compute = [&](const WRegs& r, int buf, uint32_t i) {
-    const uint32_t c = c0 + KQ * i + static_cast<uint32_t>(kq);
+    const uint32_t c = cfirst(i) + static_cast<uint32_t>(kq);
     const f16* As = lds + buf * BUF + kq * CH + (lane & 31) * LD + g * 32;
     const unsigned char* ms = mlds + buf * META + (32u * cg + static_cast<uint32_t>(lane & 31)) * MS * 2u;
     const unsigned char* mz = mlds + buf * META + NT * MS * 2 + (32u * cg + static_cast<uint32_t>(lane & 31)) * MS;
