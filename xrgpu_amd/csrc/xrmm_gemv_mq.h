@@ -2,9 +2,10 @@
 // zero points): the Qkv decode shape (four rows, RMS prologue) and
 // MatMulNBits with three or four rows.
 //
-// Work split. A workgroup owns one tile of 16 output columns; its W waves
-// split K: wave w takes chunks [w*4J, (w+1)*4J) of every column (a chunk is 16
-// bytes = 32 codes of one column). Lane l = 16 g + n loads chunk w*4J + 4j + g
+// Work split. A workgroup owns one or two tiles of 16 output columns (TT);
+// its W waves split K: wave w takes chunks [w*4J, (w+1)*4J) of every column
+// (a chunk is 16 bytes = 32 codes of one column), and one staging of its K
+// slice of the activations serves every tile. Lane l = 16 g + n loads chunk w*4J + 4j + g
 // of column n for j = 0..J-1, so one load instruction reads 64 contiguous
 // bytes of each of 16 columns. Every weight load of a wave is issued before
 // its activation staging, so the whole stream is in flight from the start.
@@ -108,8 +109,9 @@ __host__ __device__ constexpr uint32_t mq_slice_bytes() {
   return 4 * mq_row_stride<J>() + 16;
 }
 
-template <int ZPK, int J, int W, int OPK, bool SK>
+template <int ZPK, int J, int W, int OPK, bool SK, int TT>
 __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
+  static_assert(TT == 1 || TT == 2, "one or two 16-column tiles per workgroup");
   static_assert(ZPK == ZP_NONE || ZPK == ZP_PACKED, "integer zero points");
   static_assert(OPK == OP_MATMUL || OPK == OP_QKV, "operator");
   constexpr bool QKV = OPK == OP_QKV;
@@ -121,10 +123,10 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
   // stride, so the 16 columns' writes spread over the banks and an output
   // thread reads its 4 W values as 16-byte pieces
   constexpr int PST = ((4 * W + 3) / 4) * 4 + 4;
-  __shared__ __align__(16) float part[4][16][PST];
+  __shared__ __align__(16) float part[TT][4][16][PST];
   __shared__ float red[QKV ? W : 1][4][4];  // per wave, row and 16-lane row of the wave
-  __shared__ __align__(16) unsigned char meta_s[MQ_META_LOADS * W * 64 * 16 + 16 * 16];
-  __shared__ __align__(16) unsigned char meta_z[ZPK == ZP_PACKED ? MQ_META_LOADS * W * 64 * 16 + 16 * 16 : 16];
+  __shared__ __align__(16) unsigned char meta_s[MQ_META_LOADS * W * 64 * 16 + 16 * 16 * TT];
+  __shared__ __align__(16) unsigned char meta_z[ZPK == ZP_PACKED ? MQ_META_LOADS * W * 64 * 16 + 16 * 16 * TT : 16];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -141,9 +143,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
   const uint32_t t0 = pick(a.p[0].t0, a.p[1].t0, a.p[2].t0);
   const uint32_t K = a.K, rowb = a.rowb, nchunk = a.nchunk;
   const int M = static_cast<int>(a.M);
-  const uint32_t col0 = (tile - t0) * 16u;
-  const uint32_t col = col0 + n;
-  const uint32_t colc = col < N ? col : N - 1;  // loads clamp, stores check
+  const uint32_t col0 = (tile - t0) * 16u * TT;
   const uint32_t ch0 = wave * CPW;              // first chunk of this wave
 
   // ---- this wave's activation slice first (the staging waits for it, and
@@ -154,7 +154,8 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
   const rsrc_t rK = mk_rsrc(a.skip, SK ? static_cast<uint32_t>(M) * K * 2u : 0u);
   const rsrc_t rG = mk_rsrc(a.gamma, QKV ? K * 2u : 0u);
   const uint32_t k0 = ch0 * 32u;
-  u32x4 ar[J], sk[SK ? J : 1], gm[QKV ? J : 1];
+  // gamma depends on the piece's k only, the same for every row: one load
+  u32x4 ar[J], sk[SK ? J : 1], gm[1];
 #pragma unroll
   for (int q = 0; q < J; ++q) {
     const uint32_t idx = q * 64u + lane, r = idx / (16u * J), pc = idx % (16u * J);
@@ -163,7 +164,9 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
     const uint32_t off = ok ? (r * K + k) * 2u : kOOB;
     ar[q] = bld16(rA, off, 0);
     if constexpr (SK) sk[q] = bld16(rK, off, 0);
-    if constexpr (QKV) gm[q] = bld16(rG, k < K ? k * 2u : kOOB, 0);
+    if constexpr (QKV) {
+      if (q == 0) gm[0] = bld16(rG, k < K ? k * 2u : kOOB, 0);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
   // start at the dword boundary at or below the tile's bytes: the range check
   // zeroes a whole dword that straddles the bound. (Scale blocks start
   // dword-aligned: 16 columns of whole fp16 rows.)
-  const uint32_t ncols = N - col0 < 16u ? N - col0 : 16u;
+  const uint32_t ncols = N - col0 < 16u * TT ? N - col0 : 16u * TT;
   const uint32_t sb0 = col0 * a.kb * 2u, sbytes = ncols * a.kb * 2u;
   const uint32_t zb0 = col0 * a.zrow, zbytes = ZPK == ZP_PACKED ? ncols * a.zrow : 0u;
   const uint32_t zdel = zb0 & 3u;
@@ -192,11 +195,16 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
   // (the column offset differs per lane, so it goes into the vector offset:
   // a per-lane scalar offset would serialise the load over the columns)
   const rsrc_t rB = mk_rsrc(Bp, N * rowb);
-  u32x4 wv[J];
+  u32x4 wv[TT][J];
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const uint32_t ch = ch0 + 4u * j + g;
-    wv[j] = bld16_nt(rB, ch < nchunk ? colc * rowb + ch * 16u : kOOB, 0);
+  for (int tt = 0; tt < TT; ++tt) {
+    const uint32_t col = col0 + 16u * tt + n;
+    const uint32_t colc = col < N ? col : N - 1;  // loads clamp, stores check
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t ch = ch0 + 4u * j + g;
+      wv[tt][j] = bld16_nt(rB, ch < nchunk ? colc * rowb + ch * 16u : kOOB, 0);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -230,22 +238,45 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
     float mx = 0.f;
     f16* res = static_cast<f16*>(a.residual);
     const bool write_res = res != nullptr && tile == 0;
+    // without skip r = A, and u = A * gamma is one packed binary16 multiply
+    // per pair (the product of two binary16 values rounded once, as the
+    // float32 product rounded to binary16 would be); the sum of squares takes
+    // v_dot2_f32_f16 (exact products, float32 sums) and the range check works
+    // on the binary16 bit patterns (|u| > 32768 exactly when the magnitude
+    // bits exceed 0x7800)
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 big = {0, 0};
 #pragma unroll
     for (int q = 0; q < J; ++q) {
       const uint32_t idx = q * 64u + lane, r = idx / (16u * J), pc = idx % (16u * J);
       const f16x8 av = __builtin_bit_cast(f16x8, ar[q]);
       const f16x8 sv = __builtin_bit_cast(f16x8, sk[SK ? q : 0]);
-      const f16x8 gv = __builtin_bit_cast(f16x8, gm[q]);
+      const f16x8 gv = __builtin_bit_cast(f16x8, gm[0]);
       f16x8 u, rv;
       float s2 = 0.f;
+      if constexpr (SK) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float rf = SK ? __fadd_rn(static_cast<float>(av[e]), static_cast<float>(sv[e])) : static_cast<float>(av[e]);
-        const float uf = rf * static_cast<float>(gv[e]);
-        s2 = __builtin_fmaf(rf, rf, s2);
-        mx = __builtin_fmaxf(mx, __builtin_fabsf(uf));
-        u[e] = static_cast<f16>(uf);
-        rv[e] = static_cast<f16>(rf);
+        for (int e = 0; e < 8; ++e) {
+          const float rf = __fadd_rn(static_cast<float>(av[e]), static_cast<float>(sv[e]));
+          const float uf = rf * static_cast<float>(gv[e]);
+          s2 = __builtin_fmaf(rf, rf, s2);
+          mx = __builtin_fmaxf(mx, __builtin_fabsf(uf));
+          u[e] = static_cast<f16>(uf);
+          rv[e] = static_cast<f16>(rf);
+        }
+      } else {
+        float s2b = 0.f;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const f16x2 a2 = h2(ar[q][d]), g2 = h2(gm[0][d]);
+          const f16x2 u2 = a2 * g2;
+          u[2 * d] = u2[0];
+          u[2 * d + 1] = u2[1];
+          if (d & 1) s2b = __builtin_amdgcn_fdot2(a2, a2, s2b, false);
+          else s2 = __builtin_amdgcn_fdot2(a2, a2, s2, false);
+          big = __builtin_elementwise_max(big, __builtin_bit_cast(u16x2, as_u32(u2) & 0x7FFF7FFFu));
+        }
+        s2 += s2b;
       }
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) sq[rr] += r == static_cast<uint32_t>(rr) ? s2 : 0.f;
@@ -264,6 +295,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
     // Rescale only when some |u| exceeds 32768 (a ballot; the wave-wide
     // maximum is taken only then). NaN compares false: a NaN row stays NaN
     // through the unscaled path.
+    if (!SK) mx = (big[0] > 0x7800 || big[1] > 0x7800) ? 65536.f : 0.f;  // only the comparison below uses it
     if (__builtin_amdgcn_ballot_w64(mx > 32768.f) != 0) {
       const float wmx = mq_wave_max(mx);
       int e = 0;
@@ -275,7 +307,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
         const uint32_t idx = q * 64u + lane, r = idx / (16u * J), pc = idx % (16u * J);
         const f16x8 av = __builtin_bit_cast(f16x8, ar[q]);
         const f16x8 sv = __builtin_bit_cast(f16x8, sk[SK ? q : 0]);
-        const f16x8 gv = __builtin_bit_cast(f16x8, gm[q]);
+        const f16x8 gv = __builtin_bit_cast(f16x8, gm[0]);
         f16x8 u;
 #pragma unroll
         for (int e2 = 0; e2 < 8; ++e2) {
@@ -309,29 +341,34 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       aop[j][t] = *reinterpret_cast<const u32x4*>(diag ? slice + r_of * ROWB + (4u * j + g) * 64u + 16u * t : zero);
-  uint32_t sraw[J], zraw[J];
+  uint32_t sraw[TT][J], zraw[TT][J];
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const uint32_t ch = ch0 + 4u * j + g;
-    const uint32_t b = ((ch < nchunk ? ch : nchunk - 1u) * 32u) >> a.bsl;
-    const uint32_t nn = col < N ? n : 0u;
-    sraw[j] = *reinterpret_cast<const uint16_t*>(meta_s + mq_pad((nn * a.kb + b) * 2u, a.sshift));
-    zraw[j] = ZPK == ZP_PACKED ? meta_z[mq_pad(zdel + nn * a.zrow + (b >> 1), a.zshift)] >> ((b & 1u) * 4u) : 8u;
-  }
+  for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t ch = ch0 + 4u * j + g;
+      const uint32_t b = ((ch < nchunk ? ch : nchunk - 1u) * 32u) >> a.bsl;
+      const uint32_t nn = col0 + 16u * tt + n < N ? 16u * tt + n : 0u;
+      sraw[tt][j] = *reinterpret_cast<const uint16_t*>(meta_s + mq_pad((nn * a.kb + b) * 2u, a.sshift));
+      zraw[tt][j] = ZPK == ZP_PACKED ? meta_z[mq_pad(zdel + nn * a.zrow + (b >> 1), a.zshift)] >> ((b & 1u) * 4u) : 8u;
+    }
   const f16x2 k1024 = {static_cast<f16>(1024.f), static_cast<f16>(1024.f)};
   const f16x2 k64 = {static_cast<f16>(64.f), static_cast<f16>(64.f)};
   const f16x2 inv16 = {static_cast<f16>(0.0625f), static_cast<f16>(0.0625f)};
+  f32x4 yt[TT];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
   f32x4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const f16 zf = static_cast<f16>(static_cast<float>(zraw[j] & 15u));
+    const f16 zf = static_cast<f16>(static_cast<float>(zraw[tt][j] & 15u));
     const f16x2 zz = {zf, zf};
     const f16x2 nlo = -(k1024 + zz), nhi = -(k64 + zz);  // exact: small integers
     f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const u32x4 av = aop[j][t];
-      const uint32_t x = wv[j][t], x8 = x >> 8;
+      const uint32_t x = wv[tt][j][t], x8 = x >> 8;
       const uint32_t magic = 0x64006400u;
       const f16x2 w0 = h2(and_or(x, 0x000F000Fu, magic)) + nlo;                                  // c0, c4
       const f16x2 w1 = __builtin_elementwise_fma(h2(and_or(x, 0x00F000F0u, magic)), inv16, nhi);  // c1, c5
@@ -340,23 +377,28 @@ __global__ __launch_bounds__(W * 64) void k_gemv_mq(MqArgs a) {
       const f16x8 b = {w0[0], w0[1], w1[0], w1[1], w2[0], w2[1], w3[0], w3[1]};
       d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av), b, d, 0, 0, 0);
     }
-    const float s = static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(sraw[j])));
+    const float s = static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(sraw[tt][j])));
 #pragma unroll
     for (int i = 0; i < 4; ++i) y[i] = __builtin_fmaf(s, d[i], y[i]);
+  }
+  yt[tt] = y;
   }
 
   // ---- the four k-group lanes of a column, then the waves
 #pragma unroll
-  for (int i = 0; i < 4; ++i) part[i][n][wave * 4 + g] = y[i] * escale;
+  for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[tt][i][n][wave * 4 + g] = yt[tt][i] * escale;
   __syncthreads();
-  if (tid < 64) {
-    const uint32_t i = static_cast<uint32_t>(tid) >> 4, nn = static_cast<uint32_t>(tid) & 15u;
-    const uint32_t c = col0 + nn;
+  if (tid < 64 * TT) {
+    const uint32_t tt = static_cast<uint32_t>(tid) >> 6;
+    const uint32_t i = (static_cast<uint32_t>(tid) >> 4) & 3u, nn = static_cast<uint32_t>(tid) & 15u;
+    const uint32_t c = col0 + 16u * tt + nn;
     if (static_cast<int>(i) < M && c < N) {
       float t4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int w = 0; w < W; ++w) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(&part[i][nn][w * 4]);
+        const f32x4 v = *reinterpret_cast<const f32x4*>(&part[tt][i][nn][w * 4]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) t4[q] += v[q];
       }
@@ -391,12 +433,28 @@ inline int mq_j(const Launch& L) {
 // points, a row of at most 8 x 16 chunks (K up to 4096 at 4 bits).
 inline bool mq_fits(const Launch& L) {
   if (L.M < 1 || L.M > 4 || L.block_size < 32 || L.zp_kind == ZP_FLOAT) return false;
-  if (16 * L.kb * 2 > int64_t(MQ_META_LOADS) * kMqWaves * 64 * 16) return false;  // the tile's scales in one pass
+  if (16 * L.kb * 2 > int64_t(MQ_META_LOADS) * kMqWaves * 64 * 16) return false;  // a tile's scales in one pass
   if (L.op != OP_MATMUL && !(L.op == OP_QKV && L.gamma)) return false;
   return mq_j(L) != 0;
 }
 
-template <int ZPK, int J, int OPK, bool SK>
+// Tiles per workgroup: two when the one-tile grid has more workgroups than
+// the device has CUs and two tiles' scales still fit one staging pass. A
+// workgroup stages its K slices of the activations once for all its tiles,
+// so pairing halves that work and the activation reads per column, and a
+// grid of at most one workgroup per CU leaves no CU with twice the work of
+// another (the Qkv GQA decode geometry: 384 one-tile workgroups on 256 CUs,
+// or 192 two-tile ones).
+int device_cus();
+inline int mq_tt(const Launch& L) {
+  int64_t tiles = 0;
+  for (int i = 0; i < L.nproj; ++i) tiles += (L.p[i].N + 15) / 16;
+  const int cus = device_cus() > 0 ? device_cus() : 256;
+  const bool fits2 = 32 * L.kb * 2 <= int64_t(MQ_META_LOADS) * kMqWaves * 64 * 16;
+  return (tiles > cus && fits2) ? 2 : 1;
+}
+
+template <int ZPK, int J, int OPK, bool SK, int TT>
 inline hipError_t launch_mq4(const Launch& L, hipStream_t st) {
   MqArgs a{};
   a.A = L.A;
@@ -411,7 +469,7 @@ inline hipError_t launch_mq4(const Launch& L, hipStream_t st) {
     const Proj& P = L.p[used ? i : 0];
     a.p[i] = MqProj{P.B, P.scales, static_cast<const uint8_t*>(P.zp), P.Y, static_cast<uint32_t>(P.N),
                     used ? tiles : 0xFFFFFFFFu};
-    if (used) tiles += static_cast<uint32_t>((P.N + 15) / 16);
+    if (used) tiles += static_cast<uint32_t>((P.N + 16 * TT - 1) / (16 * TT));
   }
   a.K = static_cast<uint32_t>(L.K);
   a.kb = static_cast<uint32_t>(L.kb);
@@ -431,16 +489,21 @@ inline hipError_t launch_mq4(const Launch& L, hipStream_t st) {
   };
   a.sshift = pow2_shift(L.kb * 2);
   a.zshift = ZPK == ZP_PACKED ? pow2_shift(L.zrow) : 0u;
-  hipLaunchKernelGGL((k_gemv_mq<ZPK, J, kMqWaves, OPK, SK>), dim3(tiles), dim3(kMqWaves * 64), 0, st, a);
+  hipLaunchKernelGGL((k_gemv_mq<ZPK, J, kMqWaves, OPK, SK, TT>), dim3(tiles), dim3(kMqWaves * 64), 0, st, a);
   return hipGetLastError();
+}
+
+template <int ZPK, int J, int OPK, int TT>
+inline hipError_t launch_mq3t(const Launch& L, hipStream_t st) {
+  if constexpr (OPK == OP_QKV)
+    return L.skip ? launch_mq4<ZPK, J, OPK, true, TT>(L, st) : launch_mq4<ZPK, J, OPK, false, TT>(L, st);
+  else
+    return launch_mq4<ZPK, J, OPK, false, TT>(L, st);
 }
 
 template <int ZPK, int J, int OPK>
 inline hipError_t launch_mq3(const Launch& L, hipStream_t st) {
-  if constexpr (OPK == OP_QKV)
-    return L.skip ? launch_mq4<ZPK, J, OPK, true>(L, st) : launch_mq4<ZPK, J, OPK, false>(L, st);
-  else
-    return launch_mq4<ZPK, J, OPK, false>(L, st);
+  return mq_tt(L) == 2 ? launch_mq3t<ZPK, J, OPK, 2>(L, st) : launch_mq3t<ZPK, J, OPK, 1>(L, st);
 }
 
 template <int ZPK, int OPK>
