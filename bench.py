@@ -31,7 +31,7 @@ PROFILES = os.path.join(ROOT, "profiles")
 SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048": 4, "qmoe_mixtral_t1": 6,
          "bnb4_nf4_m1": 7, "gbq_embed_t2048": 8, "int8a_decode_m1": 1, "f32_k2048_m1": 0,
          "mlp_prefill_m64": 9, "prefill_m2048_prepacked": 4, "down_proj_m64": 10, "mlp_prefill_m2048": 13,
-         "qkv_prefill_m2048": 14, "q8_f32_decode_m1": 15, "f32_prefill_m64": 16}
+         "qkv_prefill_m2048": 14, "q8_f32_decode_m1": 15, "f32_prefill_m64": 16, "qmoe_prefill_t256": 17}
 # The CPU-oracle workload on the GPU: MatMulNBits float32, M=1, K=N=2048,
 # block_size 32, packed zero points (2,703,360 algorithmic bytes per call)
 F32 = dict(M=1, K=2048, N=2048, bs=32)
@@ -62,6 +62,10 @@ GBQ = dict(rows=128256, width=4096, bs=32, n=2048)
 # com.microsoft.QMoE decode, Mixtral-8x7B expert geometry: T=1, H=4096, I=14336,
 # E=8, k=2, 4-bit codes, float32 scales per block of 64, interleaved SwiGLU
 QMOE = dict(T=1, H=4096, I=14336, E=8, k=2, bits=4, bs=64)
+# com.microsoft.QMoE prefill, the same expert geometry for 256 tokens with
+# float32 scales per row (block_size 0): the grouped-expert GEMMs,
+# 2 * T * k * 3 * H * I flops per call
+QMOE_PF = dict(T=256, H=4096, I=14336, E=8, k=2, bits=4, bs=0)
 
 
 def qmoe_algorithmic_bytes(T=1, H=4096, I=14336, k=2, bits=4, bs=64, **_):
@@ -141,6 +145,18 @@ def make_replicas(torch, name, R, dev, seed):
                 fc2=torch.randint(0, 256, (E, H, I * bits // 8), dtype=torch.uint8, device=dev, generator=g),
                 s2=torch.rand((E, H, I // bs), device=dev, generator=g) * 0.019 + 0.001))
         return dict(A=x, routers=routers, reps=reps)
+    if name == "qmoe_prefill_t256":
+        q = QMOE_PF
+        T, H, I, E = q["T"], q["H"], q["I"], q["E"]
+        x = torch.randn((T, H), device=dev, generator=g) * 0.5
+        router = torch.randn((T, E), device=dev, generator=g)
+        for _ in range(R):
+            reps.append(dict(
+                fc1=torch.randint(0, 256, (E, 2 * I, H // 2), dtype=torch.uint8, device=dev, generator=g),
+                s1=torch.rand((E, 2 * I), device=dev, generator=g) * 0.019 + 0.001,
+                fc2=torch.randint(0, 256, (E, H, I // 2), dtype=torch.uint8, device=dev, generator=g),
+                s2=torch.rand((E, H), device=dev, generator=g) * 0.019 + 0.001))
+        return dict(A=x, router=router, reps=reps)
     if name == "bnb4_nf4_m1":
         q = BNB4
         A = torch.randn((q["M"], q["K"]), device=dev, generator=g).half()
@@ -317,6 +333,15 @@ def step_fn(ops, name, w):
             return ops.qmoe(A, routers[i % len(routers)], r["fc1"], r["s1"], r["fc2"], r["s2"], k=q["k"],
                             activation="swiglu", swiglu_fusion=1, expert_weight_bits=q["bits"], block_size=q["bs"],
                             workspace=ws)
+        return f
+    if name == "qmoe_prefill_t256":
+        q = QMOE_PF
+        ws = torch.empty(ops.qmoe_workspace_bytes(q["T"], q["k"], q["H"], q["I"]), dtype=torch.uint8, device=A.device)
+
+        def f(i):
+            r = reps[i % len(reps)]
+            return ops.qmoe(A, w["router"], r["fc1"], r["s1"], r["fc2"], r["s2"], k=q["k"], activation="swiglu",
+                            swiglu_fusion=1, expert_weight_bits=q["bits"], block_size=q["bs"], workspace=ws)
         return f
     if name == "int8a_decode_m1":
         Y = torch.empty((1, w["N"]), dtype=torch.float16, device=A.device)
@@ -629,7 +654,7 @@ def main():
     names = ["decode_up_m1", "prefill_m2048", "prefill_m2048_prepacked", "qkv_gqa_m4", "mlp_swiglu_m16",
              "mlp_prefill_m64", "down_proj_m64", "mlp_prefill_m2048", "qkv_prefill_m2048", "f32_k2048_m1",
              "q8_f32_decode_m1", "f32_prefill_m64",
-             "qmoe_mixtral_t1", "bnb4_nf4_m1", "gbq_embed_t2048", "int8a_decode_m1"]
+             "qmoe_mixtral_t1", "qmoe_prefill_t256", "bnb4_nf4_m1", "gbq_embed_t2048", "int8a_decode_m1"]
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
     for name in names:
@@ -637,12 +662,12 @@ def main():
         # holds (Qkv: 24 x 13.7 MB = 328 MB)
         # (prefill legs: 8 replicas, 8 x 30-66 MB of weights and scales)
         R = {"prefill_m2048": 8, "prefill_m2048_prepacked": 8, "mlp_prefill_m2048": 8, "qkv_prefill_m2048": 24,
-             "qmoe_mixtral_t1": 2, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24,
+             "qmoe_mixtral_t1": 2, "qmoe_prefill_t256": 1, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24,
              "f32_k2048_m1": 100, "mlp_prefill_m64": 24, "down_proj_m64": 12, "q8_f32_decode_m1": 24,
              "f32_prefill_m64": 24}.get(name, args.replicas)
         w = make_replicas(torch, name, R, dev, seed=SEEDS[name])
         fn = step_fn(ops, name, w)
-        steps = args.steps if "prefill_m2048" not in name else max(10, args.steps // 10)
+        steps = args.steps if "prefill_m2048" not in name and name != "qmoe_prefill_t256" else max(10, args.steps // 10)
         ms, eager_ms, wall_ms = time_steps(torch, fn, steps, args.warmup)
         p10, p50, p90 = per_launch_percentiles(torch, fn, min(100, steps), 5)
         wl = workloads.make(name, scale_down=1) if name == "decode_up_m1" else None
@@ -809,6 +834,16 @@ def main():
             "us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
             "bytes_per_launch": nbytes, "kernel": ops.qmoe_kernel(q["T"], q["H"], q["E"], 2 * q["I"], q["k"], q["bits"],
                                                                    q["bs"], "swiglu", 1)}
+    if "qmoe_prefill_t256" in results:
+        r, q = results["qmoe_prefill_t256"], QMOE_PF
+        flops = 2 * q["T"] * q["k"] * 3 * q["H"] * q["I"]
+        tf = flops / (r["ms"] * 1e-3) / 1e12
+        out["qmoe_prefill_t256"] = {
+            "workload": "QMoE T=256 H=4096 I=14336 E=8 k=2 bits=4 row scales, interleaved SwiGLU (Mixtral-8x7B experts)",
+            "us": round(r["ms"] * 1e3, 3), "tflops": round(tf, 2), "frac_mfma": round(tf / FP16_PEAK_TFLOPS, 4),
+            "flops_per_launch": flops,
+            "numerics": "float32 activations as two binary16 terms: two fp16 MFMAs per product",
+            "kernel": ops.qmoe_kernel(q["T"], q["H"], q["E"], 2 * q["I"], q["k"], q["bits"], q["bs"], "swiglu", 1)}
     if "bnb4_nf4_m1" in results:
         r, q = results["bnb4_nf4_m1"], BNB4
         nbytes = q["N"] * q["K"] // 2 + q["N"] * q["K"] // q["bs"] * 2 + q["M"] * (q["K"] + q["N"]) * 2

@@ -325,8 +325,13 @@ void xrmm_destroy(xrmm_op* op);
  * XRMM_ACT_RELU (swiglu_fusion 0) or XRMM_ACT_SWIGLU (swiglu_fusion 1: FC1
  * rows 2j / 2j+1 are gate / linear, I = F1/2). `workspace` is device memory of
  * at least xrmm_qmoe_workspace_bytes(T, k, H, I) bytes (routing table, the
- * activated FC1 outputs, per-slot FC2 partials and their arrival counters);
- * calls that share a workspace must not overlap. */
+ * activated FC1 outputs, per-slot FC2 partials and their arrival counters or
+ * per-expert pair lists); calls that share a workspace must not overlap.
+ * With 4-bit codes, row scales, H and I multiples of 64, at most 4096 experts
+ * and at least 32 (token, slot) pairs, the pairs are grouped by expert and
+ * each expert's FC1 and FC2 run as one MFMA GEMM over its pairs
+ * ("qmoe_grouped"); other geometries run one pass per pair ("qmoe_rows") or
+ * the scalar path. */
 int64_t xrmm_qmoe_workspace_bytes(int64_t tokens, int32_t k, int64_t hidden, int64_t inter);
 int xrmm_qmoe(const void* input, const void* router, const void* fc1, const void* fc1_scales, const void* fc2,
               const void* fc2_scales, void* output, void* workspace, int64_t workspace_bytes, int64_t tokens,
@@ -334,8 +339,9 @@ int xrmm_qmoe(const void* input, const void* router, const void* fc1, const void
               int32_t activation, int32_t swiglu_fusion, float alpha, float beta, float swiglu_limit,
               int32_t has_limit, void* stream);
 
-/* Name of the kernel family xrmm_qmoe dispatches a geometry to ("qmoe_rows"
- * or "qmoe_scalar"), NULL for an invalid geometry. No device work. */
+/* Name of the kernel family xrmm_qmoe dispatches a geometry to
+ * ("qmoe_grouped", "qmoe_rows" or "qmoe_scalar"), NULL for an invalid
+ * geometry. No device work. */
 const char* xrmm_qmoe_kernel(int64_t tokens, int64_t hidden, int64_t experts, int64_t fc1_rows, int32_t k, int32_t bits,
                              int32_t block_size, int32_t activation, int32_t swiglu_fusion);
 

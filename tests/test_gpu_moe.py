@@ -156,3 +156,48 @@ def test_invalid_geometry_raises(gpu):
         run_gpu(i, at)
     with pytest.raises(nat.XrmmInvalid, match="SwiGLU fusion"):
         run_gpu(i, dict(at, k=1, swiglu_fusion=1))
+
+
+GROUPED = [
+    # T, H, I, E, k, activation, limit, x scale: the grouped-expert GEMMs
+    # (4-bit codes, row scales, at least 32 (token, slot) pairs)
+    (48, 1024, 1024, 8, 2, "swiglu", None, 0.2),    # the upstream prefill-band geometry
+    (64, 256, 128, 64, 8, "swiglu", 7.0, 1.0),      # many experts and slots, SwiGLU limit
+    (40, 512, 192, 6, 3, "relu", None, 1.0),        # ReLU, k = 3, a partial column tile (F1 = 192)
+    (33, 256, 320, 5, 1, "swiglu", None, 3e5),      # x far beyond binary16: the row exponent scales it down
+    (96, 128, 64, 16, 4, "swiglu", None, 1e-3),     # small x: scaled up before the binary16 split
+]
+
+
+@pytest.mark.parametrize("T,H,I,E,k,act,limit,xs", GROUPED)
+def test_grouped_experts(gpu, T, H, I, E, k, act, limit, xs):
+    """Float32 bar max|d| <= 1e-5 max|Y_ref| against the oracle, and
+    bitwise-repeatable outputs (the pair lists' order changes no row)."""
+    rng = np.random.default_rng(T * 7 + H + I + E + k)
+    sw = act == "swiglu"
+    i = rand_case(rng, T, H, I, E, 4, 0, sw)
+    i["inputT"] = (i["inputT"] * np.float32(xs / max(float(np.abs(i["inputT"]).max()), 1e-30))).astype(np.float32)
+    at = dict(k=k, activation=act, swiglu_fusion=1 if sw else 0, bits=4, block_size=0, alpha=1.702 if sw else 1.0,
+              beta=1.0 if sw else 0.0, swiglu_limit=limit)
+    assert ops().qmoe_kernel(T, H, E, 2 * I if sw else I, k, 4, 0, act, 1 if sw else 0) == "qmoe_grouped"
+    got = run_gpu(i, at)
+    ok, err, lim = O.tolerance_ok(got, run_oracle(i, at), np.float32)
+    assert ok, f"max|d|={err} > {lim}"
+    assert np.array_equal(got, run_gpu(i, at))
+
+
+def test_grouped_nonfinite_rows(gpu):
+    """+-Inf and NaN activations reach the sums as the reference's float32
+    products do (the binary16 split keeps lo = 0 for them); other tokens are
+    unaffected."""
+    rng = np.random.default_rng(17)
+    T, H, I, E = 48, 256, 128, 4
+    i = rand_case(rng, T, H, I, E, 4, 0, True)
+    i["inputT"][3, 5] = np.inf
+    i["inputT"][7, 0] = np.nan
+    at = dict(k=2, activation="swiglu", swiglu_fusion=1, bits=4, block_size=0, alpha=1.702, beta=1.0, swiglu_limit=None)
+    assert ops().qmoe_kernel(T, H, E, 2 * I, 2, 4, 0, "swiglu", 1) == "qmoe_grouped"
+    got, ref = run_gpu(i, at), run_oracle(i, at)
+    assert not np.isfinite(ref[3]).all() and not np.isfinite(ref[7]).all()
+    ok, err, lim = O.tolerance_ok(got, ref, np.float32)
+    assert ok, f"max|d|={err} > {lim}"

@@ -472,13 +472,13 @@ int xrmm_qmoe(const void* input, const void* router, const void* fc1, const void
 
 const char* xrmm_qmoe_kernel(int64_t tokens, int64_t hidden, int64_t experts, int64_t fc1_rows, int32_t k, int32_t bits,
                              int32_t block_size, int32_t activation, int32_t swiglu_fusion) {
-  xrmm::MoeArgs a;
+  xrmm::MoeArgs a{};
   if (qmoe_geometry(a, tokens, hidden, experts, fc1_rows, k, bits, block_size, activation, swiglu_fusion)) return nullptr;
   // pointers of 16-byte aligned allocations: the choice then depends on the geometry only
   static const uint8_t probe[16] __attribute__((aligned(16))) = {};
   a.x = reinterpret_cast<const float*>(probe);
   a.fc1 = a.fc2 = probe;
-  a.h = reinterpret_cast<float*>(const_cast<uint8_t*>(probe));
+  a.h = a.yp = reinterpret_cast<float*>(const_cast<uint8_t*>(probe));
   return xrmm::moe_kernel_name(a);
 }
 

@@ -22,7 +22,7 @@ struct MoeArgs {
   float* wts;            // workspace [T, k]: their softmax weights
   float* h;              // workspace [T, k, I]: activated FC1 outputs
   float* yp;             // workspace [T, k, ks, H]: FC2 partial outputs per slot and segment
-  uint32_t* cnt;         // workspace [T, moe_tiles2(H)]: FC2 arrival counters
+  uint32_t* cnt;         // workspace: FC2 arrival counters [T, moe_tiles2(H)] or the grouped path's lists
   int64_t T, H, E, F1, I;
   int k, bits, bs, act;
   float alpha, beta, limit;
@@ -47,13 +47,24 @@ inline int64_t moe_fc2_segments_max(int64_t T, int64_t k, int64_t H, int64_t ste
   return ks < 1 ? 1 : ks;
 }
 
+// Most experts the grouped-expert path takes (its per-expert counts live in
+// LDS and its offsets in the workspace).
+constexpr int64_t kMoeGroupMaxExperts = 4096;
+
+// 32-bit words of the grouped path's lists: offsets and row-tile offsets
+// (E + 1 each), the pair list and the per-pair |h| maxima (T k each) and the
+// row exponents of x (T).
+inline int64_t moe_list_words(int64_t T, int64_t k) { return 2 * (kMoeGroupMaxExperts + 1) + 2 * T * k + T; }
+
 // Workspace bytes for T tokens, k slots, hidden width H, intermediate width
 // I: five 256-byte-aligned regions (sel, wts, h, yp, cnt). The segment bound
-// uses 8-bit rows, which have the most steps.
+// uses 8-bit rows, which have the most steps; the last region holds either
+// path's words.
 inline int64_t moe_workspace_bytes(int64_t T, int64_t k, int64_t H, int64_t I) {
   auto al = [](int64_t b) { return (b + 255) / 256 * 256; };
   const int64_t ks = moe_fc2_segments_max(T, k, H, (I + 1023) / 1024);
-  return al(T * k * 4) + al(T * k * 4) + al(T * k * I * 4) + al(T * k * ks * H * 4) + al(T * moe_tiles2(H) * 4);
+  const int64_t words = T * moe_tiles2(H) > moe_list_words(T, k) ? T * moe_tiles2(H) : moe_list_words(T, k);
+  return al(T * k * 4) + al(T * k * 4) + al(T * k * I * 4) + al(T * k * ks * H * 4) + al(words * 4);
 }
 
 bool moe_fast_ok(const MoeArgs& a);

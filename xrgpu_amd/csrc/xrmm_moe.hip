@@ -149,6 +149,12 @@ __device__ __forceinline__ float dword_dot(uint32_t w, const float* x, float acc
   }
 }
 
+}  // namespace
+}  // namespace xrmm
+#include "xrmm_moe_gemm.h"
+namespace xrmm {
+namespace {
+
 __device__ __forceinline__ float bld_f32(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, bld_u32(r, voff, soff));
 }
@@ -598,7 +604,60 @@ bool moe_fast_ok(const MoeArgs& a) {
   return a.T * a.k * ((a.F1 + 31) / 32) < (int64_t(1) << 31) && a.T * a.k * moe_tiles2(a.H) * 1024 < (int64_t(1) << 31);
 }
 
-const char* moe_kernel_name(const MoeArgs& a) { return moe_fast_ok(a) ? "qmoe_rows" : "qmoe_scalar"; }
+// Grouped-expert path (xrmm_moe_gemm.h): 4-bit codes with row scales, K
+// steps of whole 64-element runs, at least XRMM_MOE_GROUP_MIN (token, slot)
+// pairs, and the lists fitting the workspace's counter region.
+#ifndef XRMM_MOE_GROUP_MIN
+#define XRMM_MOE_GROUP_MIN 32
+#endif
+bool moe_grouped_ok(const MoeArgs& a) {
+  if (a.bits != 4 || a.bs != 0 || a.H % 64 != 0 || a.I % 64 != 0 || a.E > kMoeGroupMaxExperts) return false;
+  if (a.T * a.k < XRMM_MOE_GROUP_MIN) return false;
+  if (!aligned16(a.x) || !aligned16(a.fc1) || !aligned16(a.fc2) || !aligned16(a.h) || !aligned16(a.yp)) return false;
+  if (a.act == XRMM_ACT_SWIGLU_CODE && a.F1 != 2 * a.I) return false;
+  const int64_t lim = int64_t(1) << 31;
+  // 32-bit row-tile grid and pair indices (the workspace's last region holds
+  // the lists for up to kMoeGroupMaxExperts experts)
+  return a.F1 * a.H / 2 < lim && a.H * a.I / 2 < lim && a.T * a.k * a.I < lim && a.T * a.k * a.H < lim;
+}
+
+const char* moe_kernel_name(const MoeArgs& a) {
+  return moe_grouped_ok(a) ? "qmoe_grouped" : moe_fast_ok(a) ? "qmoe_rows" : "qmoe_scalar";
+}
+
+namespace {
+hipError_t launch_grouped(const MoeArgs& a, hipStream_t st) {
+  MgLists g;
+  int32_t* base = reinterpret_cast<int32_t*>(a.cnt);
+  g.off = base;
+  g.toff = g.off + (a.E + 1);
+  g.list = g.toff + (a.E + 1);
+  g.hmax = reinterpret_cast<uint32_t*>(g.list + a.T * a.k);
+  g.ex = reinterpret_cast<int32_t*>(g.hmax + a.T * a.k);
+  const int T = static_cast<int>(a.T), npairs = static_cast<int>(a.T * a.k), E = static_cast<int>(a.E);
+  hipLaunchKernelGGL(k_moe_route, dim3(static_cast<uint32_t>((a.T + 3) / 4)), dim3(MOE_T), 0, st, a.router, a.sel, a.wts,
+                     T, E, a.k);
+  hipLaunchKernelGGL(k_moe_xexp, dim3(static_cast<uint32_t>((a.T + 3) / 4)), dim3(256), 0, st, a.x, T, a.H, g.ex);
+  hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(MG_T), 0, st, a.sel, npairs, E, g);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  // row tiles: at most one partial tile per expert beyond the full ones
+  const int64_t rtmax = (a.T * a.k + MG_RT - 1) / MG_RT + a.E;
+  static std::atomic<int> d1[kMaxDevices], d2[kMaxDevices], d3[kMaxDevices];
+  auto k1 = a.act == XRMM_ACT_SWIGLU_CODE ? k_moe_ggemm<MG_FC1_SWIGLU> : k_moe_ggemm<MG_FC1_RELU>;
+  auto k2 = k_moe_ggemm<MG_FC2>;
+  if (hipError_t e = raise_lds_cap(reinterpret_cast<const void*>(k1), static_cast<int>(MG_LDS),
+                                   a.act == XRMM_ACT_SWIGLU_CODE ? d1 : d2);
+      e != hipSuccess)
+    return e;
+  if (hipError_t e = raise_lds_cap(reinterpret_cast<const void*>(k2), static_cast<int>(MG_LDS), d3); e != hipSuccess) return e;
+  const int nct1 = static_cast<int>((a.F1 + MG_CT - 1) / MG_CT), nct2 = static_cast<int>((a.H + MG_CT - 1) / MG_CT);
+  if (rtmax * nct1 > 0x7FFFFFFF || rtmax * nct2 > 0x7FFFFFFF) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k1, dim3(static_cast<uint32_t>(rtmax * nct1)), dim3(MG_T), MG_LDS, st, a, g, nct1);
+  hipLaunchKernelGGL(k2, dim3(static_cast<uint32_t>(rtmax * nct2)), dim3(MG_T), MG_LDS, st, a, g, nct2);
+  hipLaunchKernelGGL(k_moe_combine, dim3(static_cast<uint32_t>((a.T * a.H + 255) / 256)), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+}  // namespace
 
 hipError_t launch_qmoe(const MoeArgs& a, hipStream_t st) {
   if (a.T == 0) return hipSuccess;
@@ -607,6 +666,7 @@ hipError_t launch_qmoe(const MoeArgs& a, hipStream_t st) {
                        a.T * a.H);
     return hipGetLastError();
   }
+  if (moe_grouped_ok(a)) return launch_grouped(a, st);
   if (moe_fast_ok(a)) {  // routing runs inside the FC1 launch
     const int cpc = 128 / a.bits;
     const int sm = a.bs == 0 ? SM_ROW : a.bs >= cpc ? SM_CHUNK : SM_HALF;

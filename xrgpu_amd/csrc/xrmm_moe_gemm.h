@@ -1,0 +1,363 @@
+// Grouped-expert QMoE for many tokens (included by xrmm_moe.hip): instead of
+// one pass over an expert's rows per (token, slot) pair, the pairs routed to
+// each expert are gathered into the rows of one GEMM per expert, so every
+// expert matrix is read once per 64 pairs.
+//
+// Launches (row scales, 4-bit codes):
+//  1. routing (k_moe_route with the row exponents of x, below);
+//  2. k_moe_group: per-expert pair counts, offsets, row-tile offsets and the
+//     pair lists (one workgroup; the order of pairs inside a list does not
+//     change any result, every GEMM row being independent);
+//  3. k_moe_ggemm FC1: rows = an expert's pairs (their tokens' x), columns =
+//     its FC1 rows, K = H; the epilogue applies the row scale, the activation
+//     (SwiGLU rows 2j / 2j + 1 sit in neighbouring lanes) and writes h[pair],
+//     folding each pair's largest |h| into an arrival-order-free atomic max;
+//  4. k_moe_ggemm FC2: rows = the pairs' h, columns = the expert's FC2 rows,
+//     K = I; writes yp[pair] (row scale applied);
+//  5. k_moe_combine: y[t] = sum over slots (ascending expert index) of
+//     w * yp, one fused multiply-add per slot in slot order.
+//
+// Arithmetic. The codes enter v_mfma_f32_32x32x16_f16 as the exact binary16
+// integers code - 8 (no scale), the row scale multiplies the float32 sum. The
+// float32 activations are split into two binary16 terms per element: a row
+// is first scaled by a power of two that puts its largest finite magnitude
+// near 2^14 (exact), then hi = binary16(v) and lo = binary16(v - hi); the
+// MFMA takes hi and lo against the same weights, so each product keeps about
+// 22 bits of the activation, and the power of two is undone on the sum.
+// Non-finite activations keep lo = 0, so +-Inf and NaN reach the sums as the
+// reference's float32 products would.
+#pragma once
+
+namespace xrmm {
+namespace {
+
+constexpr int MG_RT = 64;   // pairs per row tile
+constexpr int MG_CT = 256;  // columns per tile
+constexpr int MG_K = 64;    // K step
+constexpr int MG_LD = MG_K + 8;
+constexpr int MG_T = 512;   // threads: 8 waves, 2 (rows of 32) x 4 (columns of 64)
+constexpr int MG_STAGE = (2 * MG_RT + MG_CT) * MG_LD;  // halfs per stage: A hi, A lo, B
+constexpr size_t MG_LDS = 2 * MG_STAGE * sizeof(_Float16);
+
+// Lists of the grouped path, inside the workspace's counter region.
+struct MgLists {
+  int32_t* off;    // [E + 1] first list entry of each expert
+  int32_t* toff;   // [E + 1] first row tile of each expert
+  int32_t* list;   // [T k] pair indices grouped by expert
+  uint32_t* hmax;  // [T k] bits of the largest finite |h| of each pair
+  int32_t* ex;     // [T] row exponent of x
+};
+
+// Exponent e such that |v| * 2^-e is near 2^14 for the row maximum v
+// (0 for an all-zero row).
+__device__ __forceinline__ int mg_row_exp(float mx) {
+  if (!(mx > 0.f) || !__builtin_isfinite(mx)) return 0;
+  int e = 0;
+  (void)__builtin_frexpf(mx, &e);  // mx = f * 2^e, f in [0.5, 1)
+  return e - 15;
+}
+
+// Row exponents of x: one wave per token, over the row's finite |x|.
+__global__ __launch_bounds__(256) void k_moe_xexp(const float* __restrict__ x, int T, int64_t H, int32_t* __restrict__ ex) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;  // whole waves
+  const float* xr = x + static_cast<int64_t>(t) * H;
+  float m = 0.f;
+  for (int64_t i = lane; i < H; i += 64) {
+    const float v = __builtin_fabsf(xr[i]);
+    if (__builtin_isfinite(v)) m = fmaxf(m, v);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if (lane == 0) ex[t] = mg_row_exp(m);
+}
+
+// Pair counts, offsets and lists; also clears hmax. One workgroup of
+// MG_T threads; E <= kMoeGroupMaxExperts (LDS counters).
+__global__ __launch_bounds__(MG_T) void k_moe_group(const int32_t* __restrict__ sel, int npairs, int E, MgLists g) {
+  __shared__ int cnt[kMoeGroupMaxExperts];
+  __shared__ int part[MG_T];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += MG_T) cnt[e] = 0;
+  __syncthreads();
+  for (int p = tid; p < npairs; p += MG_T) {
+    const int e = min(max(sel[p], 0), E - 1);
+    atomicAdd(&cnt[e], 1);
+    g.hmax[p] = 0u;
+  }
+  __syncthreads();
+  // exclusive scans of the counts and of the row tiles: each thread sums a
+  // run of experts, the runs' totals are scanned in LDS
+  const int per = (E + MG_T - 1) / MG_T, e0 = tid * per;
+  int s = 0, st = 0;
+  for (int e = e0; e < e0 + per && e < E; ++e) {
+    s += cnt[e];
+    st += (cnt[e] + MG_RT - 1) / MG_RT;
+  }
+  part[tid] = s;
+  __syncthreads();
+  for (int d = 1; d < MG_T; d <<= 1) {
+    const int v = tid >= d ? part[tid - d] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  const int sbase = part[tid] - s;
+  __syncthreads();
+  part[tid] = st;
+  __syncthreads();
+  for (int d = 1; d < MG_T; d <<= 1) {
+    const int v = tid >= d ? part[tid - d] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  const int tbase = part[tid] - st;
+  int a = sbase, b = tbase;
+  for (int e = e0; e < e0 + per && e < E; ++e) {
+    g.off[e] = a;
+    g.toff[e] = b;
+    const int c = cnt[e];
+    a += c;
+    b += (c + MG_RT - 1) / MG_RT;
+  }
+  if (tid == MG_T - 1) {
+    g.off[E] = a;  // the last thread's run ends at E
+    g.toff[E] = b;
+  }
+  __syncthreads();
+  // positions: a cursor per expert (the order inside a list is free)
+  for (int e = tid; e < E; e += MG_T) cnt[e] = 0;
+  __syncthreads();
+  for (int p = tid; p < npairs; p += MG_T) {
+    const int e = min(max(sel[p], 0), E - 1);
+    const int pos = atomicAdd(&cnt[e], 1);
+    g.list[g.off[e] + pos] = p;
+  }
+}
+
+enum MgStage { MG_FC1_RELU = 0, MG_FC1_SWIGLU = 1, MG_FC2 = 2 };
+
+// Largest finite |v| over the 32 lanes of a lane half (lanes l, l ^ 1, ... l ^ 16).
+__device__ __forceinline__ float mg_half_max(float v) {
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// One 64-pair x 256-column tile of an expert's matrix.
+template <int ST>
+__global__ __launch_bounds__(MG_T, 1) void k_moe_ggemm(MoeArgs a, MgLists g, int nct) {
+  constexpr bool FC2 = ST == MG_FC2;
+  extern __shared__ __align__(16) unsigned char smem[];
+  f16* lds = reinterpret_cast<f16*>(smem);
+  __shared__ int s_pair[MG_RT];
+  __shared__ float s_rs[MG_RT];  // 2^-e per row (staging)
+  __shared__ float s_ru[MG_RT];  // 2^e per row (epilogue)
+  constexpr uint32_t OOB = 0x80000000u;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  const int E = static_cast<int>(a.E);
+  const int rt = static_cast<int>(blockIdx.x) / nct, ct = static_cast<int>(blockIdx.x) % nct;
+  const int total = g.toff[E];
+  if (rt >= total) return;  // uniform: the grid is an upper bound of the row tiles
+  // expert of this row tile: the last e with toff[e] <= rt
+  int lo = 0, hi = E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (g.toff[mid] <= rt) lo = mid;
+    else hi = mid - 1;
+  }
+  const int e = lo;
+  const int lb = g.off[e] + (rt - g.toff[e]) * MG_RT;  // first list entry of the tile
+  const int nrow = min(MG_RT, g.off[e + 1] - lb);
+  const int Kd = static_cast<int>(FC2 ? a.I : a.H);   // reduction length
+  const int Nd = static_cast<int>(FC2 ? a.H : a.F1);  // rows of the expert matrix
+  const int n0 = ct * MG_CT;
+  if (tid < MG_RT) {
+    const int p = tid < nrow ? g.list[lb + tid] : -1;
+    s_pair[tid] = p;
+    int ex = 0;
+    if (p >= 0) {
+      if constexpr (FC2) ex = mg_row_exp(__builtin_bit_cast(float, g.hmax[p]));
+      else ex = g.ex[p / a.k];
+    }
+    s_rs[tid] = __builtin_ldexpf(1.f, -ex);
+    s_ru[tid] = __builtin_ldexpf(1.f, ex);
+  }
+  __syncthreads();
+
+  // ---- global loads: thread t stages A row t / 8, floats 8 (t % 8) .. + 7 of
+  // the step, and 32 codes (16 bytes) of column t / 2, half t % 2. The rows
+  // belong to different tokens, so A goes through per-lane addresses (a
+  // buffer resource would have to be wave-uniform); rows past the tile's
+  // pairs repeat its first pair and their sums are never written.
+  const int arow = tid >> 3, agrp = tid & 7;
+  const int apair = s_pair[arow] < 0 ? s_pair[0] : s_pair[arow];
+  const float ascale = s_rs[arow];
+  const float* Asrc = FC2 ? a.h : a.x;
+  const float* Arow = Asrc + (FC2 ? static_cast<int64_t>(apair) * a.I : static_cast<int64_t>(apair / a.k) * a.H) + agrp * 8;
+  const int bcol = tid >> 1, bh = tid & 1;
+  const uint32_t rowb = static_cast<uint32_t>(Kd) / 2u;  // bytes per expert row (4-bit codes)
+  const uint8_t* Wb = FC2 ? a.fc2 + static_cast<int64_t>(e) * a.H * rowb : a.fc1 + static_cast<int64_t>(e) * a.F1 * rowb;
+  const rsrc_t rB = mk_rsrc(Wb, static_cast<uint32_t>(Nd) * rowb);
+  const bool bval = n0 + bcol < Nd;
+  const uint32_t boff = bval ? static_cast<uint32_t>(n0 + bcol) * rowb : OOB;
+  const int ksteps = (Kd + MG_K - 1) / MG_K;
+
+  struct Regs {
+    u32x4 a[2];
+    u32x4 b;
+  };
+  // steps past the end reload the last one (never staged)
+  auto gload = [&](Regs& r, int ks) {
+    const bool ok = ks < ksteps;
+    const float* pa = Arow + (ok ? ks : ksteps - 1) * MG_K;
+    r.a[0] = *reinterpret_cast<const u32x4*>(pa);
+    r.a[1] = *reinterpret_cast<const u32x4*>(pa + 4);
+    r.b = bld16(rB, (ok ? boff : OOB) + static_cast<uint32_t>(ks * MG_K / 2 + bh * 16), 0);
+  };
+  // A: scaled, split into binary16 hi / lo in the pair order of the codes;
+  // B: the codes minus 8 as exact binary16 (pair order)
+  auto sstore = [&](const Regs& r, int stage) {
+    f16* Ah = lds + stage * MG_STAGE;
+    f16* Al = Ah + MG_RT * MG_LD;
+    f16* Bs = Al + MG_RT * MG_LD;
+    f16x8 vh, vl;
+    // the eight floats by name first: this compiler folds v[i >> 2][i & 3]
+    // over an array of vectors to element 0 of each vector
+    const f32x4 lo4 = __builtin_bit_cast(f32x4, r.a[0]), hi4 = __builtin_bit_cast(f32x4, r.a[1]);
+    const float xs[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float x = xs[(q >> 1) + 4 * (q & 1)] * ascale;  // pair order 0 4 1 5 2 6 3 7
+      const f16 h = static_cast<f16>(x);
+      vh[q] = h;
+      vl[q] = __builtin_isfinite(x) ? static_cast<f16>(x - static_cast<float>(h)) : static_cast<f16>(0.f);
+    }
+    *reinterpret_cast<f16x8*>(Ah + arow * MG_LD + agrp * 8) = vh;
+    *reinterpret_cast<f16x8*>(Al + arow * MG_LD + agrp * 8) = vl;
+    const uint32_t magic = 0x64006400u;
+    const f16x2 n1032 = {static_cast<f16>(-1032.f), static_cast<f16>(-1032.f)};
+    const f16x2 inv16 = {static_cast<f16>(0.0625f), static_cast<f16>(0.0625f)};
+    const f16x2 n72 = {static_cast<f16>(-72.f), static_cast<f16>(-72.f)};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t x = r.b[d], x8 = x >> 8;
+      const f16x2 d0 = as_h2(and_or(x, 0x000F000Fu, magic)) + n1032;
+      const f16x2 d1 = __builtin_elementwise_fma(as_h2(and_or(x, 0x00F000F0u, magic)), inv16, n72);
+      const f16x2 d2 = as_h2(and_or(x8, 0x000F000Fu, magic)) + n1032;
+      const f16x2 d3 = __builtin_elementwise_fma(as_h2(and_or(x8, 0x00F000F0u, magic)), inv16, n72);
+      const f16x8 b = {d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+      *reinterpret_cast<f16x8*>(Bs + bcol * MG_LD + bh * 32 + d * 8) = b;
+    }
+  };
+
+  f32x16 acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int q = 0; q < 16; ++q) acc[j][q] = 0.f;
+  auto mfmas = [&](int stage) {
+    const f16* Ah = lds + stage * MG_STAGE;
+    const f16* Al = Ah + MG_RT * MG_LD;
+    const f16* Bs = Al + MG_RT * MG_LD;
+#pragma unroll
+    for (int kk = 0; kk < MG_K / 16; ++kk) {
+      const int ko = kk * 16 + (lane >> 5) * 8;
+      const int ar = wm * 32 + (lane & 31);
+      const f16x8 fh = *reinterpret_cast<const f16x8*>(Ah + ar * MG_LD + ko);
+      const f16x8 fl = *reinterpret_cast<const f16x8*>(Al + ar * MG_LD + ko);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f16x8 fb = *reinterpret_cast<const f16x8*>(Bs + (wn * 64 + j * 32 + (lane & 31)) * MG_LD + ko);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh, fb, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fl, fb, acc[j], 0, 0, 0);
+      }
+    }
+  };
+
+  // two register sets, loads two steps ahead; double-buffered LDS, one
+  // barrier per step
+  // step ks on stage ks % 2: `nxt` holds step ks + 1 (stored to the other
+  // stage during the step), `fill` receives step ks + 2
+  auto step = [&](int ks, int stage, Regs& nxt, Regs& fill) {
+    gload(fill, ks + 2);
+    mfmas(stage);
+    if (ks + 1 < ksteps) sstore(nxt, stage ^ 1);
+    __syncthreads();
+  };
+  Regs r0, r1;
+  gload(r0, 0);
+  gload(r1, 1);
+  sstore(r0, 0);
+  __syncthreads();
+  int ks = 0;
+  for (; ks + 1 < ksteps; ks += 2) {
+    step(ks, 0, r1, r0);
+    step(ks + 1, 1, r0, r1);
+  }
+  if (ks < ksteps) step(ks, 0, r1, r0);
+
+  // ---- epilogue: lane holds D[8 (q / 4) + 4 (lane / 32) + q % 4][lane % 32]
+  const float* S = FC2 ? a.s2 + static_cast<int64_t>(e) * a.H : a.s1 + static_cast<int64_t>(e) * a.F1;
+  float rmax[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) rmax[q] = 0.f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = n0 + wn * 64 + j * 32 + (lane & 31);
+    const float sc = c < Nd ? S[c] : 0.f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int r = wm * 32 + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+      const int p = s_pair[r];
+      const float v = acc[j][q] * sc * s_ru[r];
+      if constexpr (FC2) {
+        if (p >= 0 && c < Nd) a.yp[static_cast<int64_t>(p) * a.H + c] = v;
+      } else if constexpr (ST == MG_FC1_SWIGLU) {
+        // gate = row 2m (even lane), linear = row 2m + 1 (odd lane)
+        const float other = __shfl_xor(v, 1, 64);
+        const float o = swiglu(v, other, a);
+        if ((lane & 1) == 0 && p >= 0 && c < Nd) {
+          a.h[static_cast<int64_t>(p) * a.I + c / 2] = o;
+          if (__builtin_isfinite(o)) rmax[q] = fmaxf(rmax[q], __builtin_fabsf(o));
+        }
+      } else {
+        const float o = fmaxf(v, 0.f);
+        if (p >= 0 && c < Nd) {
+          a.h[static_cast<int64_t>(p) * a.I + c] = o;
+          if (__builtin_isfinite(o)) rmax[q] = fmaxf(rmax[q], o);
+        }
+      }
+    }
+  }
+  if constexpr (!FC2) {
+    // each row's largest |h| over this tile, into the pair's running maximum
+    // (non-negative floats order like their bit patterns)
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const float m = mg_half_max(rmax[q]);
+      const int r = wm * 32 + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+      const int p = s_pair[r];
+      if ((lane & 31) == 0 && p >= 0 && m > 0.f) atomicMax(g.hmax + p, __builtin_bit_cast(uint32_t, m));
+    }
+  }
+}
+
+// y[t][n] = sum over slots s of w[t k + s] * yp[t k + s][n], in slot order.
+__global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= a.T * a.H) return;
+  const int64_t t = i / a.H, n = i % a.H;
+  float y = 0.f;
+  for (int s = 0; s < a.k; ++s) {
+    const int64_t pair = t * a.k + s;
+    y = __builtin_fmaf(a.wts[pair], a.yp[pair * a.H + n], y);
+  }
+  a.y[i] = y;
+}
+
+}  // namespace
+}  // namespace xrmm
