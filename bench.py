@@ -31,7 +31,8 @@ PROFILES = os.path.join(ROOT, "profiles")
 SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048": 4, "qmoe_mixtral_t1": 6,
          "bnb4_nf4_m1": 7, "gbq_embed_t2048": 8, "int8a_decode_m1": 1, "f32_k2048_m1": 0,
          "mlp_prefill_m64": 9, "prefill_m2048_prepacked": 4, "down_proj_m64": 10, "mlp_prefill_m2048": 13,
-         "qkv_prefill_m2048": 14, "q8_f32_decode_m1": 15, "f32_prefill_m64": 16, "qmoe_prefill_t256": 17}
+         "qkv_prefill_m2048": 14, "q8_f32_decode_m1": 15, "f32_prefill_m64": 16, "qmoe_prefill_t256": 17,
+         "q8_f16_decode_m1": 18}
 # The CPU-oracle workload on the GPU: MatMulNBits float32, M=1, K=N=2048,
 # block_size 32, packed zero points (2,703,360 algorithmic bytes per call)
 F32 = dict(M=1, K=2048, N=2048, bs=32)
@@ -188,14 +189,15 @@ def make_replicas(torch, name, R, dev, seed):
             reps.append(dict(gB=_gen_weights(torch, g, N, K // bs, bs // 2, dev), gS=_scales(torch, g, (N, K // bs), dev),
                              uB=_gen_weights(torch, g, N, K // bs, bs // 2, dev), uS=_scales(torch, g, (N, K // bs), dev)))
         return dict(A=A, reps=reps, K=K, N=N, bs=bs, gamma=gamma)
-    if name in ("q8_f32_decode_m1", "f32_prefill_m64"):
+    if name in ("q8_f32_decode_m1", "f32_prefill_m64", "q8_f16_decode_m1"):
         q = Q8F32 if name.startswith("q8") else F32P
+        dt = torch.float16 if name == "q8_f16_decode_m1" else torch.float32
         K, N, bs, bits = q["K"], q["N"], q["bs"], q["bits"]
         kb = K // bs
-        A = torch.randn((q["M"], K), device=dev, generator=g)
+        A = torch.randn((q["M"], K), device=dev, generator=g).to(dt)
         for _ in range(R):
             reps.append(dict(B=torch.randint(0, 256, (N, kb, bs * bits // 8), dtype=torch.uint8, device=dev, generator=g),
-                             S=torch.rand((N, kb), device=dev, generator=g) * 0.01 + 0.04))
+                             S=(torch.rand((N, kb), device=dev, generator=g) * 0.01 + 0.04).to(dt)))
         return dict(A=A, reps=reps, K=K, N=N, bs=bs, bits=bits)
     if name == "mlp_prefill_m2048":
         q = MLP2K
@@ -288,8 +290,8 @@ def step_fn(ops, name, w):
             return ops.matmul_nbits_mlp(A, r["gB"], r["gS"], r["uB"], r["uS"], norm_scale=w["gamma"],
                                         block_size=w["bs"])
         return f
-    if name in ("q8_f32_decode_m1", "f32_prefill_m64"):
-        Y = torch.empty((A.shape[0], w["N"]), dtype=torch.float32, device=A.device)
+    if name in ("q8_f32_decode_m1", "f32_prefill_m64", "q8_f16_decode_m1"):
+        Y = torch.empty((A.shape[0], w["N"]), dtype=A.dtype, device=A.device)
 
         def f(i):
             r = reps[i % len(reps)]
@@ -653,7 +655,7 @@ def main():
     results = {}
     names = ["decode_up_m1", "prefill_m2048", "prefill_m2048_prepacked", "qkv_gqa_m4", "mlp_swiglu_m16",
              "mlp_prefill_m64", "down_proj_m64", "mlp_prefill_m2048", "qkv_prefill_m2048", "f32_k2048_m1",
-             "q8_f32_decode_m1", "f32_prefill_m64",
+             "q8_f32_decode_m1", "q8_f16_decode_m1", "f32_prefill_m64",
              "qmoe_mixtral_t1", "qmoe_prefill_t256", "bnb4_nf4_m1", "gbq_embed_t2048", "int8a_decode_m1"]
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
@@ -663,7 +665,7 @@ def main():
         # (prefill legs: 8 replicas, 8 x 30-66 MB of weights and scales)
         R = {"prefill_m2048": 8, "prefill_m2048_prepacked": 8, "mlp_prefill_m2048": 8, "qkv_prefill_m2048": 24,
              "qmoe_mixtral_t1": 2, "qmoe_prefill_t256": 1, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24,
-             "f32_k2048_m1": 100, "mlp_prefill_m64": 24, "down_proj_m64": 12, "q8_f32_decode_m1": 24,
+             "f32_k2048_m1": 100, "mlp_prefill_m64": 24, "down_proj_m64": 12, "q8_f32_decode_m1": 24, "q8_f16_decode_m1": 24,
              "f32_prefill_m64": 24}.get(name, args.replicas)
         w = make_replicas(torch, name, R, dev, seed=SEEDS[name])
         fn = step_fn(ops, name, w)
@@ -801,19 +803,22 @@ def main():
                                   ops.select_kernel("MatMulNBits", q["M"], q["K"], q["N"], 4, q["bs"], zp="packed"))}
     for name, q, what in (("q8_f32_decode_m1", Q8F32, "MatMulNBits float32 M=1 K=2560 N=4096 bits=8 bs=32 (upstream "
                                                      "qwen3-qproj-decode-m1-q8g32 geometry)"),
+                          ("q8_f16_decode_m1", Q8F32, "MatMulNBits float16 M=1 K=2560 N=4096 bits=8 bs=32 (upstream "
+                                                      "qwen3-qproj-decode-m1-q8g32, float32 arithmetic)"),
                           ("f32_prefill_m64", F32P, "MatMulNBits float32 M=64 K=4096 N=4096 bits=4 bs=32")):
         if name not in results:
             continue
         r = results[name]
         kb = q["K"] // q["bs"]
-        nbytes = q["N"] * (q["K"] * q["bits"] // 8 + kb * 4) + q["M"] * (q["K"] + q["N"]) * 4
+        esz = 2 if name == "q8_f16_decode_m1" else 4
+        nbytes = q["N"] * (q["K"] * q["bits"] // 8 + kb * esz) + q["M"] * (q["K"] + q["N"]) * esz
         fl = 2 * q["M"] * q["K"] * q["N"]
         gbs = nbytes / (r["ms"] * 1e-3) / 1e9
         out[name] = {"workload": what, "us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2),
                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "tflops": round(fl / (r["ms"] * 1e-3) / 1e12, 2),
                      "bytes_per_launch": nbytes, "replicas": r["replicas"],
                      "kernel": ops.select_kernel("MatMulNBits", q["M"], q["K"], q["N"], q["bits"], q["bs"],
-                                                 torch.float32)}
+                                                 torch.float16 if esz == 2 else torch.float32)}
     if "f32_k2048_m1" in results:
         r, q = results["f32_k2048_m1"], F32
         nbytes = 2_703_360

@@ -163,7 +163,8 @@ def test_fuzz_reaches_every_kernel_family():
 @pytest.mark.parametrize("op,M,K,N,bits,bs,dtype,zp,expect", [
     (0, 1, 2560, 4096, 8, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),  # the upstream q8 decode case, float32
     (0, 512, 2560, 4096, 8, 32, nat.F32, nat.U8, "gemv_q4_f32"),         # float32 8-bit prefill, chunks of four rows
-    (0, 1, 2560, 4096, 8, 32, nat.F16, nat.UNSPECIFIED, "generic"),      # float16 8-bit codes
+    (0, 1, 2560, 4096, 8, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_f32"),  # float16 8-bit codes: float32 arithmetic
+    (0, 512, 2560, 4096, 8, 64, nat.F16, nat.U8, "gemv_q4_f32"),         # float16 8-bit prefill rows
     (0, 1, 2048, 2048, 2, 32, nat.F32, nat.UNSPECIFIED, "generic"),      # 2-bit codes
 ])
 def test_kernel_selection_bits(op, M, K, N, bits, bs, dtype, zp, expect):

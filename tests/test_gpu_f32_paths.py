@@ -76,3 +76,38 @@ def test_f32_8bit_infinite_activation(gpu):
     ref = O.matmul_nbits(A, B, S, None, None, K=K, N=N, bits=bits, block_size=bs)
     assert O.tolerance_ok(Y, ref, np.float32)[0]
     assert np.isnan(Y[1, 5]) and np.isnan(ref[1, 5])
+
+
+F16_CASES = [
+    # M, K, N, bits, bs, zp, bias: float16 calls with 8-bit codes
+    (1, 2560, 4096, 8, 32, None, False),      # the upstream q8 decode geometry in float16
+    (3, 2560, 520, 8, 32, "packed", True),
+    (4, 1024, 100, 8, 64, "float16", False),
+    (17, 1024, 96, 8, 128, None, True),
+    (130, 768, 72, 8, 32, "packed", False),
+    (512, 256, 64, 8, 16, "float16", True),   # prefill rows, 16-code blocks
+]
+
+
+@pytest.mark.parametrize("M,K,N,bits,bs,zp,bias", F16_CASES)
+def test_f16_8bit_on_the_float32_gemv(gpu, M, K, N, bits, bs, zp, bias):
+    """float16 MatMulNBits with 8-bit codes runs the float32-arithmetic GEMV:
+    activations, scales and bias widen exactly, the sums are float32 and the
+    output is rounded once, so every element is within one binary16 rounding
+    (2^-11 relative) plus 1e-5 max|Y| of the exact result, well inside the
+    float16 bar."""
+    rng = np.random.default_rng(M * 13 + K + N + bits + bs)
+    A, B, S, Z, b = case(rng, M, K, N, bits, bs, zp, bias)
+    A, S = A.astype(np.float16), S.astype(np.float16)
+    b = None if b is None else b.astype(np.float16)
+    kind = None if zp is None else ("packed" if zp == "packed" else "float")
+    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float16, kind) == "gemv_q4_f32"
+    Y = ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, bits=bits, block_size=bs)
+    assert Y.dtype == torch.float16
+    Y = Y.cpu().numpy()
+    ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, bits=bits, block_size=bs)
+    ok, err, lim = O.tolerance_ok(Y, ref, np.float16)
+    assert ok, (err, lim)
+    exact = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, bits=bits, block_size=bs, out_dtype=np.float64)
+    bound = np.abs(exact) * 2.0 ** -11 + 1e-5 * np.abs(exact).max()
+    assert np.all(np.abs(Y.astype(np.float64) - exact) <= bound)

@@ -1,10 +1,13 @@
-// MatMulNBits GEMV for float32 activations (the contract's T1 = float32),
+// MatMulNBits GEMV in float32 arithmetic: float32 activations (the
+// contract's T1 = float32), and float16 calls that no binary16-weight kernel
+// takes (8-bit codes; weights whose dequantised value binary16 cannot hold).
 // 4- or 8-bit weights, any number of rows in chunks of up to four (the grid's
 // second dimension: each chunk reads the weights again, from the L2 / the
 // Infinity Cache for all but the first). Float32 arithmetic throughout, as the
-// reference's serial loop (complex_kernel.glsl:80,83): codes convert exactly
-// to float32 and multiply the activations with fused multiply-adds, so the
-// float32 bar (1e-5 * max|Y|) holds with margin.
+// reference's serial loop (complex_kernel.glsl:80,83): activations, scales and
+// bias convert exactly to float32, codes convert exactly to float32 and
+// multiply the activations with fused multiply-adds, so the float32 bar
+// (1e-5 * max|Y|) holds with margin; float16 outputs are rounded once.
 //
 // Work split. A wave owns C consecutive output columns; its lanes split K:
 // lane l takes the 16-byte chunks l, l + 64, ... of each column, so one load
@@ -26,12 +29,12 @@
 namespace xrmm {
 
 struct F32Args {
-  const float* A;
+  const void* A;       // T [M, K]
   const uint8_t* B;
-  const float* S;
+  const void* S;       // T [N, kb]
   const void* Z;       // packed u8 [N, zrow] or float [N, kb] (zesz bytes each)
-  const float* bias;
-  float* Y;
+  const void* bias;    // T [N] or null
+  void* Y;             // T [M, N]
   uint32_t N, K, kb, rowb, zrow, M, bsl, zesz;
   uint32_t meta_bytes;  // per-wave LDS slice: C*kb*4 scales (+ zero points), 16-aligned
   uint32_t zoff;        // zero points' offset inside the slice
@@ -56,9 +59,11 @@ __device__ __forceinline__ float ubyte(uint32_t x, int i) {
   return static_cast<float>((x >> (8 * i)) & 0xFFu);
 }
 
-template <int ZPK, int CPL, int C, int MR, int W, int BITS = 4>
+// T: float (activations, scales, bias and outputs in float32) or f16.
+template <typename T, int ZPK, int CPL, int C, int MR, int W, int BITS = 4>
 __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
   static_assert(BITS == 4 || BITS == 8, "4- or 8-bit codes");
+  constexpr uint32_t TS = sizeof(T);
   constexpr uint32_t CODES = 128 / BITS;         // codes per 16-byte chunk
   constexpr uint32_t H = CODES / 16;             // 16-code halves per chunk
   constexpr uint32_t CS = f32_chunk_stride<BITS>();
@@ -71,8 +76,8 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
   // this workgroup's chunk of up to MR rows (the grid's second dimension)
   const uint32_t m0 = blockIdx.y * MR;
   const int M = static_cast<int>(a.M - m0 < MR ? a.M - m0 : MR);
-  const float* A = a.A + static_cast<size_t>(m0) * K;
-  float* Yo = a.Y + static_cast<size_t>(m0) * N;
+  const T* A = static_cast<const T*>(a.A) + static_cast<size_t>(m0) * K;
+  T* Yo = static_cast<T*>(a.Y) + static_cast<size_t>(m0) * N;
   const uint32_t col0 = (xcd_slot(blockIdx.x, gridDim.x) * W + wave) * C;
   auto clampc = [&](uint32_t c) { return c < N ? c : N - 1; };
   const uint32_t act_floats = MR * nchunk * CS;
@@ -83,17 +88,20 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
   // ---- the wave's scale / zero-point block (C consecutive rows), 16-byte
   // pieces; loads start at the dword boundary at or below the block
   const uint32_t c0 = clampc(col0);
-  const uint32_t sbytes = C * kb * 4u;
+  const uint32_t sbytes = C * kb * TS;
   const uint32_t zbytes = ZPK == ZP_NONE ? 0u : C * zrow;
   const uint32_t zdel = (c0 * zrow) & 3u;
   constexpr int MP = 4;  // up to 4 KB per block
   u32x4 sv[MP], zv[ZPK == ZP_NONE ? 1 : MP];
   {
-    const rsrc_t rS = mk_rsrc(a.S, N * kb * 4u);
+    // a dword straddling the range's end reads as zero, so the range ends on
+    // the dword boundary past the last float16 scale (the scales are 16-byte
+    // aligned, so that dword lies in the page of the last scale)
+    const rsrc_t rS = mk_rsrc(a.S, (N * kb * TS + 3u) & ~3u);
 #pragma unroll
     for (int q = 0; q < MP; ++q) {
       const uint32_t o = lane * 16u + 1024u * q;
-      sv[q] = bld16_nt(rS, o < sbytes ? c0 * kb * 4u + o : kOOB, 0);
+      sv[q] = bld16_nt(rS, o < sbytes ? c0 * kb * TS + o : kOOB, 0);
     }
     if constexpr (ZPK != ZP_NONE) {
       const rsrc_t rZ = mk_rsrc(a.Z, (N * zrow + 15u) & ~15u);
@@ -106,9 +114,9 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- activations of the workgroup: 16-byte pieces (4 floats), thread t
-  // takes pieces t, t + 64 W, ...
-  const rsrc_t rA = mk_rsrc(A, static_cast<uint32_t>(M) * K * 4u);
+  // ---- activations of the workgroup: pieces of 4 values (16 bytes of
+  // float32, 8 of float16), thread t takes pieces t, t + 64 W, ...
+  const rsrc_t rA = mk_rsrc(A, static_cast<uint32_t>(M) * K * TS);
   constexpr int PIECES_PER_ROW_MAX = 64 * CPL * CODES / 4;  // nchunk * CODES floats / 4
   constexpr int PPT = (MR * PIECES_PER_ROW_MAX + W * 64 - 1) / (W * 64);
   const uint32_t ppr = nchunk * (CODES / 4);  // pieces per staged row
@@ -118,7 +126,16 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
     const uint32_t p = static_cast<uint32_t>(tid) + it * W * 64u;
     const uint32_t m = p / ppr, k = (p % ppr) * 4u;
     const bool ok = static_cast<int>(m) < M && k < K;  // K % 4 == 0 on this path
-    av[it] = bld16(rA, ok ? (m * K + k) * 4u : kOOB, 0);
+    if constexpr (TS == 4) {
+      av[it] = bld16(rA, ok ? (m * K + k) * 4u : kOOB, 0);
+    } else {
+      // four halves, widened exactly at the staging
+      const u32x2 h = bld8(rA, ok ? (m * K + k) * 2u : kOOB, 0);
+      const f16x2 h0 = as_h2(h[0]), h1 = as_h2(h[1]);
+      const f32x4 f = {static_cast<float>(h0[0]), static_cast<float>(h0[1]), static_cast<float>(h1[0]),
+                       static_cast<float>(h1[1])};
+      av[it] = __builtin_bit_cast(u32x4, f);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -178,7 +195,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
 #pragma unroll
       for (int h = 0; h < static_cast<int>(H); ++h) {  // 16-code halves (8-bit: the chunk)
         const uint32_t b = (chc * CODES + 16u * h) >> a.bsl;
-        const float s = *reinterpret_cast<const float*>(meta + (i * kb + b) * 4u);
+        const float s = static_cast<float>(*reinterpret_cast<const T*>(meta + (i * kb + b) * TS));
         float z = ZMID;
         if constexpr (ZPK == ZP_PACKED) {
           if constexpr (BITS == 4) z = static_cast<float>((zmeta[i * zrow + (b >> 1)] >> ((b & 1u) * 4u)) & 15u);
@@ -241,10 +258,10 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
   }
   const uint32_t mycol = col0 + static_cast<uint32_t>(lane);
   if (lane < C && mycol < N) {
-    const float b = a.bias ? a.bias[mycol] : 0.f;
+    const float b = a.bias ? static_cast<float>(static_cast<const T*>(a.bias)[mycol]) : 0.f;
 #pragma unroll
     for (int m = 0; m < MR; ++m)
-      if (m < M) Yo[static_cast<uint32_t>(m) * N + mycol] = out[m] + b;
+      if (m < M) Yo[static_cast<uint32_t>(m) * N + mycol] = static_cast<T>(out[m] + b);
   }
 }
 
@@ -261,21 +278,26 @@ inline int f32_cpl(const Launch& L) {
 // Rows per workgroup: 1, 2 or 4 (more rows: chunks of four on the grid's y).
 inline int f32_mr(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
 
+// Bytes of one activation, scale, bias or output value: float32 or float16.
+inline int64_t f32_esz(const Launch& L) { return L.dtype == DT_F16 ? 2 : 4; }
+
 inline uint32_t f32_meta_bytes(const Launch& L, uint32_t& zoff) {
-  const uint32_t sb = static_cast<uint32_t>(kF32C * L.kb * 4);
+  const uint32_t sb = static_cast<uint32_t>(kF32C * L.kb * f32_esz(L));
   zoff = (sb + 15u) & ~15u;
   const int64_t zrow = L.zp_kind == ZP_PACKED ? L.zrow : L.kb * (L.zp_dtype == DT_F32 ? 4 : 2);
   const uint32_t zb = L.zp_kind == ZP_NONE ? 0u : static_cast<uint32_t>(kF32C * zrow);
   return (zoff + zb + 3u + 15u) & ~15u;
 }
 
-// fp32, 4- or 8-bit, power-of-two block_size >= 16, K a multiple of 4,
-// 16-byte aligned tensors, rows of at most 256 chunks (whole 16-byte chunks),
-// the wave's scale / zero-point block within 4 KB and the staging within
-// 160 KB of LDS; at most 65535 chunks of four rows (the grid's y).
+// fp32, or fp16 with 8-bit codes or float32 weights required (`exact`:
+// dequantised weights binary16 cannot hold); 4- or 8-bit, power-of-two
+// block_size >= 16, K a multiple of 4, 16-byte aligned tensors, rows of at
+// most 256 chunks (whole 16-byte chunks), the wave's scale / zero-point block
+// within 4 KB and the staging within 160 KB of LDS; at most 65535 chunks of
+// four rows (the grid's y).
 inline bool f32_fits(const Launch& L) {
-  if (L.dtype != DT_F32 || (L.bits != 4 && L.bits != 8) || L.bs_log2 < 4 || L.op != OP_MATMUL || L.K % 4 != 0)
-    return false;
+  const bool t_ok = L.dtype == DT_F32 || (L.dtype == DT_F16 && (L.bits == 8 || L.exact_weights));
+  if (!t_ok || (L.bits != 4 && L.bits != 8) || L.bs_log2 < 4 || L.op != OP_MATMUL || L.K % 4 != 0) return false;
   if ((L.kb * L.block_size) % (128 / L.bits) != 0) return false;
   if (L.M < 1 || (L.M + 3) / 4 > 65535) return false;
   const int mr = f32_mr(L.M), cpl = f32_cpl(L);
@@ -285,7 +307,7 @@ inline bool f32_fits(const Launch& L) {
   if (L.zp_kind == ZP_FLOAT && L.p[0].zp == nullptr) return false;
   uint32_t zoff = 0;
   const uint32_t meta = f32_meta_bytes(L, zoff);
-  if (kF32C * L.kb * 4 > 4096 || meta - zoff > 4096 + 16) return false;
+  if (kF32C * L.kb * f32_esz(L) > 4096 || meta - zoff > 4096 + 16) return false;
   const uint32_t nchunk = static_cast<uint32_t>(L.kb * L.blob / 16);
   if (mr * f32_cpl(L) * 8 / L.bits > 16) return false;  // activation loads per thread (registers)
   const int64_t codes = 128 / L.bits;
@@ -293,16 +315,16 @@ inline bool f32_fits(const Launch& L) {
   return lds <= 160 * 1024;
 }
 
-template <int ZPK, int CPL, int MR, int BITS>
+template <typename T, int ZPK, int CPL, int MR, int BITS>
 inline hipError_t launch_f32_3(const Launch& L, hipStream_t st) {
   F32Args a{};
   const Proj& P = L.p[0];
-  a.A = static_cast<const float*>(L.A);
+  a.A = L.A;
   a.B = P.B;
-  a.S = static_cast<const float*>(P.scales);
+  a.S = P.scales;
   a.Z = P.zp;
-  a.bias = static_cast<const float*>(P.bias);
-  a.Y = static_cast<float*>(P.Y);
+  a.bias = P.bias;
+  a.Y = P.Y;
   a.N = static_cast<uint32_t>(P.N);
   a.K = static_cast<uint32_t>(L.K);
   a.kb = static_cast<uint32_t>(L.kb);
@@ -314,7 +336,7 @@ inline hipError_t launch_f32_3(const Launch& L, hipStream_t st) {
   a.meta_bytes = f32_meta_bytes(L, a.zoff);
   const uint32_t nchunk = a.rowb / 16u;
   const size_t lds = f32_act_bytes<MR, BITS>(nchunk) + size_t(kF32W) * a.meta_bytes;
-  auto kern = k_gemv_f32<ZPK, CPL, kF32C, MR, kF32W, BITS>;
+  auto kern = k_gemv_f32<T, ZPK, CPL, kF32C, MR, kF32W, BITS>;
   if (lds > 64 * 1024) {
     static std::atomic<int> done[kMaxDevices];  // per instantiation and device
     const hipError_t attr = raise_lds_cap(reinterpret_cast<const void*>(kern), 160 * 1024, done);
@@ -326,27 +348,32 @@ inline hipError_t launch_f32_3(const Launch& L, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int ZPK, int CPL, int BITS>
+template <typename T, int ZPK, int CPL, int BITS>
 inline hipError_t launch_f32_2(const Launch& L, hipStream_t st) {
   switch (f32_mr(L.M)) {
-    case 1: return launch_f32_3<ZPK, CPL, 1, BITS>(L, st);
-    case 2: return launch_f32_3<ZPK, CPL, 2, BITS>(L, st);
-    default: return launch_f32_3<ZPK, CPL, 4, BITS>(L, st);
+    case 1: return launch_f32_3<T, ZPK, CPL, 1, BITS>(L, st);
+    case 2: return launch_f32_3<T, ZPK, CPL, 2, BITS>(L, st);
+    default: return launch_f32_3<T, ZPK, CPL, 4, BITS>(L, st);
   }
 }
 
-template <int ZPK, int BITS>
+template <typename T, int ZPK, int BITS>
 inline hipError_t launch_f32_b(const Launch& L, hipStream_t st) {
   switch (f32_cpl(L)) {
-    case 1: return launch_f32_2<ZPK, 1, BITS>(L, st);
-    case 2: return launch_f32_2<ZPK, 2, BITS>(L, st);
-    default: return launch_f32_2<ZPK, 4, BITS>(L, st);
+    case 1: return launch_f32_2<T, ZPK, 1, BITS>(L, st);
+    case 2: return launch_f32_2<T, ZPK, 2, BITS>(L, st);
+    default: return launch_f32_2<T, ZPK, 4, BITS>(L, st);
   }
+}
+
+template <typename T, int ZPK>
+inline hipError_t launch_f32_t(const Launch& L, hipStream_t st) {
+  return L.bits == 8 ? launch_f32_b<T, ZPK, 8>(L, st) : launch_f32_b<T, ZPK, 4>(L, st);
 }
 
 template <int ZPK>
 inline hipError_t launch_f32_1(const Launch& L, hipStream_t st) {
-  return L.bits == 8 ? launch_f32_b<ZPK, 8>(L, st) : launch_f32_b<ZPK, 4>(L, st);
+  return L.dtype == DT_F16 ? launch_f32_t<f16, ZPK>(L, st) : launch_f32_t<float, ZPK>(L, st);
 }
 
 // Entry of one zero-point kind (defined in xrmm_gemv_f32_zp.hip).

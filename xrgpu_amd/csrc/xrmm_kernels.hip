@@ -610,9 +610,12 @@ Kernel select_kernel(const Launch& L) {
     if (q4_fast_ok(L) && fits_i32(L) && (L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 &&
         L.M < split_k_min_rows(L.op) && dot_fits(L))
       return K_GEMV_DOT;
+    // MatMulNBits at any row count on the float32-arithmetic GEMV
+    if (f32_fits(L) && fits_i32(L)) return K_GEMV_F32;
     return K_GENERIC;
   }
-  // float32 activations (the contract's T1 = float32), 4-bit, up to four rows
+  // float32 activations (the contract's T1 = float32) and float16 with 8-bit
+  // codes, any row count: the float32-arithmetic GEMV
   if (f32_fits(L) && fits_i32(L)) return K_GEMV_F32;
   if (q4_fast_ok(L) && fits_i32(L)) {
     if (mq_takes(L)) return K_GEMV_MQ;
