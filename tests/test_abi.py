@@ -99,7 +99,8 @@ def test_qkv_requires_norm_scale():
     (1, 8, 4096, 4096, 64, nat.F16, nat.U8, "gemv_q4_splitk"),
     (2, 16, 4096, 14336, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_splitk"),
     (2, 16, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_mfma"),
-    (2, 17, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemm_q4_fused"),   # Mlp prefill
+    (2, 17, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemm_q4_thin"),    # Mlp prefill, 17..64 rows
+    (2, 65, 3072, 8192, 32, nat.F16, nat.UNSPECIFIED, "gemm_q4_fused"),   # Mlp prefill past 64 rows
     (2, 2048, 4096, 14336, 64, nat.F16, nat.U8, "gemm_q4_big_fused"),  # 896 tiles of 256 staged columns
     (2, 256, 4096, 14336, 64, nat.F16, nat.U8, "gemm_q4_fused"),      # 112 tiles: the 128 x 128 GEMM
     (1, 2048, 4096, 4096, 64, nat.F16, nat.U8, "gemm_q4_big_fused"),  # Qkv prefill, one grid for Q, K, V

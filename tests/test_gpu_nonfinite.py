@@ -153,8 +153,8 @@ MLP_CASES = [
     # M, K, N, bs, dtype, norm, expected family
     (8, 2048, 64, 32, np.float16, False, "gemv_q4_splitk"),
     (6, 1024, 40, 64, np.float16, True, "gemv_q4_mfma"),
-    (24, 2048, 64, 32, np.float16, False, "gemv_q4_splitk"),    # two row chunks
-    (24, 1024, 64, 32, np.float16, False, "gemm_q4_fused"),
+    (24, 2048, 64, 32, np.float16, False, "gemm_q4_thin"),      # 17..64 rows: the thin GEMM
+    (70, 1024, 64, 32, np.float16, False, "gemm_q4_fused"),
     (130, 1024, 40, 64, np.float16, True, "gemm_q4_fused"),
     (4, 96, 24, 32, np.float32, False, "generic"),
     (4, 96, 24, 32, np.float32, True, "generic"),

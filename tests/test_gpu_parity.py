@@ -623,6 +623,8 @@ MLP_GEMM_CASES = [
     (24, 256, 96, 32, None, False, True, True, "sigmoid", False),
     (24, 256, 96, 32, "float_int", True, False, True, "none", True),
     (24, 256, 96, 32, None, True, True, False, "swiglu", False),
+    (64, 2048, 5632, 32, None, False, True, False, "silu", False),  # the 64-row SwiGLU prefill leg
+    (40, 512, 130, 16, "packed", True, True, True, "silu", True),   # bs = 16, a partial last tile
 ]
 
 
@@ -636,7 +638,8 @@ def test_mlp_gemm_parity(gpu, M, K, N, bs, zp, skip, norm, biases, act, res):
     _, gB, gS, gZ, gb = rand_case(rng, 1, K, N, 4, bs, dt, zp, biases)
     _, uB, uS, uZ, ub = rand_case(rng, 1, K, N, 4, bs, dt, zp, biases)
     kind = None if zp is None else ("packed" if zp == "packed" else "float")
-    assert ops().select_kernel("MatMulNBitsMlp", M, K, N, 4, bs, torch.float16, kind) == "gemm_q4_fused"
+    want = "gemm_q4_thin" if M <= 64 else "gemm_q4_fused"  # 17..64 rows: the thin GEMM
+    assert ops().select_kernel("MatMulNBitsMlp", M, K, N, 4, bs, torch.float16, kind) == want
     Y, R = ops().matmul_nbits_mlp(dev(A), dev(gB), dev(gS), dev(uB), dev(uS), skip=dev(sk), norm_scale=dev(g),
                                   gate_bias=dev(gb), up_bias=dev(ub), block_size=bs, activation=act,
                                   gate_zero_points=dev(gZ), up_zero_points=dev(uZ), want_residual=res)
@@ -650,7 +653,8 @@ def test_mlp_gemm_parity(gpu, M, K, N, bs, zp, skip, norm, biases, act, res):
 SK_CHUNK_CASES = [
     # op, M, K, N (Qkv: Nq, Nkv), bs, zp, extras: the split-K GEMV over row
     # chunks of 16 (17..64 rows, K of 64 or 128 chunks): partial last chunks,
-    # every operator and zero-point kind, prologue and epilogue variants
+    # every operator and zero-point kind, prologue and epilogue variants (Mlp
+    # runs the thin GEMM at these rows, after the same prologue)
     ("mnb", 17, 4096, 100, 32, "packed", dict(bias=True)),
     ("mnb", 33, 2048, 260, 64, "float", dict(bias=True)),
     ("mnb", 64, 4096, 1000, 128, None, dict(bias=False)),
@@ -695,7 +699,7 @@ def test_splitk_row_chunks(gpu, op, M, K, N, bs, zp, ex):
         g = rng.uniform(0.5, 1.5, K).astype(dt) if ex["norm"] else None
         _, gB, gS, gZ, gb = rand_case(rng, 1, K, N, 4, bs, dt, zp, ex["biases"])
         _, uB, uS, uZ, ub = rand_case(rng, 1, K, N, 4, bs, dt, zp, ex["biases"])
-        assert o.select_kernel("MatMulNBitsMlp", M, K, N, 4, bs, torch.float16, kind) == "gemv_q4_splitk"
+        assert o.select_kernel("MatMulNBitsMlp", M, K, N, 4, bs, torch.float16, kind) == "gemm_q4_thin"
         Y, R = o.matmul_nbits_mlp(dev(A), dev(gB), dev(gS), dev(uB), dev(uS), skip=dev(sk), norm_scale=dev(g),
                                   gate_bias=dev(gb), up_bias=dev(ub), block_size=bs, activation=ex["act"],
                                   gate_zero_points=dev(gZ), up_zero_points=dev(uZ), want_residual=ex["res"])

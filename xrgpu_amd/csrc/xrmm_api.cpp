@@ -255,7 +255,7 @@ int64_t xs_need(xrmm::Launch L) {
   static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
   L.xs = const_cast<uint8_t*>(dummy);
   const xrmm::Kernel k = xrmm::select_kernel(L);
-  return k == xrmm::K_GEMM_FUSED || k == xrmm::K_GEMM_BIG_FUSED ? xrmm::fused_xs_bytes(L) : 0;
+  return k == xrmm::K_GEMM_FUSED || k == xrmm::K_GEMM_BIG_FUSED || k == xrmm::K_GEMM_THIN ? xrmm::fused_xs_bytes(L) : 0;
 }
 
 // Attach a caller's workspace when the launch uses one.

@@ -30,6 +30,11 @@
 // split's float32 partial tile goes to the workspace and the last split of a
 // tile to arrive adds them in split order (deterministic), clears the tile's
 // counter and writes Y (+ bias, rounded once to binary16).
+//
+// MatMulNBitsMlp (MLP): the two column groups are the gate and the up
+// projection of the same 32 outputs (CG = 2), the activations are the
+// prologue's normalised rows, and the up group's tile reaches the gate
+// group through LDS for act(g + gate bias) * (u + up bias); one split.
 #pragma once
 #include "xrmm_device.h"
 
@@ -63,8 +68,9 @@ __host__ __device__ constexpr int thin_lds_bytes() {
   return 2 * (8 / CG) * (32 * MT) * (KC + 8) * 2 + (STG ? 2 * 32 * CG * thin_meta_slots<CG, KC>() * 3 : 0);
 }
 
-template <int ZPK, int SPC, int CG, int KC, int MT>
+template <int ZPK, int SPC, int CG, int KC, int MT, bool MLP = false>
 __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
+  static_assert(!MLP || CG == 2, "Mlp tiles pair one gate and one up column group");
   // Integer zero points (and none): the iteration's scales and zero points
   // are staged in LDS with the activations, loaded by consecutive threads
   // along each column's block row. Float zero points: each lane loads its
@@ -92,7 +98,9 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
   const int cg = wave % CG, kq = wave / CG;
   const uint32_t bid = blockIdx.x;
   const uint32_t tile = bid / t.S, sp = bid % t.S;
-  const Proj& P = L.p[0];
+  // the wave's projection: Mlp gate (group 0) or up (group 1); the index is
+  // wave-uniform, so the buffer resources below stay scalar
+  const Proj& P = L.p[MLP ? cg : 0];
   const uint32_t M = static_cast<uint32_t>(L.M), N = static_cast<uint32_t>(P.N), K = static_cast<uint32_t>(L.K);
   const uint32_t kb = static_cast<uint32_t>(L.kb);
   const uint32_t rowb = static_cast<uint32_t>(L.kb * L.block_size / 2);
@@ -111,9 +119,10 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
     return c0 + KQ * ii;
   };
 
-  // ---- this lane's weight column
-  const uint32_t n0 = tile * NT;
-  const uint32_t n = n0 + 32u * cg + static_cast<uint32_t>(lane & 31);
+  // ---- this lane's weight column (Mlp: output column of both groups)
+  constexpr uint32_t NO = MLP ? 32u : static_cast<uint32_t>(NT);  // output columns per tile
+  const uint32_t n0 = tile * NO;
+  const uint32_t n = n0 + (MLP ? 0u : 32u * cg) + static_cast<uint32_t>(lane & 31);
   const uint32_t g = static_cast<uint32_t>(lane >> 5);
   const bool nval = n < N;
   const uint32_t zrow = ZPK == ZP_PACKED ? static_cast<uint32_t>(L.zrow) : kb * (L.zp_dtype == DT_F32 ? 4u : 2u);
@@ -167,17 +176,27 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
   };
   // metadata of iteration i: slot e = tid + GT_T x is block blk0 + e % MS of
   // column n0 + e / MS
+  // Mlp: the first half of the slots (x < MPT / 2) are the gate columns, the
+  // second half the up columns, so each load's projection is known at compile time
+  static_assert(!MLP || (MPT % 2 == 0 && GT_T * (MPT / 2) == 32 * MS), "gate slots, then up slots");
+  const rsrc_t rS0 = mk_rsrc(L.p[0].scales, (N * kb * 2u + 15u) & ~15u);
+  const rsrc_t rS1 = MLP ? mk_rsrc(L.p[1].scales, (N * kb * 2u + 15u) & ~15u) : rS0;
+  const void* z0 = L.p[0].zp ? L.p[0].zp : L.p[0].scales;
+  const rsrc_t rZ0 = mk_rsrc(z0, (N * zrow + 15u) & ~15u);
+  const rsrc_t rZ1 = MLP ? mk_rsrc(L.p[1].zp ? L.p[1].zp : L.p[1].scales, (N * zrow + 15u) & ~15u) : rZ0;
   auto mload = [&](MRegs& mr, uint32_t i, bool live) {
     if constexpr (STG) {
       const uint32_t b0 = blk0(i), nb = nblk(i);
       const bool it = live & (cfirst(i) < c1);
 #pragma unroll
       for (int x = 0; x < MPT; ++x) {
-        const uint32_t e = static_cast<uint32_t>(tid + GT_T * x), col = n0 + e / MS, sl = e % MS, b = b0 + sl;
+        const bool up = MLP && x >= MPT / 2;
+        const uint32_t e = static_cast<uint32_t>(tid + GT_T * x), ct = e / MS, sl = e % MS, b = b0 + sl;
+        const uint32_t col = n0 + (MLP ? (ct & 31u) : ct);
         const bool ok = it & (sl < nb) & (col < N) & (b < kb);
-        mr.s[x] = bld_u16(rS, ok ? col * kb * 2u + b * 2u : OOB, 0);
+        mr.s[x] = bld_u16(up ? rS1 : rS0, ok ? col * kb * 2u + b * 2u : OOB, 0);
         mr.z[x] = 0u;
-        if constexpr (ZPK == ZP_PACKED) mr.z[x] = bld_u8(rZ, ok ? col * zrow + (b >> 1) : OOB, 0);
+        if constexpr (ZPK == ZP_PACKED) mr.z[x] = bld_u8(up ? rZ1 : rZ0, ok ? col * zrow + (b >> 1) : OOB, 0);
       }
     }
   };
@@ -266,7 +285,10 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
 
   // ---- pipeline: weights two iterations ahead, activations one ahead, in
   // rounds of up to GT_IMAX iterations (one round unless a single split
-  // covers a long K)
+  // covers a long K). Measured slower and not kept: every weight load of a
+  // round issued at its start (activations two iterations ahead), 31.1
+  // against 27.0 us on the down projection; a rolled loop of three
+  // iterations per body, 35.4 us.
   for (uint32_t base = 0; base < t.ni; base += GT_IMAX) {
     const uint32_t nr = t.ni - base < GT_IMAX ? t.ni - base : GT_IMAX;
     WRegs wr[GT_IMAX];
@@ -321,6 +343,31 @@ __global__ __launch_bounds__(GT_T) void k_gemm_thin(Launch L, ThinArgs t) {
 
   // lane holds D[8 (e / 4) + 4 (lane / 32) + e % 4][lane % 32] of row tile r
   const uint32_t prow = 4u * g;
+  if constexpr (MLP) {
+    // the up group's tile (past the K-group partials) for the gate group
+    float* upt = red + (KQ - 1) * CG * MT * 16 * 64;
+    static_assert(((KQ - 1) * CG + 1) * MT * 16 * 64 * 4 <= thin_lds_bytes<CG, KC, MT, STG>(), "the up tile fits the LDS");
+    if (kq == 0 && cg == 1) {
+#pragma unroll
+      for (int r = 0; r < MT; ++r)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) upt[(r * 16 + e) * 64 + lane] = acc[r][e];
+    }
+    __syncthreads();
+    if (kq != 0 || cg != 0 || !nval) return;
+    const float gb = L.p[0].bias ? static_cast<float>(static_cast<const f16*>(L.p[0].bias)[n]) : 0.f;
+    const float ub = L.p[1].bias ? static_cast<float>(static_cast<const f16*>(L.p[1].bias)[n]) : 0.f;
+    f16* Y = static_cast<f16*>(L.p[0].Y);
+#pragma unroll
+    for (int r = 0; r < MT; ++r)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t m = 32u * r + 8u * (e >> 2) + prow + (e & 3);
+        const float u = upt[(r * 16 + e) * 64 + lane] + ub;
+        if (m < M) Y[m * N + n] = static_cast<f16>(activate(acc[r][e] + gb, L.act) * u);
+      }
+    return;
+  }
   if (t.S > 1) {
     // Split-K: system-coherent (sc0 sc1) 16-byte stores of this split's
     // partial tile, every wave waits for its own, then one arrival count per
@@ -419,26 +466,30 @@ constexpr int kThinKC = kThinCG == 2 ? 128 : 256;
 // Compute units of the current device (cached per device ordinal).
 int device_cus();
 
+// Mlp tiles hold 32 outputs (gate and up columns of them), one split.
 inline ThinArgs thin_args(const Launch& L, bool have_ws) {
+  if (L.op == OP_MLP) return thin_plan<2, 128>(L.kb * L.block_size, 2 * L.p[0].N, device_cus(), false);
   return thin_plan<kThinCG, kThinKC>(L.kb * L.block_size, L.p[0].N, device_cus(), have_ws);
 }
 
 // Split-K workspace bytes of the geometry (0: no split).
 inline int64_t thin_ws_bytes(const Launch& L) {
+  if (L.op == OP_MLP) return 0;
   const ThinArgs a = thin_args(L, true);
   return L.M <= 32 ? thin_workspace_bytes<kThinCG, 1>(a) : thin_workspace_bytes<kThinCG, 2>(a);
 }
 
-template <int ZPK, int SPC, int MT>
+template <int ZPK, int SPC, int MT, bool MLP>
 inline hipError_t launch_thin3(const Launch& L, hipStream_t st) {
-  auto kern = k_gemm_thin<ZPK, SPC, kThinCG, kThinKC, MT>;
-  constexpr int lds = thin_lds_bytes<kThinCG, kThinKC, MT, ZPK != ZP_FLOAT>();
+  constexpr int CG = MLP ? 2 : kThinCG, KC = MLP ? 128 : kThinKC;
+  auto kern = k_gemm_thin<ZPK, SPC, CG, KC, MT, MLP>;
+  constexpr int lds = thin_lds_bytes<CG, KC, MT, ZPK != ZP_FLOAT>();
   if (lds > 64 * 1024) {
     static std::atomic<int> done[kMaxDevices];
     const hipError_t e = raise_lds_cap(reinterpret_cast<const void*>(kern), lds, done);
     if (e != hipSuccess) return e;
   }
-  const bool ws = L.ws != nullptr && L.splits > 1;
+  const bool ws = !MLP && L.ws != nullptr && L.splits > 1;
   ThinArgs a = thin_args(L, ws);
   if (ws && a.S != static_cast<uint32_t>(L.splits)) a = thin_args(L, false);  // planned for another split: run unsplit
   const uint64_t grid = uint64_t(a.tiles) * a.S;
@@ -447,11 +498,18 @@ inline hipError_t launch_thin3(const Launch& L, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int ZPK, bool MLP>
+inline hipError_t launch_thin2(const Launch& L, hipStream_t st) {
+  if (L.block_size >= 32)
+    return L.M <= 32 ? launch_thin3<ZPK, 1, 1, MLP>(L, st) : launch_thin3<ZPK, 1, 2, MLP>(L, st);
+  return L.M <= 32 ? launch_thin3<ZPK, 2, 1, MLP>(L, st) : launch_thin3<ZPK, 2, 2, MLP>(L, st);
+}
+
+// MatMulNBits, or MatMulNBitsMlp on rows that need no prologue (normalised
+// rows from the prologue, or no skip and no normScale).
 template <int ZPK>
 inline hipError_t launch_thin(const Launch& L, hipStream_t st) {
-  if (L.block_size >= 32)
-    return L.M <= 32 ? launch_thin3<ZPK, 1, 1>(L, st) : launch_thin3<ZPK, 1, 2>(L, st);
-  return L.M <= 32 ? launch_thin3<ZPK, 2, 1>(L, st) : launch_thin3<ZPK, 2, 2>(L, st);
+  return L.op == OP_MLP ? launch_thin2<ZPK, true>(L, st) : launch_thin2<ZPK, false>(L, st);
 }
 
 // Defined once per zero-point kind (xrmm_gemm_zp.hip).

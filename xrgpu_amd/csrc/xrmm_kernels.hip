@@ -416,42 +416,25 @@ __global__ __launch_bounds__(256 * KG) void k_gemm_q4(Launch L) {
 // after the normalisation, so it stays in range wherever the normalised value
 // does (|r * gamma| itself may exceed 65504). The residual output receives r
 // rounded once. One workgroup per row, 16-byte pieces (K % 8 == 0 and 16-byte
-// aligned tensors: the fast path's conditions); the row's second pass finds
-// its pieces in the L1/L2.
+// aligned tensors: the fast path's conditions). P > 0: each thread holds its
+// P pieces of the row (and of gamma) in registers, all loaded at once (rows
+// up to 256 x 8 x P); P = 0: two passes, the second finding its pieces in
+// the L1 / L2.
+template <int P>
 __global__ __launch_bounds__(256) void k_rms_rows(Launch L) {
   const int tid = threadIdx.x;
   const int64_t m = blockIdx.x, K = L.K;
   const f16* A = static_cast<const f16*>(L.A) + m * K;
   const f16* S = L.skip ? static_cast<const f16*>(L.skip) + m * K : nullptr;
   const f16* G = static_cast<const f16*>(L.gamma);
-  auto row = [&](int64_t k, float r[8]) {
-    const f16x8 a = __builtin_bit_cast(f16x8, ld16(A + k));
-    const f16x8 sk = S ? __builtin_bit_cast(f16x8, ld16(S + k)) : f16x8{};
+  f16* X = static_cast<f16*>(L.xs) + m * K;
+  f16* R = L.residual ? static_cast<f16*>(L.residual) + m * K : nullptr;
+  auto row = [&](const f16x8& a, const f16x8& sk, float r[8]) {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
       r[e] = S ? __fadd_rn(static_cast<float>(a[e]), static_cast<float>(sk[e])) : static_cast<float>(a[e]);
   };
-  float inv = 1.f;
-  if (G) {
-    float sq = 0.f;
-    for (int64_t k = int64_t(tid) * 8; k < K; k += 256 * 8) {
-      float r[8];
-      row(k, r);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sq = __builtin_fmaf(r[e], r[e], sq);
-    }
-    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
-    __shared__ float red[4];
-    if ((tid & 63) == 0) red[tid >> 6] = sq;
-    __syncthreads();
-    inv = __builtin_amdgcn_rsqf(((red[0] + red[1]) + (red[2] + red[3])) / static_cast<float>(K) + L.eps);
-  }
-  f16* X = static_cast<f16*>(L.xs) + m * K;
-  f16* R = L.residual ? static_cast<f16*>(L.residual) + m * K : nullptr;
-  for (int64_t k = int64_t(tid) * 8; k < K; k += 256 * 8) {
-    float r[8];
-    row(k, r);
-    const f16x8 g = G ? __builtin_bit_cast(f16x8, ld16(G + k)) : f16x8{};
+  auto finish = [&](int64_t k, const float r[8], const f16x8& g, float inv) {
     f16x8 x, r16;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -460,6 +443,70 @@ __global__ __launch_bounds__(256) void k_rms_rows(Launch L) {
     }
     *reinterpret_cast<f16x8*>(X + k) = x;
     if (R) *reinterpret_cast<f16x8*>(R + k) = r16;
+  };
+  __shared__ float red[4];
+  auto row_inv = [&](float sq) {
+    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = sq;
+    __syncthreads();
+    return __builtin_amdgcn_rsqf(((red[0] + red[1]) + (red[2] + red[3])) / static_cast<float>(K) + L.eps);
+  };
+  if constexpr (P > 0) {
+    // the row's pieces (and gamma's) held in registers: one pass over memory,
+    // every load issued before the first use
+    f16x8 a[P], sk[P], g[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int64_t k = (int64_t(tid) + 256 * p) * 8;
+      const bool ok = k < K;
+      a[p] = ok ? __builtin_bit_cast(f16x8, ld16(A + k)) : f16x8{};
+      sk[p] = ok && S ? __builtin_bit_cast(f16x8, ld16(S + k)) : f16x8{};
+      g[p] = ok && G ? __builtin_bit_cast(f16x8, ld16(G + k)) : f16x8{};
+    }
+    float inv = 1.f;
+    if (G) {
+      float sq = 0.f;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        float r[8];
+        row(a[p], sk[p], r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sq = __builtin_fmaf(r[e], r[e], sq);  // zero past K
+      }
+      inv = row_inv(sq);
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int64_t k = (int64_t(tid) + 256 * p) * 8;
+      if (k >= K) break;
+      float r[8];
+      row(a[p], sk[p], r);
+      finish(k, r, g[p], inv);
+    }
+  } else {
+    // long rows: two passes, the second finds its pieces in the L1 / L2
+    auto load_row = [&](int64_t k, float r[8]) {
+      const f16x8 a = __builtin_bit_cast(f16x8, ld16(A + k));
+      const f16x8 sk = S ? __builtin_bit_cast(f16x8, ld16(S + k)) : f16x8{};
+      row(a, sk, r);
+    };
+    float inv = 1.f;
+    if (G) {
+      float sq = 0.f;
+      for (int64_t k = int64_t(tid) * 8; k < K; k += 256 * 8) {
+        float r[8];
+        load_row(k, r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sq = __builtin_fmaf(r[e], r[e], sq);
+      }
+      inv = row_inv(sq);
+    }
+    for (int64_t k = int64_t(tid) * 8; k < K; k += 256 * 8) {
+      float r[8];
+      load_row(k, r);
+      const f16x8 g = G ? __builtin_bit_cast(f16x8, ld16(G + k)) : f16x8{};
+      finish(k, r, g, inv);
+    }
   }
 }
 
@@ -467,7 +514,11 @@ __global__ __launch_bounds__(256) void k_rms_rows(Launch L) {
 // normalised binary16 rows, with no skip, normScale or residual left to do.
 static hipError_t run_prologue(const Launch& L, Launch& Lx, hipStream_t st) {
   if (L.M > 0x7FFFFFFF) return hipErrorInvalidValue;  // launch limit
-  hipLaunchKernelGGL(k_rms_rows, dim3(static_cast<uint32_t>(L.M)), dim3(256), 0, st, L);
+  // pieces of 8 per thread: rows up to 16384 held in registers
+  const int64_t pieces = (L.K / 8 + 255) / 256;
+  auto kern = pieces <= 1 ? k_rms_rows<1> : pieces <= 2 ? k_rms_rows<2> : pieces <= 4 ? k_rms_rows<4>
+            : pieces <= 8 ? k_rms_rows<8> : k_rms_rows<0>;
+  hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(L.M)), dim3(256), 0, st, L);
   Lx = L;
   Lx.A = L.xs;
   Lx.skip = nullptr;
@@ -591,15 +642,23 @@ inline int64_t split_k_min_rows(int op) { return op == OP_MATMUL ? 3 : op == OP_
 // N = 14336) and loses to the dot GEMV below.
 inline bool mq_takes(const Launch& L) { return L.op == OP_QKV && L.M <= 4 && mq_fits(L); }
 
-// MatMulNBits with 17..64 rows: the thin GEMM (weights straight into the
-// MFMA operands, activations shared through LDS) where the split-K GEMV does
-// not apply, or everywhere in that range with XRMM_THIN_OVER_SK.
+// 17..64 rows: the thin GEMM (weights straight into the MFMA operands,
+// activations shared through LDS). MatMulNBits where the split-K GEMV does
+// not apply, or everywhere in that range with XRMM_THIN_OVER_SK; Mlp on the
+// prologue's normalised rows (or rows that need no prologue), unless
+// XRMM_THIN_MLP is 0.
 #ifndef XRMM_THIN_OVER_SK
 #define XRMM_THIN_OVER_SK 0
 #endif
+#ifndef XRMM_THIN_MLP
+#define XRMM_THIN_MLP 1
+#endif
 inline bool thin_takes(const Launch& L) {
-  if (L.op != OP_MATMUL || L.M <= 16 || L.M > 64) return false;
-  return XRMM_THIN_OVER_SK || !sk_fits(L);
+  if (L.M <= 16 || L.M > 64) return false;
+  if (L.op == OP_MATMUL) return XRMM_THIN_OVER_SK || !sk_fits(L);
+  if (L.op == OP_MLP)
+    return XRMM_THIN_MLP && L.p[0].N == L.p[1].N && (L.xs != nullptr || !fused_prologue(L));
+  return false;
 }
 
 Kernel select_kernel(const Launch& L) {
@@ -762,9 +821,15 @@ hipError_t launch(const Launch& L, hipStream_t st) {
     return launch_gemm_fused_for<ZP_PACKED>(Lx, st);
   }
   if (k == K_GEMM_THIN) {
-    if (zpk == ZP_NONE) return launch_gemm_thin_for<ZP_NONE>(L, st);
-    if (zpk == ZP_FLOAT) return launch_gemm_thin_for<ZP_FLOAT>(L, st);
-    return launch_gemm_thin_for<ZP_PACKED>(L, st);
+    // Mlp: the prologue first, the GEMM on its normalised rows
+    Launch Lx = L;
+    if (L.op != OP_MATMUL && L.xs != nullptr && fused_prologue(L)) {
+      const hipError_t e = run_prologue(L, Lx, st);
+      if (e != hipSuccess) return e;
+    }
+    if (zpk == ZP_NONE) return launch_gemm_thin_for<ZP_NONE>(Lx, st);
+    if (zpk == ZP_FLOAT) return launch_gemm_thin_for<ZP_FLOAT>(Lx, st);
+    return launch_gemm_thin_for<ZP_PACKED>(Lx, st);
   }
   if (k == K_GEMM_Q4) {
     if (zpk == ZP_NONE) return launch_gemm1<ZP_NONE>(L, st);
