@@ -36,7 +36,10 @@ constexpr int MG_CT = 256;  // columns per tile
 constexpr int MG_K = 64;    // K step
 constexpr int MG_LD = MG_K + 8;
 constexpr int MG_T = 512;   // threads: 8 waves, 2 (rows of 32) x 4 (columns of 64)
-constexpr int MG_STAGE = (2 * MG_RT + MG_CT) * MG_LD;  // halfs per stage: A hi, A lo, B
+constexpr int MG_BW = MG_K / 8;  // dwords of codes per column and K step
+// halfs per stage: A hi, A lo (rows of MG_LD), then the raw codes as
+// [dword of the step][column] (a fragment's eight codes are one dword)
+constexpr int MG_STAGE = 2 * MG_RT * MG_LD + MG_BW * MG_CT * 2;
 constexpr size_t MG_LDS = 2 * MG_STAGE * sizeof(_Float16);
 
 // Lists of the grouped path, inside the workspace's counter region.
@@ -147,7 +150,7 @@ __device__ __forceinline__ float mg_half_max(float v) {
 
 // One 64-pair x 256-column tile of an expert's matrix.
 template <int ST>
-__global__ __launch_bounds__(MG_T, 1) void k_moe_ggemm(MoeArgs a, MgLists g, int nct) {
+__global__ __launch_bounds__(MG_T, 2) void k_moe_ggemm(MoeArgs a, MgLists g, int nct) {
   constexpr bool FC2 = ST == MG_FC2;
   extern __shared__ __align__(16) unsigned char smem[];
   f16* lds = reinterpret_cast<f16*>(smem);
@@ -219,11 +222,11 @@ __global__ __launch_bounds__(MG_T, 1) void k_moe_ggemm(MoeArgs a, MgLists g, int
     r.b = bld16(rB, (ok ? boff : OOB) + static_cast<uint32_t>(ks * MG_K / 2 + bh * 16), 0);
   };
   // A: scaled, split into binary16 hi / lo in the pair order of the codes;
-  // B: the codes minus 8 as exact binary16 (pair order)
+  // B: the raw code dwords (dequantised when a fragment is read)
   auto sstore = [&](const Regs& r, int stage) {
     f16* Ah = lds + stage * MG_STAGE;
     f16* Al = Ah + MG_RT * MG_LD;
-    f16* Bs = Al + MG_RT * MG_LD;
+    uint32_t* Bw = reinterpret_cast<uint32_t*>(Al + MG_RT * MG_LD);
     f16x8 vh, vl;
     // the eight floats by name first: this compiler folds v[i >> 2][i & 3]
     // over an array of vectors to element 0 of each vector
@@ -238,20 +241,22 @@ __global__ __launch_bounds__(MG_T, 1) void k_moe_ggemm(MoeArgs a, MgLists g, int
     }
     *reinterpret_cast<f16x8*>(Ah + arow * MG_LD + agrp * 8) = vh;
     *reinterpret_cast<f16x8*>(Al + arow * MG_LD + agrp * 8) = vl;
-    const uint32_t magic = 0x64006400u;
-    const f16x2 n1032 = {static_cast<f16>(-1032.f), static_cast<f16>(-1032.f)};
-    const f16x2 inv16 = {static_cast<f16>(0.0625f), static_cast<f16>(0.0625f)};
-    const f16x2 n72 = {static_cast<f16>(-72.f), static_cast<f16>(-72.f)};
+    // dword 4 bh + d of the step (codes 32 bh + 8 d .. + 7) of column bcol
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint32_t x = r.b[d], x8 = x >> 8;
-      const f16x2 d0 = as_h2(and_or(x, 0x000F000Fu, magic)) + n1032;
-      const f16x2 d1 = __builtin_elementwise_fma(as_h2(and_or(x, 0x00F000F0u, magic)), inv16, n72);
-      const f16x2 d2 = as_h2(and_or(x8, 0x000F000Fu, magic)) + n1032;
-      const f16x2 d3 = __builtin_elementwise_fma(as_h2(and_or(x8, 0x00F000F0u, magic)), inv16, n72);
-      const f16x8 b = {d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
-      *reinterpret_cast<f16x8*>(Bs + bcol * MG_LD + bh * 32 + d * 8) = b;
-    }
+    for (int d = 0; d < 4; ++d) Bw[(4 * bh + d) * MG_CT + bcol] = r.b[d];
+  };
+  // a fragment's eight codes -> c - 8 as exact binary16, pair order
+  // (c0 c4 c1 c5 c2 c6 c3 c7, the activations' staging order)
+  const f16x2 n1032 = {static_cast<f16>(-1032.f), static_cast<f16>(-1032.f)};
+  const f16x2 inv16 = {static_cast<f16>(0.0625f), static_cast<f16>(0.0625f)};
+  const f16x2 n72 = {static_cast<f16>(-72.f), static_cast<f16>(-72.f)};
+  auto dq = [&](uint32_t x) {
+    const uint32_t magic = 0x64006400u, x8 = x >> 8;
+    const f16x2 d0 = as_h2(and_or(x, 0x000F000Fu, magic)) + n1032;
+    const f16x2 d1 = __builtin_elementwise_fma(as_h2(and_or(x, 0x00F000F0u, magic)), inv16, n72);
+    const f16x2 d2 = as_h2(and_or(x8, 0x000F000Fu, magic)) + n1032;
+    const f16x2 d3 = __builtin_elementwise_fma(as_h2(and_or(x8, 0x00F000F0u, magic)), inv16, n72);
+    return f16x8{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
   };
 
   f32x16 acc[2];
@@ -262,7 +267,7 @@ __global__ __launch_bounds__(MG_T, 1) void k_moe_ggemm(MoeArgs a, MgLists g, int
   auto mfmas = [&](int stage) {
     const f16* Ah = lds + stage * MG_STAGE;
     const f16* Al = Ah + MG_RT * MG_LD;
-    const f16* Bs = Al + MG_RT * MG_LD;
+    const uint32_t* Bw = reinterpret_cast<const uint32_t*>(Al + MG_RT * MG_LD);
 #pragma unroll
     for (int kk = 0; kk < MG_K / 16; ++kk) {
       const int ko = kk * 16 + (lane >> 5) * 8;
@@ -271,7 +276,8 @@ __global__ __launch_bounds__(MG_T, 1) void k_moe_ggemm(MoeArgs a, MgLists g, int
       const f16x8 fl = *reinterpret_cast<const f16x8*>(Al + ar * MG_LD + ko);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const f16x8 fb = *reinterpret_cast<const f16x8*>(Bs + (wn * 64 + j * 32 + (lane & 31)) * MG_LD + ko);
+        // codes k = ko .. ko + 7 of column wn 64 + 32 j + lane % 32: dword ko / 8
+        const f16x8 fb = dq(Bw[(ko >> 3) * MG_CT + wn * 64 + j * 32 + (lane & 31)]);
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh, fb, acc[j], 0, 0, 0);
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fl, fb, acc[j], 0, 0, 0);
       }
