@@ -764,7 +764,7 @@ def main():
             "gbs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "flops_per_launch": fl,
             "bytes_per_launch": nbytes, "replicas": r["replicas"],
             "kernel": ops.select_kernel("MatMulNBitsMlp", q["M"], q["K"], q["N"], 4, q["bs"]),
-            "traffic": traffic_of("mlp_prefill_m64_splitk.md", ops.select_kernel("MatMulNBitsMlp", q["M"], q["K"], q["N"], 4, q["bs"]))}
+            "traffic": traffic_of("mlp_prefill_m64_thin.md", ops.select_kernel("MatMulNBitsMlp", q["M"], q["K"], q["N"], 4, q["bs"]))}
     for name, q, kern_args in (("mlp_prefill_m2048", MLP2K, ("MatMulNBitsMlp", MLP2K["M"], MLP2K["K"], MLP2K["N"], 4,
                                                              MLP2K["bs"])),
                                ("qkv_prefill_m2048", QKV2K, ("MatMulNBitsQkv", QKV2K["M"], QKV2K["K"], QKV2K["Nq"], 4,
