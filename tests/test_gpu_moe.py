@@ -166,6 +166,8 @@ GROUPED = [
     (40, 512, 192, 6, 3, "relu", None, 1.0),        # ReLU, k = 3, a partial column tile (F1 = 192)
     (33, 256, 320, 5, 1, "swiglu", None, 3e5),      # x far beyond binary16: the row exponent scales it down
     (96, 128, 64, 16, 4, "swiglu", None, 1e-3),     # small x: scaled up before the binary16 split
+    (40, 256, 2048, 4, 2, "swiglu", None, 1.0),      # FC2 over two K splits (few tiles)
+    (36, 256, 4096, 3, 2, "relu", 5.0, 1.0),         # FC2 over four K splits
 ]
 
 

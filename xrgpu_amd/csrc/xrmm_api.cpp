@@ -457,7 +457,7 @@ int xrmm_qmoe(const void* input, const void* router, const void* fc1, const void
   a.sel = reinterpret_cast<int32_t*>(ws);
   a.wts = reinterpret_cast<float*>(ws + al(tokens * k * 4));
   a.h = reinterpret_cast<float*>(ws + 2 * al(tokens * k * 4));
-  const int64_t ksmax = xrmm::moe_fc2_segments_max(tokens, k, hidden, (a.I + 1023) / 1024);
+  const int64_t ksmax = xrmm::moe_yp_segments(tokens, k, hidden, a.I);
   a.yp = reinterpret_cast<float*>(ws + 2 * al(tokens * k * 4) + al(tokens * k * a.I * 4));
   a.cnt = reinterpret_cast<uint32_t*>(ws + 2 * al(tokens * k * 4) + al(tokens * k * a.I * 4) +
                                       al(tokens * k * ksmax * hidden * 4));

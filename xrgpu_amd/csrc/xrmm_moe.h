@@ -56,13 +56,34 @@ constexpr int64_t kMoeGroupMaxExperts = 4096;
 // row exponents of x (T).
 inline int64_t moe_list_words(int64_t T, int64_t k) { return 2 * (kMoeGroupMaxExperts + 1) + 2 * T * k + T; }
 
+// K splits of the grouped path's FC2 GEMM (64-pair x 256-column tiles over
+// K = I): enough for about 512 workgroups (two per CU) when the pairs would
+// make fewer, four at most, each split at least 16 steps of 64. From the
+// geometry alone (one tile per 64 pairs), so the workspace bound and the
+// launch agree.
+inline int64_t moe_group_fc2_splits(int64_t T, int64_t k, int64_t H, int64_t I) {
+  const int64_t tiles = ((T * k + 63) / 64) * ((H + 255) / 256);
+  if (tiles <= 0) return 1;
+  int64_t s = (512 + tiles - 1) / tiles;
+  if (s > 4) s = 4;
+  if (s > I / 64 / 16) s = I / 64 / 16;
+  return s < 1 ? 1 : s;
+}
+
+// FC2 partials per (token, slot) the workspace holds: the per-pair path's
+// segment bound (8-bit rows, which have the most steps) or the grouped
+// path's K splits, whichever is larger.
+inline int64_t moe_yp_segments(int64_t T, int64_t k, int64_t H, int64_t I) {
+  const int64_t a = moe_fc2_segments_max(T, k, H, (I + 1023) / 1024), b = moe_group_fc2_splits(T, k, H, I);
+  return a > b ? a : b;
+}
+
 // Workspace bytes for T tokens, k slots, hidden width H, intermediate width
-// I: five 256-byte-aligned regions (sel, wts, h, yp, cnt). The segment bound
-// uses 8-bit rows, which have the most steps; the last region holds either
-// path's words.
+// I: five 256-byte-aligned regions (sel, wts, h, yp, cnt); the last region
+// holds either path's words.
 inline int64_t moe_workspace_bytes(int64_t T, int64_t k, int64_t H, int64_t I) {
   auto al = [](int64_t b) { return (b + 255) / 256 * 256; };
-  const int64_t ks = moe_fc2_segments_max(T, k, H, (I + 1023) / 1024);
+  const int64_t ks = moe_yp_segments(T, k, H, I);
   const int64_t words = T * moe_tiles2(H) > moe_list_words(T, k) ? T * moe_tiles2(H) : moe_list_words(T, k);
   return al(T * k * 4) + al(T * k * 4) + al(T * k * I * 4) + al(T * k * ks * H * 4) + al(words * 4);
 }

@@ -618,7 +618,8 @@ bool moe_grouped_ok(const MoeArgs& a) {
   const int64_t lim = int64_t(1) << 31;
   // 32-bit row-tile grid and pair indices (the workspace's last region holds
   // the lists for up to kMoeGroupMaxExperts experts)
-  return a.F1 * a.H / 2 < lim && a.H * a.I / 2 < lim && a.T * a.k * a.I < lim && a.T * a.k * a.H < lim;
+  return a.F1 * a.H / 2 < lim && a.H * a.I / 2 < lim && a.T * a.k * a.I < lim &&
+         a.T * a.k * a.H * moe_group_fc2_splits(a.T, a.k, a.H, a.I) < lim;
 }
 
 const char* moe_kernel_name(const MoeArgs& a) {
@@ -626,7 +627,9 @@ const char* moe_kernel_name(const MoeArgs& a) {
 }
 
 namespace {
-hipError_t launch_grouped(const MoeArgs& a, hipStream_t st) {
+hipError_t launch_grouped(const MoeArgs& a0, hipStream_t st) {
+  MoeArgs a = a0;
+  a.ks = static_cast<int>(moe_group_fc2_splits(a.T, a.k, a.H, a.I));  // FC2 K splits (the combine sums them)
   MgLists g;
   int32_t* base = reinterpret_cast<int32_t*>(a.cnt);
   g.off = base;
@@ -651,9 +654,9 @@ hipError_t launch_grouped(const MoeArgs& a, hipStream_t st) {
     return e;
   if (hipError_t e = raise_lds_cap(reinterpret_cast<const void*>(k2), static_cast<int>(MG_LDS), d3); e != hipSuccess) return e;
   const int nct1 = static_cast<int>((a.F1 + MG_CT - 1) / MG_CT), nct2 = static_cast<int>((a.H + MG_CT - 1) / MG_CT);
-  if (rtmax * nct1 > 0x7FFFFFFF || rtmax * nct2 > 0x7FFFFFFF) return hipErrorInvalidValue;
+  if (rtmax * nct1 > 0x7FFFFFFF || rtmax * nct2 * a.ks > 0x7FFFFFFF) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k1, dim3(static_cast<uint32_t>(rtmax * nct1)), dim3(MG_T), MG_LDS, st, a, g, nct1);
-  hipLaunchKernelGGL(k2, dim3(static_cast<uint32_t>(rtmax * nct2)), dim3(MG_T), MG_LDS, st, a, g, nct2);
+  hipLaunchKernelGGL(k2, dim3(static_cast<uint32_t>(rtmax * nct2 * a.ks)), dim3(MG_T), MG_LDS, st, a, g, nct2);
   hipLaunchKernelGGL(k_moe_combine, dim3(static_cast<uint32_t>((a.T * a.H + 255) / 256)), dim3(256), 0, st, a);
   return hipGetLastError();
 }

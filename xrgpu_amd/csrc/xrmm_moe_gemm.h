@@ -13,9 +13,11 @@
 //     (SwiGLU rows 2j / 2j + 1 sit in neighbouring lanes) and writes h[pair],
 //     folding each pair's largest |h| into an arrival-order-free atomic max;
 //  4. k_moe_ggemm FC2: rows = the pairs' h, columns = the expert's FC2 rows,
-//     K = I; writes yp[pair] (row scale applied);
+//     K = I, split over a.ks workgroups when the tiles are few; writes each
+//     split's yp[pair][split] (row scale applied);
 //  5. k_moe_combine: y[t] = sum over slots (ascending expert index) of
-//     w * yp, one fused multiply-add per slot in slot order.
+//     w * (the slot's splits summed in split order), one fused multiply-add
+//     per slot in slot order.
 //
 // Arithmetic. The codes enter v_mfma_f32_32x32x16_f16 as the exact binary16
 // integers code - 8 (no scale), the row scale multiplies the float32 sum. The
@@ -162,7 +164,10 @@ __global__ __launch_bounds__(MG_T, 2) void k_moe_ggemm(MoeArgs a, MgLists g, int
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
   const int E = static_cast<int>(a.E);
-  const int rt = static_cast<int>(blockIdx.x) / nct, ct = static_cast<int>(blockIdx.x) % nct;
+  // FC2: workgroup b is split b % ks of tile b / ks
+  const int ks2 = FC2 ? a.ks : 1;
+  const int sp = static_cast<int>(blockIdx.x) % ks2, tb = static_cast<int>(blockIdx.x) / ks2;
+  const int rt = tb / nct, ct = tb % nct;
   const int total = g.toff[E];
   if (rt >= total) return;  // uniform: the grid is an upper bound of the row tiles
   // expert of this row tile: the last e with toff[e] <= rt
@@ -207,7 +212,10 @@ __global__ __launch_bounds__(MG_T, 2) void k_moe_ggemm(MoeArgs a, MgLists g, int
   const rsrc_t rB = mk_rsrc(Wb, static_cast<uint32_t>(Nd) * rowb);
   const bool bval = n0 + bcol < Nd;
   const uint32_t boff = bval ? static_cast<uint32_t>(n0 + bcol) * rowb : OOB;
-  const int ksteps = (Kd + MG_K - 1) / MG_K;
+  // this workgroup's K steps [kstep0, kstep0 + ksteps)
+  const int kall = (Kd + MG_K - 1) / MG_K, kper = (kall + ks2 - 1) / ks2;
+  const int kstep0 = sp * kper;
+  const int ksteps = kall - kstep0 < kper ? kall - kstep0 : kper;
 
   struct Regs {
     u32x4 a[2];
@@ -216,10 +224,10 @@ __global__ __launch_bounds__(MG_T, 2) void k_moe_ggemm(MoeArgs a, MgLists g, int
   // steps past the end reload the last one (never staged)
   auto gload = [&](Regs& r, int ks) {
     const bool ok = ks < ksteps;
-    const float* pa = Arow + (ok ? ks : ksteps - 1) * MG_K;
+    const float* pa = Arow + (kstep0 + (ok ? ks : ksteps - 1)) * MG_K;
     r.a[0] = *reinterpret_cast<const u32x4*>(pa);
     r.a[1] = *reinterpret_cast<const u32x4*>(pa + 4);
-    r.b = bld16(rB, (ok ? boff : OOB) + static_cast<uint32_t>(ks * MG_K / 2 + bh * 16), 0);
+    r.b = bld16(rB, (ok ? boff : OOB) + static_cast<uint32_t>((kstep0 + ks) * MG_K / 2 + bh * 16), 0);
   };
   // A: scaled, split into binary16 hi / lo in the pair order of the codes;
   // B: the raw code dwords (dequantised when a fragment is read)
@@ -321,7 +329,7 @@ __global__ __launch_bounds__(MG_T, 2) void k_moe_ggemm(MoeArgs a, MgLists g, int
       const int p = s_pair[r];
       const float v = acc[j][q] * sc * s_ru[r];
       if constexpr (FC2) {
-        if (p >= 0 && c < Nd) a.yp[static_cast<int64_t>(p) * a.H + c] = v;
+        if (p >= 0 && c < Nd) a.yp[(static_cast<int64_t>(p) * ks2 + sp) * a.H + c] = v;
       } else if constexpr (ST == MG_FC1_SWIGLU) {
         // gate = row 2m (even lane), linear = row 2m + 1 (odd lane)
         const float other = __shfl_xor(v, 1, 64);
@@ -352,7 +360,8 @@ __global__ __launch_bounds__(MG_T, 2) void k_moe_ggemm(MoeArgs a, MgLists g, int
   }
 }
 
-// y[t][n] = sum over slots s of w[t k + s] * yp[t k + s][n], in slot order.
+// y[t][n] = sum over slots s of w[t k + s] * yp[t k + s][n], in slot order,
+// each slot's a.ks FC2 splits summed first in split order.
 __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= a.T * a.H) return;
@@ -360,7 +369,10 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
   float y = 0.f;
   for (int s = 0; s < a.k; ++s) {
     const int64_t pair = t * a.k + s;
-    y = __builtin_fmaf(a.wts[pair], a.yp[pair * a.H + n], y);
+    const float* part = a.yp + pair * a.ks * a.H + n;
+    float v = part[0];
+    for (int sp = 1; sp < a.ks; ++sp) v += part[static_cast<int64_t>(sp) * a.H];
+    y = __builtin_fmaf(a.wts[pair], v, y);
   }
   a.y[i] = y;
 }
