@@ -327,11 +327,11 @@ void xrmm_destroy(xrmm_op* op);
  * at least xrmm_qmoe_workspace_bytes(T, k, H, I) bytes (routing table, the
  * activated FC1 outputs, per-slot FC2 partials and their arrival counters or
  * per-expert pair lists); calls that share a workspace must not overlap.
- * With 4-bit codes, row scales, H and I multiples of 64, at most 4096 experts
- * and at least 32 (token, slot) pairs, the pairs are grouped by expert and
- * each expert's FC1 and FC2 run as one MFMA GEMM over its pairs
- * ("qmoe_grouped"); other geometries run one pass per pair ("qmoe_rows") or
- * the scalar path. */
+ * With 4- or 8-bit codes, row scales or blocks of 32 or more codes, H and I
+ * multiples of 64, at most 4096 experts and at least 32 (token, slot) pairs,
+ * the pairs are grouped by expert and each expert's FC1 and FC2 run as one
+ * MFMA GEMM over its pairs ("qmoe_grouped"); other geometries run one pass
+ * per pair ("qmoe_rows") or the scalar path. */
 int64_t xrmm_qmoe_workspace_bytes(int64_t tokens, int32_t k, int64_t hidden, int64_t inter);
 int xrmm_qmoe(const void* input, const void* router, const void* fc1, const void* fc1_scales, const void* fc2,
               const void* fc2_scales, void* output, void* workspace, int64_t workspace_bytes, int64_t tokens,

@@ -176,15 +176,17 @@ def test_kernel_selection_bits(op, M, K, N, bits, bs, dtype, zp, expect):
     (256, 4096, 4, 12800, 2, 4, 0, nat.ACT["swiglu"], 1, "qmoe_grouped"),   # many tokens, 4-bit row scales
     (16, 2048, 64, 1536, 2, 4, 0, nat.ACT["swiglu"], 1, "qmoe_grouped"),    # 32 (token, slot) pairs
     (15, 2048, 64, 1536, 2, 4, 0, nat.ACT["swiglu"], 1, "qmoe_rows"),       # 30 pairs: one pass per pair
-    (256, 4096, 4, 12800, 2, 4, 64, nat.ACT["swiglu"], 1, "qmoe_rows"),     # block scales
-    (256, 4096, 4, 12800, 2, 8, 0, nat.ACT["swiglu"], 1, "qmoe_rows"),      # 8-bit codes
+    (256, 4096, 4, 12800, 2, 4, 64, nat.ACT["swiglu"], 1, "qmoe_grouped"),  # block scales
+    (256, 4096, 4, 12800, 2, 8, 0, nat.ACT["swiglu"], 1, "qmoe_grouped"),   # 8-bit codes
+    (256, 4096, 4, 12800, 2, 4, 16, nat.ACT["swiglu"], 1, "qmoe_rows"),     # blocks of 16: one pass per pair
     (256, 4000, 4, 12800, 2, 4, 0, nat.ACT["swiglu"], 1, "qmoe_rows"),      # H not a multiple of 64
     (64, 256, 4097, 256, 1, 4, 0, nat.ACT["relu"], 0, "qmoe_scalar"),       # more experts than either fast path counts
 ])
 def test_qmoe_kernel_selection(T, H, E, F1, k, bits, bs, act, fusion, expect):
-    """The grouped-expert path takes 4-bit row-scaled experts with at least
-    32 pairs; the workspace holds its lists (two offsets per expert up to
-    4096 experts, two words per pair, one per token)."""
+    """The grouped-expert path takes 4- or 8-bit experts with row scales or
+    power-of-two blocks dividing H and I, and at least 32 pairs; the
+    workspace holds its lists (two offsets per expert up to 4096 experts, two
+    words per pair, one per token)."""
     lib = nat.lib()
     assert lib.xrmm_qmoe_kernel(T, H, E, F1, k, bits, bs, act, fusion).decode() == expect
     I = F1 // 2 if fusion else F1

@@ -188,6 +188,36 @@ def test_grouped_experts(gpu, T, H, I, E, k, act, limit, xs):
     assert np.array_equal(got, run_gpu(i, at))
 
 
+GROUPED_BLOCKS = [
+    # T, H, I, E, k, activation, bits, block_size: block scales and 8-bit
+    # codes on the grouped-expert GEMMs
+    (48, 512, 512, 6, 2, "swiglu", 4, 32),      # two blocks per K step
+    (40, 256, 1024, 4, 2, "relu", 8, 64),       # 8-bit codes, one block per step
+    (36, 256, 2048, 3, 2, "swiglu", 4, 128),    # a block over two steps; FC2 in two K splits
+    (33, 128, 256, 5, 1, "relu", 8, 32),        # 8-bit, two blocks per K step
+    (64, 256, 4096, 2, 2, "relu", 4, 256),      # FC2 in four K splits of whole blocks
+    (36, 2048, 4096, 2, 2, "relu", 4, 2048),    # splits past the last block hold zero partials
+    (72, 384, 640, 9, 3, "swiglu", 8, 32),      # 8-bit, odd tile counts
+]
+
+
+@pytest.mark.parametrize("T,H,I,E,k,act,bits,bs", GROUPED_BLOCKS)
+def test_grouped_block_scales(gpu, T, H, I, E, k, act, bits, bs):
+    """Float32 bar against the oracle with per-block scales (each block's sum
+    scaled before it joins the row's sum) and 8-bit codes (c - 128 exact in
+    binary16), plus bitwise-repeatable outputs."""
+    rng = np.random.default_rng(T * 5 + H + I + E + k + bits + bs)
+    sw = act == "swiglu"
+    i = rand_case(rng, T, H, I, E, bits, bs, sw)
+    at = dict(k=k, activation=act, swiglu_fusion=1 if sw else 0, bits=bits, block_size=bs, alpha=1.702 if sw else 1.0,
+              beta=1.0 if sw else 0.0, swiglu_limit=None)
+    assert ops().qmoe_kernel(T, H, E, 2 * I if sw else I, k, bits, bs, act, 1 if sw else 0) == "qmoe_grouped"
+    got = run_gpu(i, at)
+    ok, err, lim = O.tolerance_ok(got, run_oracle(i, at), np.float32)
+    assert ok, f"max|d|={err} > {lim}"
+    assert np.array_equal(got, run_gpu(i, at))
+
+
 def test_grouped_nonfinite_rows(gpu):
     """+-Inf and NaN activations reach the sums as the reference's float32
     products do (the binary16 split keeps lo = 0 for them); other tokens are

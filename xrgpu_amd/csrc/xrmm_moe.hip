@@ -611,7 +611,12 @@ bool moe_fast_ok(const MoeArgs& a) {
 #define XRMM_MOE_GROUP_MIN 32
 #endif
 bool moe_grouped_ok(const MoeArgs& a) {
-  if (a.bits != 4 || a.bs != 0 || a.H % 64 != 0 || a.I % 64 != 0 || a.E > kMoeGroupMaxExperts) return false;
+  if ((a.bits != 4 && a.bits != 8) || a.H % 64 != 0 || a.I % 64 != 0 || a.E > kMoeGroupMaxExperts) return false;
+  // row scales, or power-of-two blocks of at least 32 codes that divide both
+  // rows (blocks of 16, one scaled sum per MFMA slice, need more registers
+  // than a wave has and spill: 5.6 ms against 0.95 ms for blocks of 64 at
+  // T = 256 on the Mixtral experts)
+  if (a.bs != 0 && (a.bs < 32 || (a.bs & (a.bs - 1)) != 0 || a.H % a.bs != 0 || a.I % a.bs != 0)) return false;
   if (a.T * a.k < XRMM_MOE_GROUP_MIN) return false;
   if (!aligned16(a.x) || !aligned16(a.fc1) || !aligned16(a.fc2) || !aligned16(a.h) || !aligned16(a.yp)) return false;
   if (a.act == XRMM_ACT_SWIGLU_CODE && a.F1 != 2 * a.I) return false;
@@ -627,6 +632,35 @@ const char* moe_kernel_name(const MoeArgs& a) {
 }
 
 namespace {
+// One grouped GEMM launch of stage ST, BITS-bit codes, block mode BKM.
+template <int ST, int BITS, int BKM>
+hipError_t mg_launch(const MoeArgs& a, const MgLists& g, int nct, int64_t grid, hipStream_t st) {
+  auto kern = k_moe_ggemm<ST, BITS, BKM>;
+  constexpr size_t lds = mg_lds<BITS>();
+  if constexpr (lds > 64 * 1024) {
+    static std::atomic<int> done[kMaxDevices];  // per instantiation and device
+    if (hipError_t e = raise_lds_cap(reinterpret_cast<const void*>(kern), static_cast<int>(lds), done); e != hipSuccess)
+      return e;
+  }
+  hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(grid)), dim3(MG_T), lds, st, a, g, nct);
+  return hipGetLastError();
+}
+
+template <int ST, int BITS>
+hipError_t mg_launch_b(const MoeArgs& a, const MgLists& g, int nct, int64_t grid, hipStream_t st) {
+  switch (mg_block_mode(a.bs)) {  // blocks of 16 (mode 1) do not take this path
+    case 0: return mg_launch<ST, BITS, 0>(a, g, nct, grid, st);
+    case 2: return mg_launch<ST, BITS, 2>(a, g, nct, grid, st);
+    case 4: return mg_launch<ST, BITS, 4>(a, g, nct, grid, st);
+    default: return mg_launch<ST, BITS, 8>(a, g, nct, grid, st);
+  }
+}
+
+template <int ST>
+hipError_t mg_launch_s(const MoeArgs& a, const MgLists& g, int nct, int64_t grid, hipStream_t st) {
+  return a.bits == 8 ? mg_launch_b<ST, 8>(a, g, nct, grid, st) : mg_launch_b<ST, 4>(a, g, nct, grid, st);
+}
+
 hipError_t launch_grouped(const MoeArgs& a0, hipStream_t st) {
   MoeArgs a = a0;
   a.ks = static_cast<int>(moe_group_fc2_splits(a.T, a.k, a.H, a.I));  // FC2 K splits (the combine sums them)
@@ -645,18 +679,12 @@ hipError_t launch_grouped(const MoeArgs& a0, hipStream_t st) {
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   // row tiles: at most one partial tile per expert beyond the full ones
   const int64_t rtmax = (a.T * a.k + MG_RT - 1) / MG_RT + a.E;
-  static std::atomic<int> d1[kMaxDevices], d2[kMaxDevices], d3[kMaxDevices];
-  auto k1 = a.act == XRMM_ACT_SWIGLU_CODE ? k_moe_ggemm<MG_FC1_SWIGLU> : k_moe_ggemm<MG_FC1_RELU>;
-  auto k2 = k_moe_ggemm<MG_FC2>;
-  if (hipError_t e = raise_lds_cap(reinterpret_cast<const void*>(k1), static_cast<int>(MG_LDS),
-                                   a.act == XRMM_ACT_SWIGLU_CODE ? d1 : d2);
-      e != hipSuccess)
-    return e;
-  if (hipError_t e = raise_lds_cap(reinterpret_cast<const void*>(k2), static_cast<int>(MG_LDS), d3); e != hipSuccess) return e;
   const int nct1 = static_cast<int>((a.F1 + MG_CT - 1) / MG_CT), nct2 = static_cast<int>((a.H + MG_CT - 1) / MG_CT);
   if (rtmax * nct1 > 0x7FFFFFFF || rtmax * nct2 * a.ks > 0x7FFFFFFF) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k1, dim3(static_cast<uint32_t>(rtmax * nct1)), dim3(MG_T), MG_LDS, st, a, g, nct1);
-  hipLaunchKernelGGL(k2, dim3(static_cast<uint32_t>(rtmax * nct2 * a.ks)), dim3(MG_T), MG_LDS, st, a, g, nct2);
+  const hipError_t e1 = a.act == XRMM_ACT_SWIGLU_CODE ? mg_launch_s<MG_FC1_SWIGLU>(a, g, nct1, rtmax * nct1, st)
+                                                      : mg_launch_s<MG_FC1_RELU>(a, g, nct1, rtmax * nct1, st);
+  if (e1 != hipSuccess) return e1;
+  if (hipError_t e = mg_launch_s<MG_FC2>(a, g, nct2, rtmax * nct2 * a.ks, st); e != hipSuccess) return e;
   hipLaunchKernelGGL(k_moe_combine, dim3(static_cast<uint32_t>((a.T * a.H + 255) / 256)), dim3(256), 0, st, a);
   return hipGetLastError();
 }

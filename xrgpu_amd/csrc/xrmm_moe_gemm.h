@@ -38,11 +38,23 @@ constexpr int MG_CT = 256;  // columns per tile
 constexpr int MG_K = 64;    // K step
 constexpr int MG_LD = MG_K + 8;
 constexpr int MG_T = 512;   // threads: 8 waves, 2 (rows of 32) x 4 (columns of 64)
-constexpr int MG_BW = MG_K / 8;  // dwords of codes per column and K step
 // halfs per stage: A hi, A lo (rows of MG_LD), then the raw codes as
-// [dword of the step][column] (a fragment's eight codes are one dword)
-constexpr int MG_STAGE = 2 * MG_RT * MG_LD + MG_BW * MG_CT * 2;
-constexpr size_t MG_LDS = 2 * MG_STAGE * sizeof(_Float16);
+// [fragment of the step][column], a fragment being eight codes (one dword
+// of 4-bit codes, two of 8-bit codes)
+template <int BITS>
+constexpr int mg_stage() {
+  return 2 * MG_RT * MG_LD + (MG_K / 8) * MG_CT * (BITS / 4) * 2;
+}
+template <int BITS>
+constexpr size_t mg_lds() {
+  return 2 * mg_stage<BITS>() * sizeof(_Float16);
+}
+
+// Block-scale modes of the GEMM: 0 = one scale per row (applied to the row's
+// sum in the epilogue); 1, 2, 4 = blocks of 16, 32, 64 codes (a block's sum
+// is scaled and added every 1, 2, 4 MFMA K slices); 8 = blocks of 128 or
+// more (scaled at the end of every block_size / 64 K steps).
+inline int mg_block_mode(int bs) { return bs == 0 ? 0 : bs == 16 ? 1 : bs == 32 ? 2 : bs == 64 ? 4 : 8; }
 
 // Lists of the grouped path, inside the workspace's counter region.
 struct MgLists {
@@ -150,10 +162,13 @@ __device__ __forceinline__ float mg_half_max(float v) {
   return v;
 }
 
-// One 64-pair x 256-column tile of an expert's matrix.
-template <int ST>
+// One 64-pair x 256-column tile of an expert's matrix; BITS-bit codes, block
+// mode BKM (mg_block_mode).
+template <int ST, int BITS, int BKM>
 __global__ __launch_bounds__(MG_T, 2) void k_moe_ggemm(MoeArgs a, MgLists g, int nct) {
   constexpr bool FC2 = ST == MG_FC2;
+  constexpr int MG_STAGE = mg_stage<BITS>();
+  constexpr int BW = BITS / 4;  // dwords per fragment
   extern __shared__ __align__(16) unsigned char smem[];
   f16* lds = reinterpret_cast<f16*>(smem);
   __shared__ int s_pair[MG_RT];
@@ -207,34 +222,42 @@ __global__ __launch_bounds__(MG_T, 2) void k_moe_ggemm(MoeArgs a, MgLists g, int
   const float* Asrc = FC2 ? a.h : a.x;
   const float* Arow = Asrc + (FC2 ? static_cast<int64_t>(apair) * a.I : static_cast<int64_t>(apair / a.k) * a.H) + agrp * 8;
   const int bcol = tid >> 1, bh = tid & 1;
-  const uint32_t rowb = static_cast<uint32_t>(Kd) / 2u;  // bytes per expert row (4-bit codes)
+  const uint32_t rowb = static_cast<uint32_t>(Kd) * BITS / 8u;  // bytes per expert row
   const uint8_t* Wb = FC2 ? a.fc2 + static_cast<int64_t>(e) * a.H * rowb : a.fc1 + static_cast<int64_t>(e) * a.F1 * rowb;
   const rsrc_t rB = mk_rsrc(Wb, static_cast<uint32_t>(Nd) * rowb);
   const bool bval = n0 + bcol < Nd;
   const uint32_t boff = bval ? static_cast<uint32_t>(n0 + bcol) * rowb : OOB;
-  // this workgroup's K steps [kstep0, kstep0 + ksteps)
-  const int kall = (Kd + MG_K - 1) / MG_K, kper = (kall + ks2 - 1) / ks2;
+  // this workgroup's K steps [kstep0, kstep0 + ksteps); splits of blocks of
+  // 128 codes or more hold whole blocks (a split past the end holds none and
+  // writes zero partials)
+  const int kall = (Kd + MG_K - 1) / MG_K;
+  const int bsteps = BKM == 8 ? a.bs / MG_K : 1;  // K steps per block
+  const int kper = ((kall + ks2 - 1) / ks2 + bsteps - 1) / bsteps * bsteps;
   const int kstep0 = sp * kper;
   const int ksteps = kall - kstep0 < kper ? kall - kstep0 : kper;
 
   struct Regs {
     u32x4 a[2];
-    u32x4 b;
+    u32x4 b[BW];
   };
   // steps past the end reload the last one (never staged)
   auto gload = [&](Regs& r, int ks) {
     const bool ok = ks < ksteps;
-    const float* pa = Arow + (kstep0 + (ok ? ks : ksteps - 1)) * MG_K;
+    int kst = kstep0 + (ok ? ks : ksteps - 1);
+    kst = kst < kall - 1 ? kst : kall - 1;
+    const float* pa = Arow + kst * MG_K;
     r.a[0] = *reinterpret_cast<const u32x4*>(pa);
     r.a[1] = *reinterpret_cast<const u32x4*>(pa + 4);
-    r.b = bld16(rB, (ok ? boff : OOB) + static_cast<uint32_t>((kstep0 + ks) * MG_K / 2 + bh * 16), 0);
+#pragma unroll
+    for (int i = 0; i < BW; ++i)
+      r.b[i] = bld16(rB, (ok ? boff : OOB) + static_cast<uint32_t>((kstep0 + ks) * MG_K * BITS / 8 + (bh * BW + i) * 16), 0);
   };
   // A: scaled, split into binary16 hi / lo in the pair order of the codes;
   // B: the raw code dwords (dequantised when a fragment is read)
   auto sstore = [&](const Regs& r, int stage) {
     f16* Ah = lds + stage * MG_STAGE;
     f16* Al = Ah + MG_RT * MG_LD;
-    uint32_t* Bw = reinterpret_cast<uint32_t*>(Al + MG_RT * MG_LD);
+    uint32_t* Bw = reinterpret_cast<uint32_t*>(Al + MG_RT * MG_LD);  // [fragment][column][BW dwords]
     f16x8 vh, vl;
     // the eight floats by name first: this compiler folds v[i >> 2][i & 3]
     // over an array of vectors to element 0 of each vector
@@ -249,30 +272,81 @@ __global__ __launch_bounds__(MG_T, 2) void k_moe_ggemm(MoeArgs a, MgLists g, int
     }
     *reinterpret_cast<f16x8*>(Ah + arow * MG_LD + agrp * 8) = vh;
     *reinterpret_cast<f16x8*>(Al + arow * MG_LD + agrp * 8) = vl;
-    // dword 4 bh + d of the step (codes 32 bh + 8 d .. + 7) of column bcol
+    // fragment 4 bh + d of the step (codes 32 bh + 8 d .. + 7) of column bcol
 #pragma unroll
-    for (int d = 0; d < 4; ++d) Bw[(4 * bh + d) * MG_CT + bcol] = r.b[d];
+    for (int d = 0; d < 4; ++d) {
+      if constexpr (BW == 1) {
+        Bw[(4 * bh + d) * MG_CT + bcol] = r.b[0][d];
+      } else {
+        const u32x2 v = {r.b[d >> 1][2 * (d & 1)], r.b[d >> 1][2 * (d & 1) + 1]};
+        *reinterpret_cast<u32x2*>(Bw + ((4 * bh + d) * MG_CT + bcol) * 2) = v;
+      }
+    }
   };
-  // a fragment's eight codes -> c - 8 as exact binary16, pair order
-  // (c0 c4 c1 c5 c2 c6 c3 c7, the activations' staging order)
+  // a fragment's eight codes -> c - 2^(bits - 1) as exact binary16, pair
+  // order (c0 c4 c1 c5 c2 c6 c3 c7, the activations' staging order)
   const f16x2 n1032 = {static_cast<f16>(-1032.f), static_cast<f16>(-1032.f)};
   const f16x2 inv16 = {static_cast<f16>(0.0625f), static_cast<f16>(0.0625f)};
   const f16x2 n72 = {static_cast<f16>(-72.f), static_cast<f16>(-72.f)};
-  auto dq = [&](uint32_t x) {
-    const uint32_t magic = 0x64006400u, x8 = x >> 8;
-    const f16x2 d0 = as_h2(and_or(x, 0x000F000Fu, magic)) + n1032;
-    const f16x2 d1 = __builtin_elementwise_fma(as_h2(and_or(x, 0x00F000F0u, magic)), inv16, n72);
-    const f16x2 d2 = as_h2(and_or(x8, 0x000F000Fu, magic)) + n1032;
-    const f16x2 d3 = __builtin_elementwise_fma(as_h2(and_or(x8, 0x00F000F0u, magic)), inv16, n72);
-    return f16x8{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+  const f16x2 n1152 = {static_cast<f16>(-1152.f), static_cast<f16>(-1152.f)};
+  auto dq = [&](const uint32_t* w) {
+    const uint32_t magic = 0x64006400u;
+    if constexpr (BW == 1) {
+      const uint32_t x = w[0], x8 = x >> 8;
+      const f16x2 d0 = as_h2(and_or(x, 0x000F000Fu, magic)) + n1032;
+      const f16x2 d1 = __builtin_elementwise_fma(as_h2(and_or(x, 0x00F000F0u, magic)), inv16, n72);
+      const f16x2 d2 = as_h2(and_or(x8, 0x000F000Fu, magic)) + n1032;
+      const f16x2 d3 = __builtin_elementwise_fma(as_h2(and_or(x8, 0x00F000F0u, magic)), inv16, n72);
+      return f16x8{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+    } else {
+      // bytes c0..c3 in w[0], c4..c7 in w[1]: (c_i, c_i+4) into the low bytes
+      // of a half pair, then 0x64 above each: 1024 + c exactly
+      const uint32_t x0 = w[0], x1 = w[1];
+      const f16x2 d0 = as_h2(__builtin_amdgcn_perm(x1, x0, 0x0c040c00u) | magic) + n1152;
+      const f16x2 d1 = as_h2(__builtin_amdgcn_perm(x1, x0, 0x0c050c01u) | magic) + n1152;
+      const f16x2 d2 = as_h2(__builtin_amdgcn_perm(x1, x0, 0x0c060c02u) | magic) + n1152;
+      const f16x2 d3 = as_h2(__builtin_amdgcn_perm(x1, x0, 0x0c070c03u) | magic) + n1152;
+      return f16x8{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+    }
   };
 
-  f32x16 acc[2];
+  // block sums (acc) and, with block scales, the scaled running sums (yacc)
+  f32x16 acc[2], yacc[BKM ? 2 : 1];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int q = 0; q < 16; ++q) acc[j][q] = 0.f;
-  auto mfmas = [&](int stage) {
+#pragma unroll
+  for (int j = 0; j < (BKM ? 2 : 1); ++j)
+#pragma unroll
+    for (int q = 0; q < 16; ++q) yacc[j][q] = 0.f;
+  // the scales of this lane's two columns: [E, Nd] (row scales) or
+  // [E, Nd, Kd / block_size]
+  const int nblk = BKM ? Kd / a.bs : 1;
+  const float* S = FC2 ? a.s2 + static_cast<int64_t>(e) * a.H * nblk : a.s1 + static_cast<int64_t>(e) * a.F1 * nblk;
+  int scol[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int c = n0 + wn * 64 + j * 32 + (lane & 31);
+    scol[j] = (c < Nd ? c : Nd - 1) * nblk;
+  }
+  // block flushes per step: 4 / BKM inside the step, or one at its end
+  constexpr int NFL = BKM == 0 ? 0 : BKM == 8 ? 1 : 4 / BKM;
+  constexpr int NSL = NFL ? NFL : 1;
+  // (kept in place by scheduling barriers: moved among the next block's
+  // MFMAs it would hold two copies of the accumulators)
+  auto flush = [&](const float (&sc)[2]) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        yacc[BKM ? j : 0][q] = __builtin_fmaf(sc[j], acc[j][q], yacc[BKM ? j : 0][q]);
+        acc[j][q] = 0.f;
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto mfmas = [&](int stage, const float (&sl)[NSL][2]) {
     const f16* Ah = lds + stage * MG_STAGE;
     const f16* Al = Ah + MG_RT * MG_LD;
     const uint32_t* Bw = reinterpret_cast<const uint32_t*>(Al + MG_RT * MG_LD);
@@ -284,10 +358,26 @@ __global__ __launch_bounds__(MG_T, 2) void k_moe_ggemm(MoeArgs a, MgLists g, int
       const f16x8 fl = *reinterpret_cast<const f16x8*>(Al + ar * MG_LD + ko);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        // codes k = ko .. ko + 7 of column wn 64 + 32 j + lane % 32: dword ko / 8
-        const f16x8 fb = dq(Bw[(ko >> 3) * MG_CT + wn * 64 + j * 32 + (lane & 31)]);
+        // codes k = ko .. ko + 7 of column wn 64 + 32 j + lane % 32: fragment ko / 8
+        const f16x8 fb = dq(Bw + ((ko >> 3) * MG_CT + wn * 64 + j * 32 + (lane & 31)) * BW);
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh, fb, acc[j], 0, 0, 0);
         acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fl, fb, acc[j], 0, 0, 0);
+      }
+      if constexpr (BKM >= 1 && BKM <= 4) {
+        if ((kk + 1) % BKM == 0) flush(sl[kk / BKM]);
+      }
+    }
+  };
+  // the step's block scales, loaded before its fill loads (so waiting for
+  // them never waits for the fill)
+  auto sload = [&](int ks, float (&sl)[NSL][2]) {
+    if constexpr (NFL > 0) {
+      const int kg = kstep0 + (ks < ksteps ? ks : ksteps - 1);  // in range
+#pragma unroll
+      for (int f = 0; f < NFL; ++f) {
+        const int b = BKM == 8 ? (kg * MG_K) / a.bs : kg * NFL + f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) sl[f][j] = S[scol[j] + b];
       }
     }
   };
@@ -297,37 +387,43 @@ __global__ __launch_bounds__(MG_T, 2) void k_moe_ggemm(MoeArgs a, MgLists g, int
   // step ks on stage ks % 2: `nxt` holds step ks + 1 (stored to the other
   // stage during the step), `fill` receives step ks + 2
   auto step = [&](int ks, int stage, Regs& nxt, Regs& fill) {
+    float sl[NSL][2];
+    sload(ks, sl);
     gload(fill, ks + 2);
-    mfmas(stage);
+    mfmas(stage, sl);
+    if constexpr (BKM == 8) {
+      if ((kstep0 + ks + 1) % bsteps == 0) flush(sl[0]);
+    }
     if (ks + 1 < ksteps) sstore(nxt, stage ^ 1);
     __syncthreads();
   };
-  Regs r0, r1;
-  gload(r0, 0);
-  gload(r1, 1);
-  sstore(r0, 0);
-  __syncthreads();
-  int ks = 0;
-  for (; ks + 1 < ksteps; ks += 2) {
-    step(ks, 0, r1, r0);
-    step(ks + 1, 1, r0, r1);
+  if (ksteps > 0) {  // uniform: a split past the end keeps zero sums
+    Regs r0, r1;
+    gload(r0, 0);
+    gload(r1, 1);
+    sstore(r0, 0);
+    __syncthreads();
+    int ks = 0;
+    for (; ks + 1 < ksteps; ks += 2) {
+      step(ks, 0, r1, r0);
+      step(ks + 1, 1, r0, r1);
+    }
+    if (ks < ksteps) step(ks, 0, r1, r0);
   }
-  if (ks < ksteps) step(ks, 0, r1, r0);
 
   // ---- epilogue: lane holds D[8 (q / 4) + 4 (lane / 32) + q % 4][lane % 32]
-  const float* S = FC2 ? a.s2 + static_cast<int64_t>(e) * a.H : a.s1 + static_cast<int64_t>(e) * a.F1;
   float rmax[16];
 #pragma unroll
   for (int q = 0; q < 16; ++q) rmax[q] = 0.f;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int c = n0 + wn * 64 + j * 32 + (lane & 31);
-    const float sc = c < Nd ? S[c] : 0.f;
+    const float sc = BKM ? 1.f : (c < Nd ? S[c] : 0.f);
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       const int r = wm * 32 + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
       const int p = s_pair[r];
-      const float v = acc[j][q] * sc * s_ru[r];
+      const float v = (BKM ? yacc[BKM ? j : 0][q] : acc[j][q] * sc) * s_ru[r];
       if constexpr (FC2) {
         if (p >= 0 && c < Nd) a.yp[(static_cast<int64_t>(p) * ks2 + sp) * a.H + c] = v;
       } else if constexpr (ST == MG_FC1_SWIGLU) {
