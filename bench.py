@@ -32,7 +32,7 @@ SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048
          "bnb4_nf4_m1": 7, "gbq_embed_t2048": 8, "int8a_decode_m1": 1, "f32_k2048_m1": 0,
          "mlp_prefill_m64": 9, "prefill_m2048_prepacked": 4, "down_proj_m64": 10, "mlp_prefill_m2048": 13,
          "qkv_prefill_m2048": 14, "q8_f32_decode_m1": 15, "f32_prefill_m64": 16, "qmoe_prefill_t256": 17,
-         "q8_f16_decode_m1": 18}
+         "q8_f16_decode_m1": 18, "f32_prefill_m512": 19, "q2_f16_prefill_m128": 20}
 # The CPU-oracle workload on the GPU: MatMulNBits float32, M=1, K=N=2048,
 # block_size 32, packed zero points (2,703,360 algorithmic bytes per call)
 F32 = dict(M=1, K=2048, N=2048, bs=32)
@@ -45,6 +45,16 @@ MLP64 = dict(M=64, K=2048, N=5632, bs=32)
 Q8F32 = dict(M=1, K=2560, N=4096, bs=32, bits=8)
 # float32 MatMulNBits for 64 rows (K=N=4096, block_size 32, 4-bit codes)
 F32P = dict(M=64, K=4096, N=4096, bs=32, bits=4)
+# float32 MatMulNBits prefill: the upstream qwen3-qproj-prefill-m512-q4g64 case
+# (M=512, K=2560, N=4096, block_size 64, float32 scales)
+F32P512 = dict(M=512, K=2560, N=4096, bs=64, bits=4)
+# float16 MatMulNBits prefill with 2-bit codes: the upstream
+# bonsai2-ffn-gate-prefill-m128-q2g128-k5120-n17408 case (block_size 128)
+Q2F16 = dict(M=128, K=5120, N=17408, bs=128, bits=2)
+# the MatMulNBits legs with float32 arithmetic (float32 activations, or
+# float16 with 2- or 8-bit codes)
+WIDE_LEGS = {"q8_f32_decode_m1": Q8F32, "q8_f16_decode_m1": Q8F32, "f32_prefill_m64": F32P, "f32_prefill_m512": F32P512,
+             "q2_f16_prefill_m128": Q2F16}
 # MatMulNBitsMlp prefill of the Llama-3-8B FFN: 2048 rows, K=4096, N=14336,
 # block_size 32, normScale, SiLU (gate and up: 2*2*M*K*N flops per call)
 MLP2K = dict(M=2048, K=4096, N=14336, bs=32)
@@ -189,9 +199,9 @@ def make_replicas(torch, name, R, dev, seed):
             reps.append(dict(gB=_gen_weights(torch, g, N, K // bs, bs // 2, dev), gS=_scales(torch, g, (N, K // bs), dev),
                              uB=_gen_weights(torch, g, N, K // bs, bs // 2, dev), uS=_scales(torch, g, (N, K // bs), dev)))
         return dict(A=A, reps=reps, K=K, N=N, bs=bs, gamma=gamma)
-    if name in ("q8_f32_decode_m1", "f32_prefill_m64", "q8_f16_decode_m1"):
-        q = Q8F32 if name.startswith("q8") else F32P
-        dt = torch.float16 if name == "q8_f16_decode_m1" else torch.float32
+    if name in WIDE_LEGS:
+        q = WIDE_LEGS[name]
+        dt = torch.float16 if "f16" in name else torch.float32
         K, N, bs, bits = q["K"], q["N"], q["bs"], q["bits"]
         kb = K // bs
         A = torch.randn((q["M"], K), device=dev, generator=g).to(dt)
@@ -290,12 +300,16 @@ def step_fn(ops, name, w):
             return ops.matmul_nbits_mlp(A, r["gB"], r["gS"], r["uB"], r["uS"], norm_scale=w["gamma"],
                                         block_size=w["bs"])
         return f
-    if name in ("q8_f32_decode_m1", "f32_prefill_m64", "q8_f16_decode_m1"):
+    if name in WIDE_LEGS:
         Y = torch.empty((A.shape[0], w["N"]), dtype=A.dtype, device=A.device)
+        # the float32 prefill GEMM's workspace (row exponents), zero-filled once
+        # outside the timed graph (a captured call without one takes the GEMV)
+        nws = ops.matmul_nbits_workspace_bytes(A.shape[0], w["K"], w["N"], w["bits"], w["bs"], A.dtype)
+        ws = torch.zeros(nws, dtype=torch.uint8, device=A.device) if nws else None
 
         def f(i):
             r = reps[i % len(reps)]
-            return ops.matmul_nbits(A, r["B"], r["S"], block_size=w["bs"], bits=w["bits"], out=Y)
+            return ops.matmul_nbits(A, r["B"], r["S"], block_size=w["bs"], bits=w["bits"], out=Y, workspace=ws)
         return f
     if name == "mlp_prefill_m2048":
         # one workspace for the normalised rows, allocated once (the front end
@@ -655,7 +669,7 @@ def main():
     results = {}
     names = ["decode_up_m1", "prefill_m2048", "prefill_m2048_prepacked", "qkv_gqa_m4", "mlp_swiglu_m16",
              "mlp_prefill_m64", "down_proj_m64", "mlp_prefill_m2048", "qkv_prefill_m2048", "f32_k2048_m1",
-             "q8_f32_decode_m1", "q8_f16_decode_m1", "f32_prefill_m64",
+             "q8_f32_decode_m1", "q8_f16_decode_m1", "f32_prefill_m64", "f32_prefill_m512", "q2_f16_prefill_m128",
              "qmoe_mixtral_t1", "qmoe_prefill_t256", "bnb4_nf4_m1", "gbq_embed_t2048", "int8a_decode_m1"]
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
@@ -666,7 +680,7 @@ def main():
         R = {"prefill_m2048": 8, "prefill_m2048_prepacked": 8, "mlp_prefill_m2048": 8, "qkv_prefill_m2048": 24,
              "qmoe_mixtral_t1": 2, "qmoe_prefill_t256": 1, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24,
              "f32_k2048_m1": 100, "mlp_prefill_m64": 24, "down_proj_m64": 12, "q8_f32_decode_m1": 24, "q8_f16_decode_m1": 24,
-             "f32_prefill_m64": 24}.get(name, args.replicas)
+             "f32_prefill_m64": 24, "f32_prefill_m512": 24, "q2_f16_prefill_m128": 12}.get(name, args.replicas)
         w = make_replicas(torch, name, R, dev, seed=SEEDS[name])
         fn = step_fn(ops, name, w)
         steps = args.steps if "prefill_m2048" not in name and name != "qmoe_prefill_t256" else max(10, args.steps // 10)
@@ -805,12 +819,17 @@ def main():
                                                      "qwen3-qproj-decode-m1-q8g32 geometry)"),
                           ("q8_f16_decode_m1", Q8F32, "MatMulNBits float16 M=1 K=2560 N=4096 bits=8 bs=32 (upstream "
                                                       "qwen3-qproj-decode-m1-q8g32, float32 arithmetic)"),
-                          ("f32_prefill_m64", F32P, "MatMulNBits float32 M=64 K=4096 N=4096 bits=4 bs=32")):
+                          ("f32_prefill_m64", F32P, "MatMulNBits float32 M=64 K=4096 N=4096 bits=4 bs=32"),
+                          ("f32_prefill_m512", F32P512, "MatMulNBits float32 M=512 K=2560 N=4096 bits=4 bs=64 (upstream "
+                                                        "qwen3-qproj-prefill-m512-q4g64 geometry)"),
+                          ("q2_f16_prefill_m128", Q2F16, "MatMulNBits float16 M=128 K=5120 N=17408 bits=2 bs=128 "
+                                                         "(upstream bonsai2-ffn-gate-prefill-m128-q2g128 geometry, "
+                                                         "float32 arithmetic)")):
         if name not in results:
             continue
         r = results[name]
         kb = q["K"] // q["bs"]
-        esz = 2 if name == "q8_f16_decode_m1" else 4
+        esz = 2 if "f16" in name else 4
         nbytes = q["N"] * (q["K"] * q["bits"] // 8 + kb * esz) + q["M"] * (q["K"] + q["N"]) * esz
         fl = 2 * q["M"] * q["K"] * q["N"]
         gbs = nbytes / (r["ms"] * 1e-3) / 1e9

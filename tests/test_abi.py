@@ -112,7 +112,11 @@ def test_qkv_requires_norm_scale():
     (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),       # the CPU-oracle workload, float32
     (0, 4, 4096, 14336, 64, nat.F32, nat.F32, "gemv_q4_f32"),
     (0, 5, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),         # float32 beyond four rows: chunks of four
-    (0, 64, 4096, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),
+    (0, 64, 4096, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemm_f32_mfma"),  # float32, more than 16 rows: MFMA
+    (0, 16, 4096, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),
+    (0, 64, 4000, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),    # padded K not a multiple of 64
+    (0, 64, 4096, 4096, 16, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),    # blocks of 16
+    (0, 64, 4096, 4096, 32, nat.F32, nat.F32, "gemv_q4_f32"),            # float zero points
     (1, 8, 256, 64, 32, nat.F32, nat.UNSPECIFIED, "generic"),         # float32 Qkv
     (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),
     (0, 4, 16384, 14336, 16, nat.F16, nat.UNSPECIFIED, "generic"),  # dot staging would exceed 160 KB of LDS
@@ -149,24 +153,29 @@ def test_fuzz_reaches_every_kernel_family():
     from xrgpu_amd import ops
     kind = {"none": None, "packed": "packed", "float_int": "float", "float": "float"}
     seen = set()
-    for M, K, N, bits, bs, zp, _, dt in F.MM + F.MMF32:
+    for M, K, N, bits, bs, zp, _, dt in F.MM + F.MMF32 + F.MMF32P:
         seen.add(ops.select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float16 if dt == "f16" else torch.float32,
                                    kind[zp]))
     for M, K, Nq, _, bs, zp, _ in F.QKV + F.QKV2:
         seen.add(ops.select_kernel("MatMulNBitsQkv", M, K, Nq, 4, bs, torch.float16, kind[zp]))
     for M, K, N, bs, *_ in F.MLP + F.MLP2:
         seen.add(ops.select_kernel("MatMulNBitsMlp", M, K, N, 4, bs, torch.float16))
-    want = {"gemv_q4_dot", "gemv_q4_mq", "gemv_q4_splitk", "gemv_q4_mfma", "gemv_q4_f32", "gemm_q4_mfma",
+    want = {"gemv_q4_dot", "gemv_q4_mq", "gemv_q4_splitk", "gemv_q4_mfma", "gemv_q4_f32", "gemm_f32_mfma", "gemm_q4_mfma",
             "gemm_q4_thin", "gemm_q4_fused", "generic"}
     assert want <= seen, f"not reached: {sorted(want - seen)}"
 
 
 @pytest.mark.parametrize("op,M,K,N,bits,bs,dtype,zp,expect", [
     (0, 1, 2560, 4096, 8, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),  # the upstream q8 decode case, float32
-    (0, 512, 2560, 4096, 8, 32, nat.F32, nat.U8, "gemv_q4_f32"),         # float32 8-bit prefill, chunks of four rows
+    (0, 512, 2560, 4096, 8, 32, nat.F32, nat.U8, "gemm_f32_mfma"),       # the upstream q8 prefill case, float32: MFMA
     (0, 1, 2560, 4096, 8, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_f32"),  # float16 8-bit codes: float32 arithmetic
-    (0, 512, 2560, 4096, 8, 64, nat.F16, nat.U8, "gemv_q4_f32"),         # float16 8-bit prefill rows
-    (0, 1, 2048, 2048, 2, 32, nat.F32, nat.UNSPECIFIED, "generic"),      # 2-bit codes
+    (0, 512, 2560, 4096, 8, 64, nat.F16, nat.U8, "gemm_f32_mfma"),       # float16 8-bit prefill rows: MFMA
+    (0, 512, 2560, 4096, 8, 16, nat.F16, nat.U8, "gemv_q4_f32"),         # blocks of 16: the GEMV
+    (0, 512, 2560, 4096, 8, 64, nat.F16, nat.F16, "gemv_q4_f32"),        # float zero points: the GEMV
+    (0, 1, 2048, 2048, 2, 32, nat.F32, nat.UNSPECIFIED, "generic"),      # 2-bit codes, one row
+    (0, 128, 5120, 17408, 2, 128, nat.F16, nat.UNSPECIFIED, "gemm_f32_mfma"),  # upstream bonsai2 2-bit prefill
+    (0, 64, 2048, 2048, 2, 32, nat.F32, nat.U8, "gemm_f32_mfma"),        # 2-bit, float32
+    (0, 64, 2048, 2048, 4, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_splitk"),  # 4-bit float16: the binary16 kernels
 ])
 def test_kernel_selection_bits(op, M, K, N, bits, bs, dtype, zp, expect):
     assert nat.lib().xrmm_select_kernel(op, M, K, N, bits, bs, dtype, zp).decode() == expect

@@ -1,7 +1,8 @@
 """GPU: float32 MatMulNBits on the float32 GEMV beyond four rows (chunks of
 four rows on the grid) and with 8-bit codes (the upstream
 qwen3-qproj-decode-m1-q8g32 case's geometry, …/com.microsoft.MatMulNBits/
-build/webgpu/bench.json:224), against the oracle at the float32 bar
+build/webgpu/bench.json:224), and on the float32 matrix-core GEMM (more than
+16 rows, with a workspace), against the oracle at the float32 bar
 max|d| <= 1e-5 max|Y_ref|."""
 import numpy as np
 import pytest
@@ -51,16 +52,105 @@ CASES = [
 ]
 
 
+def gemv_call(A, B, S, Z, b, M, K, N, bits, bs):
+    """The workspace-free entry point: float32 calls take the float32 GEMV at
+    every row count."""
+    from xrgpu_amd import _native as nat
+    tA, tB, tS, tZ, tb = dev(A), dev(B), dev(S), dev(Z), dev(b)
+    zdt = nat.UNSPECIFIED if Z is None else {np.uint8: nat.U8, np.float16: nat.F16, np.float32: nat.F32}[Z.dtype.type]
+    Y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    nat.check(nat.lib().xrmm_matmul_nbits(ptr(tA), ptr(tB), ptr(tS), ptr(tZ), zdt, ptr(tb), Y.data_ptr(), M, K, N,
+                                          bits, bs, nat.F32, None))
+    return Y.cpu().numpy()
+
+
 @pytest.mark.parametrize("M,K,N,bits,bs,zp,bias", CASES)
 def test_f32_gemv_parity(gpu, M, K, N, bits, bs, zp, bias):
     rng = np.random.default_rng(M * 11 + K + N + bits + bs)
     A, B, S, Z, b = case(rng, M, K, N, bits, bs, zp, bias)
     kind = None if zp is None else ("packed" if zp == "packed" else "float")
-    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float32, kind) == "gemv_q4_f32"
+    # more than 16 rows with a workspace (ops supplies one): the matrix-core
+    # GEMM, except for float zero points and blocks of 16
+    want = "gemm_f32_mfma" if M > 16 and zp not in ("float", "float16") and bs >= 32 else "gemv_q4_f32"
+    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float32, kind) == want
     Y = ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, bits=bits, block_size=bs).cpu().numpy()
     ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, bits=bits, block_size=bs)
     ok, err, lim = O.tolerance_ok(Y, ref, np.float32)
     assert ok, (err, lim)
+    # the workspace-free entry point runs the GEMV at any row count
+    ok, err, lim = O.tolerance_ok(gemv_call(A, B, S, Z, b, M, K, N, bits, bs), ref, np.float32)
+    assert ok, (err, lim)
+
+
+MFMA_CASES = [
+    # M, K, N, bits, bs, zp, bias: the float32 matrix-core GEMM
+    (17, 4096, 4096, 4, 32, None, False),     # 64 tiles: K split in four
+    (64, 4096, 4096, 4, 32, "packed", True),
+    (100, 2560, 4096, 8, 32, None, True),     # the q8 geometry at prefill rows
+    (65, 2048, 300, 8, 64, "packed", False),  # ragged column tile, 64-code blocks
+    (130, 1000, 520, 4, 128, "packed", True),  # partial last block (K = 1000)
+    (33, 8192, 96, 4, 256, None, False),       # one column tile: four splits of 32 steps
+    (48, 6144, 200, 8, 2048, "packed", True),  # blocks of 32 K steps
+    (300, 1536, 1024, 4, 64, "packed", False),
+    (520, 4096, 2048, 8, 128, None, False),    # many tiles: one split
+    (40, 2052, 260, 8, 2048, None, True),      # one 2048-code block, then a partial one
+    (64, 2560, 4096, 2, 64, None, False),      # 2-bit codes
+    (100, 1000, 300, 2, 32, "packed", True),
+    (48, 4096, 520, 2, 256, "packed", False),  # 2-bit blocks of 4 K steps, split K
+]
+
+
+@pytest.mark.parametrize("M,K,N,bits,bs,zp,bias", MFMA_CASES)
+def test_f32_mfma_gemm_parity(gpu, M, K, N, bits, bs, zp, bias):
+    """The float32 matrix-core GEMM against the oracle at the float32 bar, and
+    against the float32 GEMV of the workspace-free entry point."""
+    rng = np.random.default_rng(M * 7 + K + N + bits + bs)
+    A, B, S, Z, b = case(rng, M, K, N, bits, bs, zp, bias)
+    kind = None if zp is None else "packed"
+    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float32, kind) == "gemm_f32_mfma"
+    Y = ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, bits=bits, block_size=bs).cpu().numpy()
+    ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, bits=bits, block_size=bs)
+    ok, err, lim = O.tolerance_ok(Y, ref, np.float32)
+    assert ok, (err, lim)
+    ok, err, lim = O.tolerance_ok(Y, gemv_call(A, B, S, Z, b, M, K, N, bits, bs), np.float32)
+    assert ok, (err, lim)
+
+
+def test_f32_mfma_row_scaling_extremes(gpu):
+    """Rows scaled by powers of ten far from 1 (1e-38 .. 1e36), a row of zeros,
+    a row of float32 subnormals, infinities and a NaN. Finite rows: within
+    1e-5 of the row's largest exact (float64) output plus half a subnormal
+    step (the output's own rounding); non-finite elements as the oracle's
+    serial float32 loop gives them (Inf * 0 = NaN on the column whose code
+    equals its zero point)."""
+    M, K, N, bits, bs = 24, 512, 128, 4, 32
+    rng = np.random.default_rng(77)
+    A, B, S, Z, b = case(rng, M, K, N, bits, bs, "packed", False)
+    scale = np.array([1e-38, 1e-30, 1e-10, 1.0, 1e10, 1e30, 1e36, 2.0 ** -100] * 3, dtype=np.float64)
+    A = (A.astype(np.float64) * scale[:, None]).astype(np.float32)
+    A[8] = 0.0
+    A[9] = np.where(A[9] < 0, -1.0, 1.0).astype(np.float32) * np.float32(1e-44)  # subnormals only
+    A[10, 5] = np.inf
+    A[11, 100] = -np.inf
+    A[12, 7] = np.nan
+    B[3, 0, 2] = (B[3, 0, 2] & 0x0F) | 0x80  # k = 5 (high nibble of byte 2): code 8 ...
+    Z[3, 0] = (Z[3, 0] & 0xF0) | 8           # ... at zero point 8: W = 0 on column 3
+    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float32, "packed") == "gemm_f32_mfma"
+    Y = ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), None, K=K, N=N, bits=bits, block_size=bs).cpu().numpy()
+    ref = O.matmul_nbits(A, B, S, Z, None, K=K, N=N, bits=bits, block_size=bs)
+    bad = (10, 11, 12)
+    assert np.array_equal(np.isnan(Y[list(bad)]), np.isnan(ref[list(bad)]))
+    inf = np.isinf(ref[list(bad)])
+    assert np.array_equal(Y[list(bad)][inf], ref[list(bad)][inf])
+    assert np.isnan(Y[10, 3]) and np.isinf(Y[10, 4]) and np.isnan(Y[12]).all()
+    fin = [m for m in range(M) if m not in bad]
+    exact = O.matmul_nbits(A[fin], B, S, Z, None, K=K, N=N, bits=bits, block_size=bs, out_dtype=np.float64)
+    for i, m in enumerate(fin):
+        lim = 1e-5 * np.abs(exact[i]).max() + 2.0 ** -150
+        assert np.isfinite(Y[m]).all(), m
+        assert np.abs(Y[m].astype(np.float64) - exact[i]).max() <= lim, m
+    assert np.array_equal(Y[8], np.zeros(N, np.float32))
 
 
 def test_f32_8bit_infinite_activation(gpu):
@@ -101,7 +191,42 @@ def test_f16_8bit_on_the_float32_gemv(gpu, M, K, N, bits, bs, zp, bias):
     A, S = A.astype(np.float16), S.astype(np.float16)
     b = None if b is None else b.astype(np.float16)
     kind = None if zp is None else ("packed" if zp == "packed" else "float")
-    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float16, kind) == "gemv_q4_f32"
+    want = "gemm_f32_mfma" if M > 16 and zp not in ("float", "float16") and bs >= 32 else "gemv_q4_f32"
+    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float16, kind) == want
+    Y = ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, bits=bits, block_size=bs)
+    assert Y.dtype == torch.float16
+    Y = Y.cpu().numpy()
+    ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, bits=bits, block_size=bs)
+    ok, err, lim = O.tolerance_ok(Y, ref, np.float16)
+    assert ok, (err, lim)
+    exact = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, bits=bits, block_size=bs, out_dtype=np.float64)
+    bound = np.abs(exact) * 2.0 ** -11 + 1e-5 * np.abs(exact).max()
+    assert np.all(np.abs(Y.astype(np.float64) - exact) <= bound)
+
+
+F16_MFMA_CASES = [
+    # M, K, N, bits, bs, zp, bias: float16 activations on the float32-arithmetic GEMM
+    (512, 2560, 4096, 8, 32, None, False),      # the upstream q8 geometry at 512 rows, float16
+    (128, 5120, 1040, 2, 128, "packed", False),  # 2-bit, bonsai2-like (K 5120, blocks of 128)
+    (65, 1024, 300, 2, 32, None, True),
+    (33, 2048, 96, 8, 64, "packed", True),       # one column tile: K split
+    (200, 1000, 257, 8, 256, None, False),       # partial last block (K % 8 == 0)
+]
+
+
+@pytest.mark.parametrize("M,K,N,bits,bs,zp,bias", F16_MFMA_CASES)
+def test_f16_wide_codes_on_the_mfma_gemm(gpu, M, K, N, bits, bs, zp, bias):
+    """float16 activations with 2- or 8-bit codes and more than 16 rows run the
+    float32-arithmetic MFMA GEMM: exact binary16 operands (activations, codes
+    minus zero points), float32 block sums and scales, one rounding at the
+    output, so every element is within one binary16 rounding (2^-11
+    relative) plus 1e-5 max|Y| of the exact result."""
+    rng = np.random.default_rng(M * 17 + K + N + bits + bs)
+    A, B, S, Z, b = case(rng, M, K, N, bits, bs, zp, bias)
+    A, S = A.astype(np.float16), S.astype(np.float16)
+    b = None if b is None else b.astype(np.float16)
+    kind = None if zp is None else "packed"
+    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float16, kind) == "gemm_f32_mfma"
     Y = ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, bits=bits, block_size=bs)
     assert Y.dtype == torch.float16
     Y = Y.cpu().numpy()

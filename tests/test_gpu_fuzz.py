@@ -232,6 +232,33 @@ def _f32_cases(n=10):
 MMF32 = _f32_cases()
 
 
+def _wide_prefill_cases(n, seed, dt, bit_choices):
+    """More than 16 rows on the float32-arithmetic MFMA GEMM: blocks of
+    32..256 with partial last blocks, no or packed zero points (float zero
+    points fall back to the float32 GEMV)."""
+    rng = np.random.default_rng(seed)
+    q = 4 if dt == "f32" else 8  # K % 4 (float32) or K % 8 (float16)
+    out = []
+    for _ in range(n):
+        bits = int(rng.choice(bit_choices))
+        bs = int(rng.choice([32, 64, 128, 256]))
+        step = max(64, bs)
+        Kd = step * int(rng.integers(1, max(2, 2048 // step + 1)))
+        K = Kd - q * int(rng.integers(0, bs // q))  # a partial last block
+        out.append((int(rng.choice([17, 33, 64, 65, 100, 130, 200, 300])), K, int(rng.integers(1, 600)), bits, bs,
+                    str(rng.choice(["none", "packed", "packed", "float"])), bool(rng.integers(0, 2)), dt))
+    return out
+
+
+# float32 activations with 2-, 4- and 8-bit codes; float16 with 2 and 8
+MMF32P = _wide_prefill_cases(12, SEED + 15, "f32", [2, 4, 8]) + _wide_prefill_cases(8, SEED + 16, "f16", [2, 8])
+
+
+@pytest.mark.parametrize("M,K,N,bits,bs,zp,bias,dt", MMF32P, ids=ids(MMF32P))
+def test_matmul_nbits_wide_prefill_random(gpu, M, K, N, bits, bs, zp, bias, dt):
+    test_matmul_nbits_random(gpu, M, K, N, bits, bs, zp, bias, dt)
+
+
 @pytest.mark.parametrize("M,K,N,bits,bs,zp,bias,dt", MMF32, ids=ids(MMF32))
 def test_matmul_nbits_f32_random(gpu, M, K, N, bits, bs, zp, bias, dt):
     test_matmul_nbits_random(gpu, M, K, N, bits, bs, zp, bias, dt)

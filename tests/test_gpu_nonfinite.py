@@ -204,8 +204,9 @@ def test_lifecycle_scales_beyond_binary16_weight_range(gpu, M, K, N, bs):
     """Scales of 30000 with an implicit zero point give float32 weights up to
     240000 (finite in the reference, beyond binary16). The request lifecycle
     checks the scales at prepare and runs kernels that keep weights in
-    float32 (the dot GEMV for one row, the float32-arithmetic GEMV beyond);
-    the result matches the oracle."""
+    float32 (the dot GEMV for up to two rows, the float32-arithmetic GEMV up
+    to 16, the float32-arithmetic GEMM beyond); the result matches the
+    oracle."""
     rng = np.random.default_rng(M + K + N + 2)
     kb = K // bs
     ins = dict(aT=(rng.standard_normal((M, K)) * 1e-4).astype(np.float16),
@@ -221,4 +222,4 @@ def test_lifecycle_scales_beyond_binary16_weight_range(gpu, M, K, N, bs):
     assert np.isfinite(ref).all()
     ok, err, lim = O.tolerance_ok(y.data, ref, np.float16)
     assert ok, (info.get("kernel"), err, lim)
-    assert info.get("kernel") == ("gemv_q4_dot" if M <= 2 else "gemv_q4_f32")
+    assert info.get("kernel") == ("gemv_q4_dot" if M <= 2 else "gemv_q4_f32" if M <= 16 else "gemm_f32_mfma")

@@ -91,6 +91,28 @@ thread_local bool g_exact_weights = false;
 ExactWeightsScope::ExactWeightsScope(bool on) : prev_(g_exact_weights) { g_exact_weights = on; }
 ExactWeightsScope::~ExactWeightsScope() { g_exact_weights = prev_; }
 bool ExactWeightsScope::active() { return g_exact_weights; }
+
+const char* select_kernel_name(int32_t op, int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size,
+                               int32_t dtype, int32_t zp_dtype, bool with_ws) {
+  Launch L;
+  if (op < OP_MATMUL || op > OP_MLP) {
+    fail(XRMM_EINVAL, "unknown operator code");
+    return nullptr;
+  }
+  if (geometry(L, op, M, K, bits, block_size, dtype, zp_dtype)) return nullptr;
+  // aligned placeholders: the selection only looks at pointer alignment
+  static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
+  L.nproj = op == OP_QKV ? 3 : op == OP_MLP ? 2 : 1;
+  L.A = dummy;
+  if (op == OP_QKV) L.gamma = dummy;  // normScaleT is required for Qkv
+  for (int i = 0; i < L.nproj; ++i) L.p[i] = Proj{dummy, dummy, zp_dtype == XRMM_UNSPECIFIED ? nullptr : dummy, nullptr, nullptr, N};
+  if (with_ws) {
+    L.xs = const_cast<uint8_t*>(dummy);
+    L.ws = const_cast<uint8_t*>(dummy);
+  }
+  ok();
+  return kernel_name(select_kernel(L));
+}
 }  // namespace xrmm
 
 extern "C" {
@@ -122,8 +144,17 @@ int64_t xrmm_matmul_nbits_workspace_bytes(int64_t M, int64_t K, int64_t N, int32
   }
   L.nproj = 1;
   L.p[0].N = N;
+  // aligned placeholders: the choice depends on the geometry (and on a
+  // workspace being there)
+  static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
+  L.A = dummy;
+  L.p[0].B = dummy;
+  L.p[0].scales = dummy;
+  L.ws = const_cast<uint8_t*>(dummy);
   const xrmm::Kernel k = M > 0 ? xrmm::select_kernel(L) : xrmm::K_GENERIC;
+  if (k == xrmm::K_GEMM_F32X) return xrmm::f32x_workspace_bytes(L);
   if (k != xrmm::K_GEMM_Q4 && k != xrmm::K_GEMM_THIN) return 0;
+  L.ws = nullptr;
   return xrmm::gemm_workspace_bytes(L, xrmm::gemm_splits(L));
 }
 
@@ -138,6 +169,20 @@ int xrmm_matmul_nbits_ws(const void* A, const void* B, const void* scales, const
   L.nproj = 1;
   L.A = A;
   L.p[0] = xrmm::Proj{static_cast<const uint8_t*>(B), scales, zero_points, bias, Y, N};
+  if (workspace && M > 0) {
+    // the float32 MFMA GEMM runs only with a workspace: row exponents and
+    // split partials
+    xrmm::Launch Lw = L;
+    Lw.ws = workspace;
+    if (xrmm::select_kernel(Lw) == xrmm::K_GEMM_F32X) {
+      const int64_t need = xrmm::f32x_workspace_bytes(L);
+      if (workspace_bytes < need)
+        return fail(XRMM_EINVAL, "workspace smaller than xrmm_matmul_nbits_workspace_bytes: " + std::to_string(need));
+      if (reinterpret_cast<uintptr_t>(workspace) & 255u) return fail(XRMM_EINVAL, "workspace must be 256-byte aligned");
+      L.ws = workspace;
+      return run(L, stream);
+    }
+  }
   const xrmm::Kernel k = M > 0 ? xrmm::select_kernel(L) : xrmm::K_GENERIC;
   if (workspace && (k == xrmm::K_GEMM_Q4 || k == xrmm::K_GEMM_THIN)) {
     const int splits = xrmm::gemm_splits(L);
@@ -366,23 +411,9 @@ int xrmm_dequantize(const void* B, const void* scales, const void* zero_points, 
 
 const char* xrmm_select_kernel(int32_t op, int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size,
                                int32_t dtype, int32_t zp_dtype) {
-  xrmm::Launch L;
-  if (op < xrmm::OP_MATMUL || op > xrmm::OP_MLP) {
-    fail(XRMM_EINVAL, "unknown operator code");
-    return nullptr;
-  }
-  if (geometry(L, op, M, K, bits, block_size, dtype, zp_dtype)) return nullptr;
-  // aligned placeholders: the selection only looks at pointer alignment
-  static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
-  L.nproj = op == xrmm::OP_QKV ? 3 : op == xrmm::OP_MLP ? 2 : 1;
-  L.A = dummy;
-  if (op == xrmm::OP_QKV) L.gamma = dummy;  // normScaleT is required for Qkv
-  for (int i = 0; i < L.nproj; ++i) L.p[i] = xrmm::Proj{dummy, dummy, zp_dtype == XRMM_UNSPECIFIED ? nullptr : dummy, nullptr, nullptr, N};
   // the front ends (ops.py, the request lifecycle) supply the Qkv / Mlp
-  // prefill workspace, so the selection assumes one
-  L.xs = const_cast<uint8_t*>(dummy);
-  ok();
-  return xrmm::kernel_name(xrmm::select_kernel(L));
+  // prefill workspace and the MatMulNBits one, so the selection assumes them
+  return xrmm::select_kernel_name(op, M, K, N, bits, block_size, dtype, zp_dtype, true);
 }
 
 }  // extern "C"

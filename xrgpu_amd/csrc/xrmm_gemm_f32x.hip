@@ -1,0 +1,100 @@
+// MatMulNBits with float32 arithmetic on the matrix cores (the kernels are in
+// xrmm_gemm_f32x.h): the geometry check, the K splits, the workspace layout
+// and the launch.
+#include "xrmm_gemm_f32x.h"
+
+namespace xrmm {
+
+namespace {
+
+int64_t al256(int64_t b) { return (b + 255) / 256 * 256; }
+
+// The workspace's first kFxKeep bytes are left alone: front ends share one
+// workspace between this GEMM and the split-K GEMMs, whose arrival counters
+// live there and must stay zero. Then, for float32 activations, the row
+// exponents and the prepared binary16 terms (hi, lo); then the split
+// partials.
+constexpr int64_t kFxKeep = 4096;
+
+int64_t fx_kd(const Launch& L) { return L.kb * L.block_size; }
+
+int64_t fx_prep_bytes(const Launch& L) {
+  return L.dtype == DT_F32 ? al256(L.M * 4) + 2 * al256(L.M * fx_kd(L) * 2) : 0;
+}
+
+}  // namespace
+
+// K splits: enough for about 256 workgroups (one per CU) when the tiles are
+// fewer, eight at most, each split at least 8 K steps of 64.
+int f32x_splits(const Launch& L) {
+  const int64_t tiles = ((L.M + fx::RT - 1) / fx::RT) * ((L.p[0].N + fx::CT - 1) / fx::CT);
+  const int64_t ksteps = fx_kd(L) / fx::KS;
+  int64_t s = (256 + tiles - 1) / tiles;
+  if (s > 8) s = 8;
+  if (s > ksteps / 8) s = ksteps / 8;
+  return s < 1 ? 1 : static_cast<int>(s);
+}
+
+int64_t f32x_workspace_bytes(const Launch& L) {
+  const int s = f32x_splits(L);
+  return kFxKeep + fx_prep_bytes(L) + (s > 1 ? al256(int64_t(s) * L.M * L.p[0].N * 4) : 0);
+}
+
+// MatMulNBits with more than 16 rows: float32 activations with 2-, 4- or
+// 8-bit codes, float16 activations with 2- or 8-bit codes (4-bit with exact
+// weights); blocks of 32 or more codes (powers of two), a padded K that is a
+// multiple of 64, K a multiple of 4 (float32) or 8 (float16), packed or no
+// zero points, 16-byte aligned tensors, 32-bit offsets. The caller supplies
+// the workspace.
+bool f32x_fits(const Launch& L) {
+  if (L.op != OP_MATMUL || L.M <= 16 || (L.bits != 2 && L.bits != 4 && L.bits != 8)) return false;
+  if (L.dtype == DT_F16) {
+    if (L.bits == 4 && !L.exact_weights) return false;  // the binary16 GEMMs
+    if (L.K % 8 != 0) return false;
+  } else if (L.dtype != DT_F32 || L.K % 4 != 0) {
+    return false;
+  }
+  if (L.block_size < 32 || L.bs_log2 < 5 || fx_kd(L) % fx::KS != 0) return false;
+  if (L.zp_kind == ZP_FLOAT) return false;
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (!al(L.A) || !al(L.p[0].B) || !al(L.p[0].scales)) return false;
+  const int64_t lim = int64_t(1) << 31, rowb = fx_kd(L) * L.bits / 8;
+  return L.M * fx_kd(L) * 4 < lim && L.p[0].N * rowb < lim && int64_t(f32x_splits(L)) * L.M * L.p[0].N < lim &&
+         L.M < lim / fx::RT;
+}
+
+hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st) {
+  fx::Args a{};
+  a.A = L.A;
+  a.B = L.p[0].B;
+  a.S = L.p[0].scales;
+  a.Z = L.zp_kind == ZP_PACKED ? static_cast<const uint8_t*>(L.p[0].zp) : nullptr;
+  a.bias = L.p[0].bias;
+  a.Y = L.p[0].Y;
+  a.M = static_cast<int>(L.M);
+  a.K = static_cast<int>(L.K);
+  a.N = static_cast<int>(L.p[0].N);
+  a.kb = static_cast<int>(L.kb);
+  a.bs = static_cast<int>(L.block_size);
+  a.Kd = static_cast<int>(fx_kd(L));
+  a.rowb = static_cast<int>(fx_kd(L) * L.bits / 8);
+  a.zrow = static_cast<int>(L.zrow);
+  a.bits = L.bits;
+  a.splits = f32x_splits(L);
+  uint8_t* w = static_cast<uint8_t*>(L.ws) + kFxKeep;
+  if (L.dtype == DT_F32) {
+    int32_t* ex = reinterpret_cast<int32_t*>(w);
+    f16* hi = reinterpret_cast<f16*>(w + al256(L.M * 4));
+    f16* lo = hi + al256(L.M * fx_kd(L) * 2) / 2;
+    a.ex = ex;
+    a.Ahi = hi;
+    a.Alo = lo;
+    hipLaunchKernelGGL(fx::k_fx_prep, dim3(static_cast<uint32_t>(L.M)), dim3(256), 0, st, static_cast<const float*>(L.A),
+                       a.K, a.Kd, ex, hi, lo);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  }
+  a.part = reinterpret_cast<float*>(w + fx_prep_bytes(L));
+  return L.dtype == DT_F32 ? fx::launch_gemm<float>(a, st) : fx::launch_gemm_f16(a, st);
+}
+
+}  // namespace xrmm

@@ -75,7 +75,7 @@ class ExactWeightsScope {
 
 // Kernel families the dispatcher chooses between.
 enum Kernel { K_GENERIC = 0, K_GEMV_Q4 = 1, K_GEMM_Q4 = 2, K_GEMV_DOT = 3, K_GEMM_BIG = 4, K_GEMV_SK = 5, K_GEMV_MQ = 6,
-              K_GEMV_F32 = 7, K_GEMM_FUSED = 8, K_GEMM_BIG_FUSED = 9, K_GEMM_THIN = 10 };
+              K_GEMV_F32 = 7, K_GEMM_FUSED = 8, K_GEMM_BIG_FUSED = 9, K_GEMM_THIN = 10, K_GEMM_F32X = 11 };
 
 // Whether a Qkv / Mlp launch has a prologue (skip or normScale) whose
 // normalised activations a prefill GEMM can take from L.xs.
@@ -83,9 +83,23 @@ inline bool fused_prologue(const Launch& L) { return L.op != OP_MATMUL && (L.ski
 // Bytes of L.xs for the geometry (binary16 [M, K], 256-byte multiple).
 inline int64_t fused_xs_bytes(const Launch& L) { return (L.M * L.K * 2 + 255) / 256 * 256; }
 
+// MatMulNBits with float32 arithmetic on the matrix cores
+// (xrmm_gemm_f32x.hip): whether a geometry fits, its K splits, the workspace
+// it needs (prepared float32 rows and split partials; the launch takes it
+// from Launch::ws), and the launch.
+bool f32x_fits(const Launch& L);
+int f32x_splits(const Launch& L);
+int64_t f32x_workspace_bytes(const Launch& L);
+hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st);
+
 // Choose a kernel family for the geometry (host only, no device calls).
 Kernel select_kernel(const Launch& L);
 const char* kernel_name(Kernel k);
+// The family xrmm_select_kernel names, for a caller that does (with_ws) or
+// does not supply the MatMulNBits / Qkv / Mlp workspace; null (and the
+// status set) for an invalid geometry.
+const char* select_kernel_name(int32_t op, int64_t M, int64_t K, int64_t N, int32_t bits, int32_t block_size,
+                               int32_t dtype, int32_t zp_dtype, bool with_ws);
 
 // Enqueue the operator on `stream`. Returns hipSuccess or the launch error.
 hipError_t launch(const Launch& L, hipStream_t stream);

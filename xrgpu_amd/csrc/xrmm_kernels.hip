@@ -663,8 +663,9 @@ inline bool thin_takes(const Launch& L) {
 
 Kernel select_kernel(const Launch& L) {
   if (L.exact_weights) {
-    // the dot and four-row MFMA GEMVs keep weights out of binary16; every
-    // other fast kernel stages binary16 weights
+    // the dot and four-row MFMA GEMVs and the float32-arithmetic GEMM keep
+    // weights out of binary16; every other fast kernel stages binary16 weights
+    if (L.ws != nullptr && f32x_fits(L)) return K_GEMM_F32X;
     if (q4_fast_ok(L) && fits_i32(L) && mq_takes(L)) return K_GEMV_MQ;
     if (q4_fast_ok(L) && fits_i32(L) && (L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 &&
         L.M < split_k_min_rows(L.op) && dot_fits(L))
@@ -673,6 +674,9 @@ Kernel select_kernel(const Launch& L) {
     if (f32_fits(L) && fits_i32(L)) return K_GEMV_F32;
     return K_GENERIC;
   }
+  // more than 16 rows of float32 activations, or of float16 activations with
+  // 2- or 8-bit codes, and a caller workspace: the float32-arithmetic GEMM
+  if (L.ws != nullptr && f32x_fits(L)) return K_GEMM_F32X;
   // float32 activations (the contract's T1 = float32) and float16 with 8-bit
   // codes, any row count: the float32-arithmetic GEMV
   if (f32_fits(L) && fits_i32(L)) return K_GEMV_F32;
@@ -706,6 +710,7 @@ const char* kernel_name(Kernel k) {
     case K_GEMM_FUSED: return "gemm_q4_fused";
     case K_GEMM_BIG_FUSED: return "gemm_q4_big_fused";
     case K_GEMM_THIN: return "gemm_q4_thin";
+    case K_GEMM_F32X: return "gemm_f32_mfma";
     default: return "generic";
   }
 }
@@ -776,6 +781,7 @@ hipError_t launch(const Launch& L, hipStream_t st) {
   Kernel k = select_kernel(L);
   const int zpk = effective_zpk(L);
   if (zpk < 0) k = K_GENERIC;  // mixed presence of zero points
+  if (k == K_GEMM_F32X) return launch_gemm_f32x(L, st);
   if (k == K_GEMV_F32) {
     if (zpk == ZP_NONE) return launch_f32_for<ZP_NONE>(L, st);
     if (zpk == ZP_PACKED) return launch_f32_for<ZP_PACKED>(L, st);

@@ -273,14 +273,16 @@ __global__ __launch_bounds__(MG_T, 2) void k_moe_ggemm(MoeArgs a, MgLists g, int
     *reinterpret_cast<f16x8*>(Ah + arow * MG_LD + agrp * 8) = vh;
     *reinterpret_cast<f16x8*>(Al + arow * MG_LD + agrp * 8) = vl;
     // fragment 4 bh + d of the step (codes 32 bh + 8 d .. + 7) of column bcol
+    if constexpr (BW == 1) {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      if constexpr (BW == 1) {
-        Bw[(4 * bh + d) * MG_CT + bcol] = r.b[0][d];
-      } else {
-        const u32x2 v = {r.b[d >> 1][2 * (d & 1)], r.b[d >> 1][2 * (d & 1) + 1]};
-        *reinterpret_cast<u32x2*>(Bw + ((4 * bh + d) * MG_CT + bcol) * 2) = v;
-      }
+      for (int d = 0; d < 4; ++d) Bw[(4 * bh + d) * MG_CT + bcol] = r.b[0][d];
+    } else {
+      // the eight dwords by name (no v[i >> 1][...] indexing, see above)
+      const u32x4 b0 = r.b[0], b1 = r.b[BW - 1];
+      const uint32_t w[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        *reinterpret_cast<u32x2*>(Bw + ((4 * bh + d) * MG_CT + bcol) * 2) = u32x2{w[2 * d], w[2 * d + 1]};
     }
   };
   // a fragment's eight codes -> c - 2^(bits - 1) as exact binary16, pair

@@ -779,15 +779,19 @@ int xrmm_prepare(const xrmm_request* request, const xrmm_options* options, xrmm_
     if (p.contract->op == OP_GBQ) ws = 4;
     total += align256(ws);
     if (total > o.memory_limit_bytes) throw Invalid("Extended heap memory limit exceeded");
-    // The split-K workspace of MatMulNBits and the normalised-activation
-    // workspace of the Qkv / Mlp prefill GEMMs are performance options, not
-    // part of the request's memory: each is reserved only when it fits the
-    // limit beside the data, and the call runs without it otherwise.
-    if (!weights_need_float32(p)) {
+    // The MatMulNBits workspace (split K, the float32-arithmetic GEMM) and
+    // the normalised-activation workspace of the Qkv / Mlp prefill GEMMs are
+    // performance options, not part of the request's memory: each is
+    // reserved only when it fits the limit beside the data, and the call runs
+    // without it otherwise. Weights beyond binary16 keep the MatMulNBits one
+    // (for the float32-arithmetic GEMM).
+    {
+      const bool exact = weights_need_float32(p);
+      const xrmm::ExactWeightsScope scope(exact);
       uint64_t opt = 0;
       if (p.contract->op == xrmm::OP_MATMUL)
         opt = uint64_t(xrmm_matmul_nbits_workspace_bytes(p.M, p.K, p.N, p.bits, p.block_size, p.dtype));
-      else if (p.contract->op == xrmm::OP_QKV || p.contract->op == xrmm::OP_MLP)
+      else if (!exact && (p.contract->op == xrmm::OP_QKV || p.contract->op == xrmm::OP_MLP))
         opt = uint64_t(xrmm_matmul_nbits_fused_workspace_bytes(
             p.contract->op, p.M, p.K, p.contract->op == xrmm::OP_QKV ? p.Nq : p.N, p.Nkv, p.bits, p.block_size,
             p.dtype, p.in.count("skipT") ? 1 : 0, p.in.count("normScaleT") ? 1 : 0));
@@ -854,7 +858,7 @@ int xrmm_prepare(const xrmm_request* request, const xrmm_options* options, xrmm_
       op->exact_weights = weights_need_float32(p);
       const xrmm::ExactWeightsScope exact(op->exact_weights);
       const int64_t n0 = code == xrmm::OP_QKV ? p.Nq : p.N;
-      k = xrmm_select_kernel(code, p.M, p.K, n0, p.bits, p.block_size, p.dtype, zk);
+      k = xrmm::select_kernel_name(code, p.M, p.K, n0, p.bits, p.block_size, p.dtype, zk, op->workspace != nullptr);
       // prepare = upload / prepack: MatMulNBits requests that reach the 256 x
       // 256 prefill GEMM get their weights prepacked once, here, when the
       // copy fits the memory limit beside the arena

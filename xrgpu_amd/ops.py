@@ -120,7 +120,9 @@ def matmul_nbits(A, B, scales, zero_points=None, bias=None, *, K=None, N=None, b
     """com.microsoft.MatMulNBits on the GPU. Returns Y ``A.shape[:-1] + [N]``.
 
     Geometries with few output tiles split K across workgroups on a workspace
-    (``matmul_nbits_workspace_bytes``). Eager calls use one zero-filled
+    (``matmul_nbits_workspace_bytes``), and float32 activations with more than
+    16 rows run the float32 matrix-core GEMM, whose row exponents (and split
+    partials) live there too. Eager calls use one zero-filled
     workspace per (device, stream) kept by this module. A caller may pass its
     own ``workspace`` (uint8, 256-byte aligned, its first 4096 bytes zero
     before first use; every call leaves them zero); calls that may overlap
