@@ -92,7 +92,15 @@ int xrmm_matmul_nbits(const void* A, const void* B, const void* scales, const vo
  * a tile adds them in split order (deterministic). No counterpart in the
  * reference (one serial loop, complex_kernel.glsl:83); same results as
  * xrmm_matmul_nbits within the float16 bar.
- * xrmm_matmul_nbits_workspace_bytes gives the bytes (0: no split applies,
+ * The workspace also carries the float32-arithmetic MFMA GEMM that runs
+ * more than 16 rows of float32 activations, or of float16 activations with
+ * 2- or 8-bit codes ("gemm_f32_mfma"; without a workspace those calls take
+ * the float32-arithmetic GEMV): its prepared rows (binary16 hi / lo terms of
+ * float32 activations, block sums for float zero points) and split partials;
+ * same results as xrmm_matmul_nbits within the float32 bar (float32
+ * activations) or within one binary16 rounding of float32 arithmetic
+ * (float16).
+ * xrmm_matmul_nbits_workspace_bytes gives the bytes (0: neither applies,
  * and the call runs like xrmm_matmul_nbits). The workspace is 256-byte
  * aligned; its first 4096 bytes (per-tile arrival counters) are zero before
  * its first use and every call leaves them zero, so one workspace serves

@@ -114,9 +114,10 @@ def test_qkv_requires_norm_scale():
     (0, 5, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),         # float32 beyond four rows: chunks of four
     (0, 64, 4096, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemm_f32_mfma"),  # float32, more than 16 rows: MFMA
     (0, 16, 4096, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),
-    (0, 64, 4000, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),    # padded K not a multiple of 64
+    (0, 64, 4000, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemm_f32_mfma"),  # padded K not a multiple of 64
     (0, 64, 4096, 4096, 16, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),    # blocks of 16
-    (0, 64, 4096, 4096, 32, nat.F32, nat.F32, "gemv_q4_f32"),            # float zero points
+    (0, 64, 4096, 4096, 32, nat.F32, nat.F32, "gemv_q4_f32"),            # float zero points, blocks of 32
+    (0, 64, 4096, 4096, 64, nat.F32, nat.F32, "gemm_f32_mfma"),          # float zero points, blocks of 64
     (1, 8, 256, 64, 32, nat.F32, nat.UNSPECIFIED, "generic"),         # float32 Qkv
     (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),
     (0, 4, 16384, 14336, 16, nat.F16, nat.UNSPECIFIED, "generic"),  # dot staging would exceed 160 KB of LDS
@@ -171,7 +172,12 @@ def test_fuzz_reaches_every_kernel_family():
     (0, 1, 2560, 4096, 8, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_f32"),  # float16 8-bit codes: float32 arithmetic
     (0, 512, 2560, 4096, 8, 64, nat.F16, nat.U8, "gemm_f32_mfma"),       # float16 8-bit prefill rows: MFMA
     (0, 512, 2560, 4096, 8, 16, nat.F16, nat.U8, "gemv_q4_f32"),         # blocks of 16: the GEMV
-    (0, 512, 2560, 4096, 8, 64, nat.F16, nat.F16, "gemv_q4_f32"),        # float zero points: the GEMV
+    (0, 512, 2560, 4096, 8, 64, nat.F16, nat.F16, "gemm_f32_mfma"),      # float zero points, blocks of 64: MFMA
+    (0, 512, 2560, 4096, 8, 32, nat.F16, nat.F16, "gemv_q4_f32"),        # float zero points, blocks of 32: the GEMV
+    (0, 512, 2560, 4096, 4, 64, nat.F32, nat.F16, "gemv_q4_f32"),        # zero points of another type: the GEMV
+    (0, 512, 2560, 4096, 4, 64, nat.F32, nat.F32, "gemm_f32_mfma"),      # upstream qwen3 prefill zero-bias case
+    (0, 48, 2561, 1021, 8, 32, nat.F32, nat.UNSPECIFIED, "gemm_f32_mfma"),  # upstream tail case (K % 4 != 0)
+    (0, 128, 5120, 17408, 2, 128, nat.F16, nat.F16, "gemm_f32_mfma"),    # upstream bonsai2 case, float16 zero points
     (0, 1, 2048, 2048, 2, 32, nat.F32, nat.UNSPECIFIED, "generic"),      # 2-bit codes, one row
     (0, 128, 5120, 17408, 2, 128, nat.F16, nat.UNSPECIFIED, "gemm_f32_mfma"),  # upstream bonsai2 2-bit prefill
     (0, 64, 2048, 2048, 2, 32, nat.F32, nat.U8, "gemm_f32_mfma"),        # 2-bit, float32

@@ -52,6 +52,15 @@ CASES = [
 ]
 
 
+def want_kernel(M, bs, zp, float16):
+    """The family a call with a workspace takes: the float32-arithmetic MFMA
+    GEMM beyond 16 rows for blocks of 32 or more, float zero points only of
+    the activations' type and with blocks of 64 or more."""
+    fz = {"float": not float16, "float16": float16}
+    ok = M > 16 and bs >= 32 and (zp not in fz or (fz[zp] and bs >= 64))
+    return "gemm_f32_mfma" if ok else "gemv_q4_f32"
+
+
 def gemv_call(A, B, S, Z, b, M, K, N, bits, bs):
     """The workspace-free entry point: float32 calls take the float32 GEMV at
     every row count."""
@@ -70,10 +79,10 @@ def test_f32_gemv_parity(gpu, M, K, N, bits, bs, zp, bias):
     rng = np.random.default_rng(M * 11 + K + N + bits + bs)
     A, B, S, Z, b = case(rng, M, K, N, bits, bs, zp, bias)
     kind = None if zp is None else ("packed" if zp == "packed" else "float")
-    # more than 16 rows with a workspace (ops supplies one): the matrix-core
-    # GEMM, except for float zero points and blocks of 16
-    want = "gemm_f32_mfma" if M > 16 and zp not in ("float", "float16") and bs >= 32 else "gemv_q4_f32"
-    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float32, kind) == want
+    # more than 16 rows with a workspace (ops supplies one): the matrix-core GEMM
+    want = want_kernel(M, bs, zp, False)
+    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float32, kind,
+                               zp_dtype=torch.float16 if zp == "float16" else None) == want
     Y = ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, bits=bits, block_size=bs).cpu().numpy()
     ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, bits=bits, block_size=bs)
     ok, err, lim = O.tolerance_ok(Y, ref, np.float32)
@@ -98,6 +107,12 @@ MFMA_CASES = [
     (64, 2560, 4096, 2, 64, None, False),      # 2-bit codes
     (100, 1000, 300, 2, 32, "packed", True),
     (48, 4096, 520, 2, 256, "packed", False),  # 2-bit blocks of 4 K steps, split K
+    (512, 2560, 4096, 4, 64, "float", True),   # upstream qwen3 prefill zero-bias: float zero points
+    (64, 1000, 300, 8, 128, "float", False),   # float zero points, partial last block
+    (40, 4096, 200, 2, 2048, "float", True),   # float zero points, blocks of 32 K steps, split K
+    (48, 2561, 1021, 8, 32, None, False),      # upstream tail case: K % 4 != 0, half a last K step
+    (32, 2561, 4096, 4, 32, "packed", True),
+    (17, 99, 33, 4, 64, None, True),           # one short K step
 ]
 
 
@@ -107,8 +122,7 @@ def test_f32_mfma_gemm_parity(gpu, M, K, N, bits, bs, zp, bias):
     against the float32 GEMV of the workspace-free entry point."""
     rng = np.random.default_rng(M * 7 + K + N + bits + bs)
     A, B, S, Z, b = case(rng, M, K, N, bits, bs, zp, bias)
-    kind = None if zp is None else "packed"
-    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float32, kind) == "gemm_f32_mfma"
+    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float32, zp) == "gemm_f32_mfma"
     Y = ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, bits=bits, block_size=bs).cpu().numpy()
     ref = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, bits=bits, block_size=bs)
     ok, err, lim = O.tolerance_ok(Y, ref, np.float32)
@@ -191,8 +205,9 @@ def test_f16_8bit_on_the_float32_gemv(gpu, M, K, N, bits, bs, zp, bias):
     A, S = A.astype(np.float16), S.astype(np.float16)
     b = None if b is None else b.astype(np.float16)
     kind = None if zp is None else ("packed" if zp == "packed" else "float")
-    want = "gemm_f32_mfma" if M > 16 and zp not in ("float", "float16") and bs >= 32 else "gemv_q4_f32"
-    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float16, kind) == want
+    want = want_kernel(M, bs, zp, True)
+    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float16, kind,
+                               zp_dtype=torch.float32 if zp == "float" else None) == want
     Y = ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, bits=bits, block_size=bs)
     assert Y.dtype == torch.float16
     Y = Y.cpu().numpy()
@@ -211,6 +226,8 @@ F16_MFMA_CASES = [
     (65, 1024, 300, 2, 32, None, True),
     (33, 2048, 96, 8, 64, "packed", True),       # one column tile: K split
     (200, 1000, 257, 8, 256, None, False),       # partial last block (K % 8 == 0)
+    (128, 5120, 1040, 2, 128, "float16", False),  # upstream bonsai2: float16 zero points
+    (64, 2048, 300, 8, 64, "float16", True),
 ]
 
 
@@ -225,7 +242,7 @@ def test_f16_wide_codes_on_the_mfma_gemm(gpu, M, K, N, bits, bs, zp, bias):
     A, B, S, Z, b = case(rng, M, K, N, bits, bs, zp, bias)
     A, S = A.astype(np.float16), S.astype(np.float16)
     b = None if b is None else b.astype(np.float16)
-    kind = None if zp is None else "packed"
+    kind = None if zp is None else ("packed" if zp == "packed" else "float")
     assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.float16, kind) == "gemm_f32_mfma"
     Y = ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), dev(b), K=K, N=N, bits=bits, block_size=bs)
     assert Y.dtype == torch.float16
@@ -236,3 +253,33 @@ def test_f16_wide_codes_on_the_mfma_gemm(gpu, M, K, N, bits, bs, zp, bias):
     exact = O.matmul_nbits(A, B, S, Z, b, K=K, N=N, bits=bits, block_size=bs, out_dtype=np.float64)
     bound = np.abs(exact) * 2.0 ** -11 + 1e-5 * np.abs(exact).max()
     assert np.all(np.abs(Y.astype(np.float64) - exact) <= bound)
+
+
+@pytest.mark.parametrize("dt,bits,bs,zp", [(np.float32, 4, 64, "float"), (np.float32, 8, 128, "float"),
+                                           (np.float16, 2, 128, "float16"), (np.float32, 4, 32, "packed"),
+                                           (np.float16, 8, 64, None)])
+def test_mfma_gemm_nonfinite_rows(gpu, dt, bits, bs, zp):
+    """Rows holding +Inf, -Inf and NaN among finite rows, fractional float zero
+    points: with float zero points such rows are recomputed in the
+    reference's serial form (the integer / fraction split of z would turn
+    Inf * (code - z) into Inf * 0); with integer zero points Inf * (code - z)
+    is the reference's product already. Every element matches the oracle:
+    non-finite ones exactly, finite rows within the bar."""
+    M, K, N = 40, 1024, 300
+    rng = np.random.default_rng(bits * 100 + bs)
+    A, B, S, Z, _ = case(rng, M, K, N, bits, bs, zp, False)
+    A[3, 17] = np.inf
+    A[7, 500] = -np.inf
+    A[11, 1000] = np.nan
+    A[20, 5] = np.inf
+    A[20, 6] = -np.inf
+    A, S = A.astype(dt), S.astype(dt)
+    if zp == "float16":
+        Z = Z.astype(np.float16)
+    kind = None if zp is None else ("packed" if zp == "packed" else "float")
+    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.from_numpy(A).dtype, kind) == "gemm_f32_mfma"
+    Y = ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), None, K=K, N=N, bits=bits, block_size=bs).cpu().numpy()
+    ref = O.matmul_nbits(A, B, S, Z, None, K=K, N=N, bits=bits, block_size=bs)
+    ok, err, lim = O.tolerance_ok(Y, ref, dt)
+    assert ok, (err, lim, np.argwhere(np.isfinite(Y) != np.isfinite(ref))[:5])
+    assert not np.isfinite(ref[3]).any() and np.isnan(ref[11]).all() and np.isfinite(ref[0]).all()

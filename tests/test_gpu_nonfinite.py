@@ -75,6 +75,8 @@ MNB_CASES = [
     (3, 2048, 33, 64, np.float32, "float", "gemv_q4_f32"),
     (1, 4096, 64, 16, np.float32, None, "gemv_q4_f32"),
     (4, 100, 17, 32, np.float16, None, "generic"),   # K % 8 != 0
+    (48, 512, 128, 32, np.float32, "packed", "gemm_f32_mfma"),  # float32 prefill rows
+    (40, 1024, 96, 64, np.float32, "float", "gemm_f32_mfma"),   # float zero points: rows recomputed
 ]
 
 

@@ -152,7 +152,12 @@ int64_t xrmm_matmul_nbits_workspace_bytes(int64_t M, int64_t K, int64_t N, int32
   L.p[0].scales = dummy;
   L.ws = const_cast<uint8_t*>(dummy);
   const xrmm::Kernel k = M > 0 ? xrmm::select_kernel(L) : xrmm::K_GENERIC;
-  if (k == xrmm::K_GEMM_F32X) return xrmm::f32x_workspace_bytes(L);
+  if (k == xrmm::K_GEMM_F32X) {
+    // sized for float zero points (their row sums), the kind that needs most
+    xrmm::Launch Lz = L;
+    Lz.zp_kind = xrmm::ZP_FLOAT;
+    return xrmm::f32x_workspace_bytes(Lz);
+  }
   if (k != xrmm::K_GEMM_Q4 && k != xrmm::K_GEMM_THIN) return 0;
   L.ws = nullptr;
   return xrmm::gemm_workspace_bytes(L, xrmm::gemm_splits(L));

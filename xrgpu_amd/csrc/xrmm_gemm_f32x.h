@@ -7,7 +7,12 @@
 // Arithmetic. The codes enter v_mfma_f32_32x32x16_f16 as the exact binary16
 // integers code - z (z the packed zero point or the midpoint 2^(bits - 1)),
 // each block's float32 sum is multiplied by the block's float32 scale as it
-// joins the row's running sum, and the bias is added once at the end.
+// joins the row's running sum, and the bias is added once at the end. A float
+// zero point z splits into zi = rint(z) (the integer the codes meet) and
+// zf = z - zi: the block then also adds -scale * zf * (the block's sum of the
+// row's activations), sums the prepass computes. A row holding +-Inf or NaN
+// is recomputed by k_fx_fix in the reference's serial form (the split would
+// turn Inf * (code - z) into Inf * 0 where code == zi).
 //  * float16 activations are exact binary16 operands: every product and every
 //    block sum is exact or float32-rounded, the output is rounded once.
 //  * float32 activations are first prepared by k_fx_prep: each row scaled by a
@@ -18,12 +23,13 @@
 //    about 22 bits of the activation and the result meets the float32 bar
 //    (1e-5 max|Y|); the power of two is undone at the end.
 //
-// Launches: k_fx_prep (float32 only: one workgroup per row), k_gemm_fx
+// Launches: k_fx_prep (float32 activations, or float zero points: one
+// workgroup per row), k_gemm_fx
 // (64-row x 256-column tiles over 8 waves of 32 x 64, K steps of 64 through a
 // double-buffered LDS; the codes stay raw dwords in LDS and each wave
 // dequantises a fragment's eight codes as it reads them; optionally K split
-// over workgroups), and with split K k_fx_combine (the splits added in split
-// order, then the bias).
+// over workgroups), with split K k_fx_combine (the splits added in split
+// order, then the bias), and with float zero points k_fx_fix.
 #pragma once
 
 #include <atomic>
@@ -36,15 +42,18 @@ namespace fx {
 
 struct Args {
   const void* A;     // float16 activations [M][K] (read directly)
-  const f16* Ahi;    // float32 activations, prepared: [M][Kd] binary16 terms
+  const f16* Ahi;    // float32 activations, prepared: [M][Kd] binary16 terms (Kd: K padded to whole K steps)
   const f16* Alo;
   const uint8_t* B;
   const void* S;     // scales [N][kb], the activations' type
-  const uint8_t* Z;  // packed zero points or null
+  const uint8_t* Z;   // packed zero points or null
+  const void* Zf;     // float zero points [N][kb] (the activations' type) or null
   const void* bias;
   void* Y;
-  const int32_t* ex;  // float32 activations: the row exponents
-  float* part;        // [splits][M][N] with split K
+  const int32_t* ex;   // float32 activations: the row exponents
+  const float* rsum;   // float zero points: block sums of the (scaled) rows, [kb][M]
+  const int32_t* bad;  // float zero points: rows holding +-Inf or NaN
+  float* part;         // [splits][M][N] with split K
   int M, K, N, kb, bs, Kd, rowb, zrow, bits, splits;
 };
 
@@ -84,53 +93,105 @@ __device__ __forceinline__ float fin_abs(float x) {
   return __builtin_isfinite(v) ? v : 0.f;
 }
 
-// One workgroup per float32 row: its exponent into ex[m] and its binary16
-// terms hi / lo into [m][Kd] in pair order (c0 c4 c1 c5 c2 c6 c3 c7 within
-// each group of eight, the order the weight fragments are dequantised in),
-// zero from K to Kd. Needs K % 4 == 0 and a 16-byte aligned A.
-__global__ __launch_bounds__(256) void k_fx_prep(const float* __restrict__ A, int K, int Kd, int32_t* __restrict__ ex,
-                                                 f16* __restrict__ hi, f16* __restrict__ lo) {
+// One workgroup per row. HL (float32 activations): the row's exponent into
+// ex[m] and its binary16 terms hi / lo into [m][Kd] in pair order (c0 c4 c1
+// c5 c2 c6 c3 c7 within each group of eight, the order the weight fragments
+// are dequantised in), zero from K to Kd. RS (float zero points): whether the
+// row holds +-Inf or NaN into bad[m], and the float32 sums of its (scaled)
+// values over each block into rsum[b][m] (zero for such a row). vec: K % VW
+// == 0 and A 16-byte aligned (16-byte loads), else element loads.
+template <typename TA, bool HL, bool RS>
+__global__ __launch_bounds__(256) void k_fx_prep(const TA* __restrict__ A, int M, int K, int Kd, int bs, int kb, int vec,
+                                                 int32_t* __restrict__ ex, f16* __restrict__ hi, f16* __restrict__ lo,
+                                                 float* __restrict__ rsum, int32_t* __restrict__ bad) {
+  constexpr int VW = 16 / sizeof(TA);
   __shared__ float red[4];
+  __shared__ int nred[4];
   const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
-  const float* row = A + static_cast<int64_t>(m) * K;
+  const TA* row = A + static_cast<int64_t>(m) * K;
   float mx = 0.f;
-  for (int k = tid * 4; k < K; k += 1024) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(row + k);
-    mx = fmaxf(fmaxf(mx, fin_abs(v.x)), fmaxf(fin_abs(v.y), fmaxf(fin_abs(v.z), fin_abs(v.w))));
+  int nf = 0;
+  auto see = [&](float x) {
+    const float v = __builtin_fabsf(x);
+    if (__builtin_isfinite(v)) mx = fmaxf(mx, v);
+    else nf = 1;
+  };
+  if (vec) {
+    for (int k = tid * VW; k < K; k += 256 * VW) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(row + k);
+      if constexpr (VW == 4) {
+        const f32x4 v = __builtin_bit_cast(f32x4, w);
+        see(v.x), see(v.y), see(v.z), see(v.w);
+      } else {
+        const f16x8 v = __builtin_bit_cast(f16x8, w);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) see(static_cast<float>(v[q]));
+      }
+    }
+  } else {
+    for (int k = tid; k < K; k += 256) see(static_cast<float>(row[k]));
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if (lane == 0) red[tid >> 6] = mx;
+  for (int off = 32; off > 0; off >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    nf |= __shfl_xor(nf, off, 64);
+  }
+  if (lane == 0) {
+    red[tid >> 6] = mx;
+    nred[tid >> 6] = nf;
+  }
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const int e = row_exp(mx);
-  if (tid == 0) ex[m] = e;
+  nf = nred[0] | nred[1] | nred[2] | nred[3];
+  const int e = HL ? row_exp(mx) : 0;
   const float rs = __builtin_ldexpf(1.f, -e);
-  f16* h = hi + static_cast<int64_t>(m) * Kd;
-  f16* l = lo + static_cast<int64_t>(m) * Kd;
-  for (int g = tid; g < Kd / 8; g += 256) {
-    const int k0 = g * 8;
-    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    const f32x4 v0 = k0 < K ? *reinterpret_cast<const f32x4*>(row + k0) : zero;
-    const f32x4 v1 = k0 + 4 < K ? *reinterpret_cast<const f32x4*>(row + k0 + 4) : zero;
-    const float xs[8] = {v0.x, v1.x, v0.y, v1.y, v0.z, v1.z, v0.w, v1.w};  // pair order
-    f16x8 vh, vl;
+  if (tid == 0) {
+    if constexpr (HL) ex[m] = e;
+    if constexpr (RS) bad[m] = nf;
+  }
+  if constexpr (HL) {
+    f16* h = hi + static_cast<int64_t>(m) * Kd;
+    f16* l = lo + static_cast<int64_t>(m) * Kd;
+    for (int g = tid; g < Kd / 8; g += 256) {
+      const int k0 = g * 8;
+      float x8[8];
+      if (vec) {
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 v0 = k0 < K ? *reinterpret_cast<const f32x4*>(row + k0) : zero;
+        const f32x4 v1 = k0 + 4 < K ? *reinterpret_cast<const f32x4*>(row + k0 + 4) : zero;
+        x8[0] = v0.x, x8[1] = v0.y, x8[2] = v0.z, x8[3] = v0.w;
+        x8[4] = v1.x, x8[5] = v1.y, x8[6] = v1.z, x8[7] = v1.w;
+      } else {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const float x = xs[q] * rs;
-      const f16 t = static_cast<f16>(x);
-      vh[q] = t;
-      vl[q] = __builtin_isfinite(x) ? static_cast<f16>(x - static_cast<float>(t)) : static_cast<f16>(0.f);
+        for (int q = 0; q < 8; ++q) x8[q] = k0 + q < K ? static_cast<float>(row[k0 + q]) : 0.f;
+      }
+      f16x8 vh, vl;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float x = x8[(q >> 1) + 4 * (q & 1)] * rs;  // pair order 0 4 1 5 2 6 3 7
+        const f16 t = static_cast<f16>(x);
+        vh[q] = t;
+        vl[q] = __builtin_isfinite(x) ? static_cast<f16>(x - static_cast<float>(t)) : static_cast<f16>(0.f);
+      }
+      *reinterpret_cast<f16x8*>(h + k0) = vh;
+      *reinterpret_cast<f16x8*>(l + k0) = vl;
     }
-    *reinterpret_cast<f16x8*>(h + k0) = vh;
-    *reinterpret_cast<f16x8*>(l + k0) = vl;
+  }
+  if constexpr (RS) {
+    for (int b = tid; b < kb; b += 256) {
+      const int k1 = (b + 1) * bs < K ? (b + 1) * bs : K;
+      float acc = 0.f;
+      for (int k = b * bs; k < k1; ++k) acc += static_cast<float>(row[k]) * rs;
+      rsum[static_cast<int64_t>(b) * M + m] = nf ? 0.f : acc;
+    }
   }
 }
 
-// Block modes: 2, 4 = blocks of 32, 64 codes (a block's sum is scaled every
-// 2, 4 MFMA K slices); 8 = blocks of 128 or more (scaled at the end of every
+// Zero points ZK: 0 none (the midpoint), 1 packed, 2 float. Block modes BKM:
+// 2, 4 = blocks of 32, 64 codes (a block's sum is scaled every 2, 4 MFMA K
+// slices); 8 = blocks of 128 or more (scaled at the end of every
 // block_size / 64 K steps).
-template <typename T, int BITS, bool ZP, int BKM>
+template <typename T, int BITS, int ZK, int BKM>
 __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
   constexpr bool LO = std::is_same<T, float>::value;  // float32 activations: hi and lo terms
   constexpr int STAGE = stage_halfs<LO, BITS>();
@@ -139,6 +200,7 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
   extern __shared__ __align__(16) unsigned char smem[];
   f16* lds = reinterpret_cast<f16*>(smem);
   __shared__ float s_ru[RT];  // 2^e per row
+  __shared__ __align__(16) float s_rsum[2][2][RT];  // float zero points: [stage][block of the step][row]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
@@ -170,14 +232,26 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
   const int kstep0 = sp * kper;
   const int ksteps = kall - kstep0 < kper ? kall - kstep0 : kper;
 
+  constexpr int NB = BKM == 8 ? 1 : 4 / BKM;  // blocks touched per step
   struct Regs {
     u32x4 a[LO ? 2 : 1];
     u32x4 b[BITS == 8 ? 2 : 1];
     u32x2 b2;  // 2-bit codes
+    float rs;  // float zero points: a row's block sum (threads below RT * NB)
   };
   auto gload = [&](Regs& r, int ks) {
     const bool ok = ks < ksteps;
     const int k = (kstep0 + ks) * KS + agrp * 8;
+    if constexpr (ZK == 2) {
+      // row tid % RT's sum over block tid / RT of the step, from an address
+      // clamped into range (threads past RT * NB store nothing)
+      const int f = tid / RT < NB ? tid / RT : NB - 1;
+      const int kst = kstep0 + (ks < ksteps ? ks : ksteps - 1);
+      const int b = BKM == 8 ? (kst * KS) / a.bs : kst * NB + f;
+      const int blk = b < a.kb ? b : a.kb - 1;
+      const int m = m0 + (tid & (RT - 1)) < a.M ? m0 + (tid & (RT - 1)) : a.M - 1;
+      r.rs = a.rsum[static_cast<int64_t>(blk) * a.M + m];
+    }
     if constexpr (LO) {
       // the prepared terms are zero from K to Kd
       const uint32_t off = ok && am < a.M ? (static_cast<uint32_t>(am) * static_cast<uint32_t>(a.Kd) + static_cast<uint32_t>(k)) * 2u : OOB;
@@ -200,6 +274,9 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
     f16* Ah = lds + stage * STAGE;
     f16* Al = Ah + RT * LD;
     uint32_t* Bw = reinterpret_cast<uint32_t*>(Ah + (LO ? 2 : 1) * RT * LD);
+    if constexpr (ZK == 2) {
+      if (tid < RT * NB) s_rsum[stage][tid / RT][tid & (RT - 1)] = r.rs;
+    }
     if constexpr (LO) {
       *reinterpret_cast<u32x4*>(Ah + arow * LD + agrp * 8) = r.a[0];
       *reinterpret_cast<u32x4*>(Al + arow * LD + agrp * 8) = r.a[1];
@@ -237,22 +314,34 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
     const int c = n0 + wn * 64 + j * 32 + (lane & 31);
     col[j] = c < a.N ? c : a.N - 1;
   }
-  // Per block and column: the scale and the dequantisation constants
-  // -(base + z), z the zero point, exact in binary16; the bases are the
-  // values of the magic exponents the code bits are or-ed into.
+  // Per block and column: the scale, the dequantisation constants
+  // -(base + z), z the (integer) zero point, exact in binary16 (the bases are
+  // the values of the magic exponents the code bits are or-ed into), and for
+  // float zero points -scale * (z - zi), zi = rint(z) in [-1024, 1024].
   struct Meta {
     float s[2];
     f16x2 n[NQ][2];
+    float nz[ZK == 2 ? 2 : 1];
   };
-  auto mload = [&](int blk) {
+  auto mload = [&](int blk0) {
+    // a block past the last (the second half of a last K step of blocks of
+    // 32) has scale zero; its codes (the next column's, or zeros) meet zero
+    // activations
+    const bool past = blk0 >= a.kb;
+    const int blk = past ? a.kb - 1 : blk0;
     Meta mt;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      mt.s[j] = static_cast<float>(static_cast<const T*>(a.S)[static_cast<int64_t>(col[j]) * a.kb + blk]);
+      const float sv = static_cast<float>(static_cast<const T*>(a.S)[static_cast<int64_t>(col[j]) * a.kb + blk]);
+      mt.s[j] = past ? 0.f : sv;
       float z = static_cast<float>(1 << (BITS - 1));
-      if constexpr (ZP) {
+      if constexpr (ZK == 1) {
         const uint32_t zb = a.Z[static_cast<int64_t>(col[j]) * a.zrow + (blk * BITS) / 8];
         z = static_cast<float>((zb >> ((blk * BITS) % 8)) & ((1u << BITS) - 1u));
+      } else if constexpr (ZK == 2) {
+        const float zv = static_cast<float>(static_cast<const T*>(a.Zf)[static_cast<int64_t>(col[j]) * a.kb + blk]);
+        z = fminf(fmaxf(__builtin_rintf(zv), -1024.f), 1024.f);  // NaN -> -1024, its fraction NaN
+        mt.nz[j] = past ? 0.f : -(mt.s[j] * (zv - z));
       }
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
@@ -301,18 +390,31 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
     acc[j] = zero16;
     yacc[j] = zero16;
   }
-  // a block's sums into the running sums; blocks of 128 or more codes start
-  // from zeroed sums, shorter ones from a zero accumulator operand
-  auto flush = [&](const Meta& mt) {
+  // a block's sums into the running sums (with float zero points, plus
+  // -scale * zf * the row's block sum, block f of the step on `stage`);
+  // blocks of 128 or more codes start from zeroed sums, shorter ones from a
+  // zero accumulator operand
+  auto flush = [&](const Meta& mt, int stage, int f) {
+    float rr[16];
+    if constexpr (ZK == 2) {
+      // the lane's rows wm 32 + 8 (q / 4) + 4 (lane / 32) + q % 4, by name
+      const float* rp = &s_rsum[stage][f][wm * 32 + 4 * (lane >> 5)];
+      const f32x4 v0 = *reinterpret_cast<const f32x4*>(rp), v1 = *reinterpret_cast<const f32x4*>(rp + 8);
+      const f32x4 v2 = *reinterpret_cast<const f32x4*>(rp + 16), v3 = *reinterpret_cast<const f32x4*>(rp + 24);
+      const float t[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+#pragma unroll
+      for (int q = 0; q < 16; ++q) rr[q] = t[q];
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
-        yacc[j][q] = __builtin_fmaf(mt.s[j], acc[j][q], yacc[j][q]);
+        float y = yacc[j][q];
+        if constexpr (ZK == 2) y = __builtin_fmaf(mt.nz[j], rr[q], y);
+        yacc[j][q] = __builtin_fmaf(mt.s[j], acc[j][q], y);
         if constexpr (BKM == 8) acc[j][q] = 0.f;
       }
   };
-  constexpr int NB = BKM == 8 ? 1 : 4 / BKM;  // blocks touched per step
   auto mfmas = [&](int stage, const Meta (&mt)[NB]) {
     const f16* Ah = lds + stage * STAGE;
     const f16* Al = Ah + RT * LD;
@@ -335,7 +437,7 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
         if constexpr (LO) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fl, fb, acc[j], 0, 0, 0);
       }
       if constexpr (BKM != 8) {
-        if ((kk + 1) % BKM == 0) flush(m);
+        if ((kk + 1) % BKM == 0) flush(m, stage, kk / BKM);
       }
     }
   };
@@ -358,7 +460,7 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
     __builtin_amdgcn_sched_barrier(0);
     mfmas(stage, mc);
     if constexpr (BKM == 8) {
-      if ((kstep0 + ks + 1) % bsteps == 0) flush(mc[0]);
+      if ((kstep0 + ks + 1) % bsteps == 0) flush(mc[0], stage, 0);
     }
     if (ks + 1 < ksteps) sstore(nxt, stage ^ 1);
     __syncthreads();
@@ -410,9 +512,35 @@ __global__ __launch_bounds__(256) void k_fx_combine(Args a) {
   static_cast<T*>(a.Y)[i] = static_cast<T>(y);
 }
 
-template <typename T, int BITS, bool ZP, int BKM>
+// Float zero points: rows holding +-Inf or NaN recomputed in the reference's
+// serial form, W = (code - z) * scale in float32 and one float32 sum over K
+// (complex_kernel.glsl:80,83); one workgroup per row, the others exit at once.
+template <typename T, int BITS>
+__global__ __launch_bounds__(256) void k_fx_fix(Args a) {
+  const int m = blockIdx.x;
+  if (!a.bad[m]) return;
+  const T* row = static_cast<const T*>(a.A) + static_cast<int64_t>(m) * a.K;
+  const T* S = static_cast<const T*>(a.S);
+  const T* Zf = static_cast<const T*>(a.Zf);
+  const int blob = a.bs * BITS / 8;
+  for (int n = threadIdx.x; n < a.N; n += 256) {
+    const uint8_t* Bn = a.B + static_cast<int64_t>(n) * a.rowb;
+    float acc = 0.f;
+    for (int k = 0; k < a.K; ++k) {
+      const int b = k / a.bs, e = k - b * a.bs;
+      const uint32_t c = (static_cast<uint32_t>(Bn[b * blob + (e * BITS) / 8]) >> ((e * BITS) % 8)) & ((1u << BITS) - 1u);
+      const int64_t i = static_cast<int64_t>(n) * a.kb + b;
+      const float w = (static_cast<float>(c) - static_cast<float>(Zf[i])) * static_cast<float>(S[i]);
+      acc += static_cast<float>(row[k]) * w;
+    }
+    if (a.bias) acc += static_cast<float>(static_cast<const T*>(a.bias)[n]);
+    static_cast<T*>(a.Y)[static_cast<int64_t>(m) * a.N + n] = static_cast<T>(acc);
+  }
+}
+
+template <typename T, int BITS, int ZK, int BKM>
 hipError_t launch1(const Args& a, int nct, int64_t grid, hipStream_t st) {
-  auto kern = k_gemm_fx<T, BITS, ZP, BKM>;
+  auto kern = k_gemm_fx<T, BITS, ZK, BKM>;
   constexpr size_t lds = lds_bytes<std::is_same<T, float>::value, BITS>();
   if constexpr (lds > 64 * 1024) {
     static std::atomic<int> done[kMaxDevices];  // per instantiation and device
@@ -423,29 +551,47 @@ hipError_t launch1(const Args& a, int nct, int64_t grid, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <typename T, int BITS, bool ZP>
+// Blocks of 32 with float zero points are not instantiated (their block
+// metadata and row sums would spill).
+template <typename T, int BITS, int ZK>
 hipError_t launch_b(const Args& a, int nct, int64_t grid, hipStream_t st) {
-  if (a.bs == 32) return launch1<T, BITS, ZP, 2>(a, nct, grid, st);
-  if (a.bs == 64) return launch1<T, BITS, ZP, 4>(a, nct, grid, st);
-  return launch1<T, BITS, ZP, 8>(a, nct, grid, st);
+  if (a.bs == 32) {
+    if constexpr (ZK == 2) return hipErrorInvalidValue;
+    else return launch1<T, BITS, ZK, 2>(a, nct, grid, st);
+  }
+  if (a.bs == 64) return launch1<T, BITS, ZK, 4>(a, nct, grid, st);
+  return launch1<T, BITS, ZK, 8>(a, nct, grid, st);
 }
 
-// The GEMM (and the combine with split K) for activations of type T.
-template <typename T>
-hipError_t launch_gemm(const Args& a, hipStream_t st) {
-  const int nct = (a.N + CT - 1) / CT;
-  const int64_t grid = static_cast<int64_t>((a.M + RT - 1) / RT) * nct * a.splits;
-  const bool zp = a.Z != nullptr;
-  hipError_t e;
-  if (a.bits == 8) e = zp ? launch_b<T, 8, true>(a, nct, grid, st) : launch_b<T, 8, false>(a, nct, grid, st);
-  else if (a.bits == 2) e = zp ? launch_b<T, 2, true>(a, nct, grid, st) : launch_b<T, 2, false>(a, nct, grid, st);
-  else e = zp ? launch_b<T, 4, true>(a, nct, grid, st) : launch_b<T, 4, false>(a, nct, grid, st);
+template <typename T, int BITS>
+hipError_t launch_z(const Args& a, int nct, int64_t grid, hipStream_t st) {
+  if (a.Zf) {
+    if (hipError_t e = launch_b<T, BITS, 2>(a, nct, grid, st); e != hipSuccess) return e;
+    if (a.splits > 1) {
+      const int64_t MN = static_cast<int64_t>(a.M) * a.N;
+      hipLaunchKernelGGL(k_fx_combine<T>, dim3(static_cast<uint32_t>((MN + 255) / 256)), dim3(256), 0, st, a);
+    }
+    hipLaunchKernelGGL((k_fx_fix<T, BITS>), dim3(static_cast<uint32_t>(a.M)), dim3(256), 0, st, a);
+    return hipGetLastError();
+  }
+  hipError_t e = a.Z ? launch_b<T, BITS, 1>(a, nct, grid, st) : launch_b<T, BITS, 0>(a, nct, grid, st);
   if (e != hipSuccess) return e;
   if (a.splits > 1) {
     const int64_t MN = static_cast<int64_t>(a.M) * a.N;
     hipLaunchKernelGGL(k_fx_combine<T>, dim3(static_cast<uint32_t>((MN + 255) / 256)), dim3(256), 0, st, a);
   }
   return hipGetLastError();
+}
+
+// The GEMM (then the combine with split K, and the recomputation of
+// non-finite rows with float zero points) for activations of type T.
+template <typename T>
+hipError_t launch_gemm(const Args& a, hipStream_t st) {
+  const int nct = (a.N + CT - 1) / CT;
+  const int64_t grid = static_cast<int64_t>((a.M + RT - 1) / RT) * nct * a.splits;
+  if (a.bits == 8) return launch_z<T, 8>(a, nct, grid, st);
+  if (a.bits == 2) return launch_z<T, 2>(a, nct, grid, st);
+  return launch_z<T, 4>(a, nct, grid, st);
 }
 
 }  // namespace

@@ -12,15 +12,22 @@ int64_t al256(int64_t b) { return (b + 255) / 256 * 256; }
 // The workspace's first kFxKeep bytes are left alone: front ends share one
 // workspace between this GEMM and the split-K GEMMs, whose arrival counters
 // live there and must stay zero. Then, for float32 activations, the row
-// exponents and the prepared binary16 terms (hi, lo); then the split
+// exponents and the prepared binary16 terms (hi, lo); for float zero points
+// the rows' block sums [kb][M] and their non-finite flags; then the split
 // partials.
 constexpr int64_t kFxKeep = 4096;
 
-int64_t fx_kd(const Launch& L) { return L.kb * L.block_size; }
+// K padded to whole K steps of 64 (blocks of 32 may leave half a step,
+// which the kernel reads as a block past the last, of scale zero)
+int64_t fx_kd(const Launch& L) { return (L.kb * L.block_size + fx::KS - 1) / fx::KS * fx::KS; }
 
-int64_t fx_prep_bytes(const Launch& L) {
+int64_t fx_hl_bytes(const Launch& L) {
   return L.dtype == DT_F32 ? al256(L.M * 4) + 2 * al256(L.M * fx_kd(L) * 2) : 0;
 }
+int64_t fx_rs_bytes(const Launch& L) {
+  return L.zp_kind == ZP_FLOAT ? al256(L.kb * L.M * 4) + al256(L.M * 4) : 0;
+}
+int64_t fx_prep_bytes(const Launch& L) { return fx_hl_bytes(L) + fx_rs_bytes(L); }
 
 }  // namespace
 
@@ -41,26 +48,26 @@ int64_t f32x_workspace_bytes(const Launch& L) {
 }
 
 // MatMulNBits with more than 16 rows: float32 activations with 2-, 4- or
-// 8-bit codes, float16 activations with 2- or 8-bit codes (4-bit with exact
-// weights); blocks of 32 or more codes (powers of two), a padded K that is a
-// multiple of 64, K a multiple of 4 (float32) or 8 (float16), packed or no
-// zero points, 16-byte aligned tensors, 32-bit offsets. The caller supplies
-// the workspace.
+// 8-bit codes (any K), float16 activations with 2- or 8-bit codes (4-bit with
+// exact weights; K a multiple of 8, A 16-byte aligned); blocks of 32 or more
+// codes (powers of two), packed, float
+// (of the activations' type, blocks of 64 or more) or no zero points,
+// 16-byte aligned B, 32-bit offsets. The caller supplies the workspace.
 bool f32x_fits(const Launch& L) {
   if (L.op != OP_MATMUL || L.M <= 16 || (L.bits != 2 && L.bits != 4 && L.bits != 8)) return false;
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   if (L.dtype == DT_F16) {
     if (L.bits == 4 && !L.exact_weights) return false;  // the binary16 GEMMs
-    if (L.K % 8 != 0) return false;
-  } else if (L.dtype != DT_F32 || L.K % 4 != 0) {
+    if (L.K % 8 != 0 || !al(L.A)) return false;
+  } else if (L.dtype != DT_F32) {
     return false;
   }
-  if (L.block_size < 32 || L.bs_log2 < 5 || fx_kd(L) % fx::KS != 0) return false;
-  if (L.zp_kind == ZP_FLOAT) return false;
-  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-  if (!al(L.A) || !al(L.p[0].B) || !al(L.p[0].scales)) return false;
-  const int64_t lim = int64_t(1) << 31, rowb = fx_kd(L) * L.bits / 8;
-  return L.M * fx_kd(L) * 4 < lim && L.p[0].N * rowb < lim && int64_t(f32x_splits(L)) * L.M * L.p[0].N < lim &&
-         L.M < lim / fx::RT;
+  if (L.block_size < 32 || L.bs_log2 < 5) return false;
+  if (L.zp_kind == ZP_FLOAT && (L.zp_dtype != L.dtype || L.p[0].zp == nullptr || L.block_size < 64)) return false;
+  if (!al(L.p[0].B)) return false;
+  const int64_t lim = int64_t(1) << 31, rowb = fx_kd(L) * L.bits / 8;  // rows as read (past the last: zeros)
+  return L.M * fx_kd(L) * 4 < lim && L.M * L.K * 4 < lim && L.p[0].N * rowb < lim && L.kb * L.M * 4 < lim &&
+         int64_t(f32x_splits(L)) * L.M * L.p[0].N < lim && L.p[0].N * L.kb < lim && L.M < lim / fx::RT;
 }
 
 hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st) {
@@ -69,6 +76,7 @@ hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st) {
   a.B = L.p[0].B;
   a.S = L.p[0].scales;
   a.Z = L.zp_kind == ZP_PACKED ? static_cast<const uint8_t*>(L.p[0].zp) : nullptr;
+  a.Zf = L.zp_kind == ZP_FLOAT ? L.p[0].zp : nullptr;
   a.bias = L.p[0].bias;
   a.Y = L.p[0].Y;
   a.M = static_cast<int>(L.M);
@@ -77,22 +85,43 @@ hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st) {
   a.kb = static_cast<int>(L.kb);
   a.bs = static_cast<int>(L.block_size);
   a.Kd = static_cast<int>(fx_kd(L));
-  a.rowb = static_cast<int>(fx_kd(L) * L.bits / 8);
+  a.rowb = static_cast<int>(L.kb * L.block_size * L.bits / 8);
   a.zrow = static_cast<int>(L.zrow);
   a.bits = L.bits;
   a.splits = f32x_splits(L);
   uint8_t* w = static_cast<uint8_t*>(L.ws) + kFxKeep;
+  int32_t* ex = nullptr;
+  f16 *hi = nullptr, *lo = nullptr;
   if (L.dtype == DT_F32) {
-    int32_t* ex = reinterpret_cast<int32_t*>(w);
-    f16* hi = reinterpret_cast<f16*>(w + al256(L.M * 4));
-    f16* lo = hi + al256(L.M * fx_kd(L) * 2) / 2;
-    a.ex = ex;
-    a.Ahi = hi;
-    a.Alo = lo;
-    hipLaunchKernelGGL(fx::k_fx_prep, dim3(static_cast<uint32_t>(L.M)), dim3(256), 0, st, static_cast<const float*>(L.A),
-                       a.K, a.Kd, ex, hi, lo);
-    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    ex = reinterpret_cast<int32_t*>(w);
+    hi = reinterpret_cast<f16*>(w + al256(L.M * 4));
+    lo = hi + al256(L.M * fx_kd(L) * 2) / 2;
   }
+  float* rsum = nullptr;
+  int32_t* bad = nullptr;
+  if (L.zp_kind == ZP_FLOAT) {
+    rsum = reinterpret_cast<float*>(w + fx_hl_bytes(L));
+    bad = reinterpret_cast<int32_t*>(w + fx_hl_bytes(L) + al256(L.kb * L.M * 4));
+  }
+  a.ex = ex;
+  a.Ahi = hi;
+  a.Alo = lo;
+  a.rsum = rsum;
+  a.bad = bad;
+  const dim3 pg(static_cast<uint32_t>(L.M)), pb(256);
+  const int vecf = (L.K % 4 == 0 && (reinterpret_cast<uintptr_t>(L.A) & 15u) == 0) ? 1 : 0;
+  const float* Af = static_cast<const float*>(L.A);
+  const f16* Ah = static_cast<const f16*>(L.A);
+  if (L.dtype == DT_F32 && rsum)
+    hipLaunchKernelGGL((fx::k_fx_prep<float, true, true>), pg, pb, 0, st, Af, a.M, a.K, a.Kd, a.bs, a.kb, vecf, ex, hi, lo,
+                       rsum, bad);
+  else if (L.dtype == DT_F32)
+    hipLaunchKernelGGL((fx::k_fx_prep<float, true, false>), pg, pb, 0, st, Af, a.M, a.K, a.Kd, a.bs, a.kb, vecf, ex, hi,
+                       lo, rsum, bad);
+  else if (rsum)  // float16: K % 8 == 0 and A 16-byte aligned
+    hipLaunchKernelGGL((fx::k_fx_prep<f16, false, true>), pg, pb, 0, st, Ah, a.M, a.K, a.Kd, a.bs, a.kb, 1, ex, hi, lo,
+                       rsum, bad);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   a.part = reinterpret_cast<float*>(w + fx_prep_bytes(L));
   return L.dtype == DT_F32 ? fx::launch_gemm<float>(a, st) : fx::launch_gemm_f16(a, st);
 }

@@ -353,9 +353,12 @@ def dequantize(B, scales, zero_points=None, *, K, bits=4, block_size=32, out_dty
     return W
 
 
-def select_kernel(op: str, M, K, N, bits=4, block_size=32, dtype=torch.float16, zp=None) -> str:
+def select_kernel(op: str, M, K, N, bits=4, block_size=32, dtype=torch.float16, zp=None, zp_dtype=None) -> str:
+    """The kernel family a call takes (with the workspaces this module
+    supplies). ``zp``: None, "packed" (uint8) or "float" (zero points of
+    ``zp_dtype``, by default the activations' dtype)."""
     code = {"MatMulNBits": 0, "MatMulNBitsQkv": 1, "MatMulNBitsMlp": 2}[op]
-    zdt = nat.UNSPECIFIED if zp is None else {"packed": nat.U8, "float": nat.F16}[zp]
+    zdt = nat.UNSPECIFIED if zp is None else nat.U8 if zp == "packed" else _T1[zp_dtype or dtype]
     r = nat.lib().xrmm_select_kernel(code, M, K, N, bits, block_size, _T1[dtype], zdt)
     if r is None:
         raise nat.XrmmInvalid(nat.last_error())
