@@ -98,17 +98,24 @@ __device__ __forceinline__ float fin_abs(float x) {
 // c5 c2 c6 c3 c7 within each group of eight, the order the weight fragments
 // are dequantised in), zero from K to Kd. RS (float zero points): whether the
 // row holds +-Inf or NaN into bad[m], and the float32 sums of its (scaled)
-// values over each block into rsum[b][m] (zero for such a row). vec: K % VW
-// == 0 and A 16-byte aligned (16-byte loads), else element loads.
-template <typename TA, bool HL, bool RS>
+// values over each block into rsum[b][m] (zero for such a row; each block's
+// sum in a fixed order, group by group). vec: K % VW == 0 and A 16-byte
+// aligned (16-byte loads), else element loads. P > 0: the row's groups of
+// eight stay in registers, P per thread (Kd <= 2048 P), and the row is read
+// once; P == 0: any Kd, the row is read again for each pass.
+constexpr int kPrepMaxGroups = 4096;  // groups of eight with P > 0 (Kd <= 32768)
+
+template <typename TA, bool HL, bool RS, int P>
 __global__ __launch_bounds__(256) void k_fx_prep(const TA* __restrict__ A, int M, int K, int Kd, int bs, int kb, int vec,
                                                  int32_t* __restrict__ ex, f16* __restrict__ hi, f16* __restrict__ lo,
                                                  float* __restrict__ rsum, int32_t* __restrict__ bad) {
   constexpr int VW = 16 / sizeof(TA);
   __shared__ float red[4];
   __shared__ int nred[4];
+  __shared__ float s_gsum[RS && P > 0 ? kPrepMaxGroups : 1];
   const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
   const TA* row = A + static_cast<int64_t>(m) * K;
+  const int ng = Kd / 8;
   float mx = 0.f;
   int nf = 0;
   auto see = [&](float x) {
@@ -116,7 +123,37 @@ __global__ __launch_bounds__(256) void k_fx_prep(const TA* __restrict__ A, int M
     if (__builtin_isfinite(v)) mx = fmaxf(mx, v);
     else nf = 1;
   };
-  if (vec) {
+  // group g's eight values (zero past K)
+  auto group = [&](int g, float (&x8)[8]) {
+    const int k0 = g * 8;
+    if (vec && VW == 4) {
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      const f32x4 v0 = k0 < K ? *reinterpret_cast<const f32x4*>(row + k0) : zero;
+      const f32x4 v1 = k0 + 4 < K ? *reinterpret_cast<const f32x4*>(row + k0 + 4) : zero;
+      x8[0] = v0.x, x8[1] = v0.y, x8[2] = v0.z, x8[3] = v0.w;
+      x8[4] = v1.x, x8[5] = v1.y, x8[6] = v1.z, x8[7] = v1.w;
+    } else if (vec) {
+      const u32x4 z4 = {0u, 0u, 0u, 0u};
+      const f16x8 v = __builtin_bit_cast(f16x8, k0 < K ? *reinterpret_cast<const u32x4*>(row + k0) : z4);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) x8[q] = static_cast<float>(v[q]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) x8[q] = k0 + q < K ? static_cast<float>(row[k0 + q]) : 0.f;
+    }
+  };
+  float xr[P > 0 ? P : 1][8];
+  if constexpr (P > 0) {
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const int g = tid + 256 * i;
+      if (g < ng) {
+        group(g, xr[i]);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) see(xr[i][q]);
+      }
+    }
+  } else if (vec) {
     for (int k = tid * VW; k < K; k += 256 * VW) {
       const u32x4 w = *reinterpret_cast<const u32x4*>(row + k);
       if constexpr (VW == 4) {
@@ -149,42 +186,75 @@ __global__ __launch_bounds__(256) void k_fx_prep(const TA* __restrict__ A, int M
     if constexpr (HL) ex[m] = e;
     if constexpr (RS) bad[m] = nf;
   }
-  if constexpr (HL) {
-    f16* h = hi + static_cast<int64_t>(m) * Kd;
-    f16* l = lo + static_cast<int64_t>(m) * Kd;
-    for (int g = tid; g < Kd / 8; g += 256) {
-      const int k0 = g * 8;
-      float x8[8];
-      if (vec) {
-        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 v0 = k0 < K ? *reinterpret_cast<const f32x4*>(row + k0) : zero;
-        const f32x4 v1 = k0 + 4 < K ? *reinterpret_cast<const f32x4*>(row + k0 + 4) : zero;
-        x8[0] = v0.x, x8[1] = v0.y, x8[2] = v0.z, x8[3] = v0.w;
-        x8[4] = v1.x, x8[5] = v1.y, x8[6] = v1.z, x8[7] = v1.w;
-      } else {
+  // the binary16 terms of one group, stored in pair order 0 4 1 5 2 6 3 7
+  auto terms = [&](int g, const float (&x8)[8]) {
+    f16x8 vh, vl;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) x8[q] = k0 + q < K ? static_cast<float>(row[k0 + q]) : 0.f;
-      }
-      f16x8 vh, vl;
+    for (int q = 0; q < 8; ++q) {
+      const float x = x8[(q >> 1) + 4 * (q & 1)] * rs;
+      const f16 t = static_cast<f16>(x);
+      vh[q] = t;
+      vl[q] = __builtin_isfinite(x) ? static_cast<f16>(x - static_cast<float>(t)) : static_cast<f16>(0.f);
+    }
+    *reinterpret_cast<f16x8*>(hi + static_cast<int64_t>(m) * Kd + g * 8) = vh;
+    *reinterpret_cast<f16x8*>(lo + static_cast<int64_t>(m) * Kd + g * 8) = vl;
+  };
+  if constexpr (P > 0) {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const float x = x8[(q >> 1) + 4 * (q & 1)] * rs;  // pair order 0 4 1 5 2 6 3 7
-        const f16 t = static_cast<f16>(x);
-        vh[q] = t;
-        vl[q] = __builtin_isfinite(x) ? static_cast<f16>(x - static_cast<float>(t)) : static_cast<f16>(0.f);
+    for (int i = 0; i < P; ++i) {
+      const int g = tid + 256 * i;
+      if (g < ng) {
+        if constexpr (HL) terms(g, xr[i]);
+        if constexpr (RS) {
+          float t = 0.f;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) t += xr[i][q] * rs;
+          s_gsum[g] = t;
+        }
       }
-      *reinterpret_cast<f16x8*>(h + k0) = vh;
-      *reinterpret_cast<f16x8*>(l + k0) = vl;
+    }
+    if constexpr (RS) {
+      __syncthreads();
+      const int gpb = bs / 8;  // groups per block
+      for (int b = tid; b < kb; b += 256) {
+        float acc = 0.f;
+        for (int g = b * gpb; g < (b + 1) * gpb; ++g) acc += s_gsum[g];
+        rsum[static_cast<int64_t>(b) * M + m] = nf ? 0.f : acc;
+      }
+    }
+  } else {
+    if constexpr (HL) {
+      for (int g = tid; g < ng; g += 256) {
+        float x8[8];
+        group(g, x8);
+        terms(g, x8);
+      }
+    }
+    if constexpr (RS) {
+      for (int b = tid; b < kb; b += 256) {
+        const int k1 = (b + 1) * bs < K ? (b + 1) * bs : K;
+        float acc = 0.f;
+        for (int k = b * bs; k < k1; ++k) acc += static_cast<float>(row[k]) * rs;
+        rsum[static_cast<int64_t>(b) * M + m] = nf ? 0.f : acc;
+      }
     }
   }
-  if constexpr (RS) {
-    for (int b = tid; b < kb; b += 256) {
-      const int k1 = (b + 1) * bs < K ? (b + 1) * bs : K;
-      float acc = 0.f;
-      for (int k = b * bs; k < k1; ++k) acc += static_cast<float>(row[k]) * rs;
-      rsum[static_cast<int64_t>(b) * M + m] = nf ? 0.f : acc;
-    }
-  }
+}
+
+// The prepass for a row of Kd: P = groups of eight per thread, 0 past
+// kPrepMaxGroups.
+template <typename TA, bool HL, bool RS>
+void launch_prep(const TA* A, int M, int K, int Kd, int bs, int kb, int vec, int32_t* ex, f16* hi, f16* lo, float* rsum,
+                 int32_t* bad, hipStream_t st) {
+  const dim3 g(static_cast<uint32_t>(M)), b(256);
+  const int ng = Kd / 8;
+  if (ng <= 256) hipLaunchKernelGGL((k_fx_prep<TA, HL, RS, 1>), g, b, 0, st, A, M, K, Kd, bs, kb, vec, ex, hi, lo, rsum, bad);
+  else if (ng <= 512) hipLaunchKernelGGL((k_fx_prep<TA, HL, RS, 2>), g, b, 0, st, A, M, K, Kd, bs, kb, vec, ex, hi, lo, rsum, bad);
+  else if (ng <= 1024) hipLaunchKernelGGL((k_fx_prep<TA, HL, RS, 4>), g, b, 0, st, A, M, K, Kd, bs, kb, vec, ex, hi, lo, rsum, bad);
+  else if (ng <= 2048) hipLaunchKernelGGL((k_fx_prep<TA, HL, RS, 8>), g, b, 0, st, A, M, K, Kd, bs, kb, vec, ex, hi, lo, rsum, bad);
+  else if (ng <= kPrepMaxGroups)
+    hipLaunchKernelGGL((k_fx_prep<TA, HL, RS, 16>), g, b, 0, st, A, M, K, Kd, bs, kb, vec, ex, hi, lo, rsum, bad);
+  else hipLaunchKernelGGL((k_fx_prep<TA, HL, RS, 0>), g, b, 0, st, A, M, K, Kd, bs, kb, vec, ex, hi, lo, rsum, bad);
 }
 
 // Zero points ZK: 0 none (the midpoint), 1 packed, 2 float. Block modes BKM:

@@ -108,19 +108,15 @@ hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st) {
   a.Alo = lo;
   a.rsum = rsum;
   a.bad = bad;
-  const dim3 pg(static_cast<uint32_t>(L.M)), pb(256);
   const int vecf = (L.K % 4 == 0 && (reinterpret_cast<uintptr_t>(L.A) & 15u) == 0) ? 1 : 0;
   const float* Af = static_cast<const float*>(L.A);
   const f16* Ah = static_cast<const f16*>(L.A);
   if (L.dtype == DT_F32 && rsum)
-    hipLaunchKernelGGL((fx::k_fx_prep<float, true, true>), pg, pb, 0, st, Af, a.M, a.K, a.Kd, a.bs, a.kb, vecf, ex, hi, lo,
-                       rsum, bad);
+    fx::launch_prep<float, true, true>(Af, a.M, a.K, a.Kd, a.bs, a.kb, vecf, ex, hi, lo, rsum, bad, st);
   else if (L.dtype == DT_F32)
-    hipLaunchKernelGGL((fx::k_fx_prep<float, true, false>), pg, pb, 0, st, Af, a.M, a.K, a.Kd, a.bs, a.kb, vecf, ex, hi,
-                       lo, rsum, bad);
+    fx::launch_prep<float, true, false>(Af, a.M, a.K, a.Kd, a.bs, a.kb, vecf, ex, hi, lo, rsum, bad, st);
   else if (rsum)  // float16: K % 8 == 0 and A 16-byte aligned
-    hipLaunchKernelGGL((fx::k_fx_prep<f16, false, true>), pg, pb, 0, st, Ah, a.M, a.K, a.Kd, a.bs, a.kb, 1, ex, hi, lo,
-                       rsum, bad);
+    fx::launch_prep<f16, false, true>(Ah, a.M, a.K, a.Kd, a.bs, a.kb, 1, ex, hi, lo, rsum, bad, st);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   a.part = reinterpret_cast<float*>(w + fx_prep_bytes(L));
   return L.dtype == DT_F32 ? fx::launch_gemm<float>(a, st) : fx::launch_gemm_f16(a, st);
