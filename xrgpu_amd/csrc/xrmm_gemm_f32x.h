@@ -25,7 +25,7 @@
 //
 // Launches: k_fx_prep (float32 activations, or float zero points: one
 // workgroup per row), k_gemm_fx
-// (64-row x 256-column tiles over 8 waves of 32 x 64, K steps of 64 through a
+// (64-row x 256-column tiles over 8 waves of 64 x 32, K steps of 64 through a
 // double-buffered LDS; the codes stay raw dwords in LDS and each wave
 // dequantises a fragment's eight codes as it reads them; optionally K split
 // over workgroups), with split K k_fx_combine (the splits added in split
@@ -273,7 +273,12 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
   __shared__ __align__(16) float s_rsum[2][2][RT];  // float zero points: [stage][block of the step][row]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 2, wn = wave & 3;
+  // a wave: IM x JN MFMA tiles of 32 x 32, here 64 rows x 32 columns, so each
+  // dequantised weight fragment feeds IM tiles (10-20 % faster than 32 rows x
+  // 64 columns, which dequantises every fragment in two waves)
+  constexpr int IM = 2, JN = 1;
+  constexpr int WR = 32 * IM, WC = 32 * JN, WNW = CT / WC;
+  const int wm = wave / WNW, wn = wave % WNW;
   // workgroup b: split b % splits of tile b / splits (column tiles fastest)
   const int sp = static_cast<int>(blockIdx.x) % a.splits, tb = static_cast<int>(blockIdx.x) / a.splits;
   const int m0 = (tb / nct) * RT, n0 = (tb % nct) * CT;
@@ -377,11 +382,11 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
     }
   };
 
-  // this lane's two columns
-  int col[2];
+  // this lane's columns
+  int col[JN];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int c = n0 + wn * 64 + j * 32 + (lane & 31);
+  for (int j = 0; j < JN; ++j) {
+    const int c = n0 + wn * WC + j * 32 + (lane & 31);
     col[j] = c < a.N ? c : a.N - 1;
   }
   // Per block and column: the scale, the dequantisation constants
@@ -389,9 +394,9 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
   // the values of the magic exponents the code bits are or-ed into), and for
   // float zero points -scale * (z - zi), zi = rint(z) in [-1024, 1024].
   struct Meta {
-    float s[2];
-    f16x2 n[NQ][2];
-    float nz[ZK == 2 ? 2 : 1];
+    float s[JN];
+    f16x2 n[NQ][JN];
+    float nz[JN];
   };
   auto mload = [&](int blk0) {
     // a block past the last (the second half of a last K step of blocks of
@@ -401,7 +406,7 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
     const int blk = past ? a.kb - 1 : blk0;
     Meta mt;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < JN; ++j) {
       const float sv = static_cast<float>(static_cast<const T*>(a.S)[static_cast<int64_t>(col[j]) * a.kb + blk]);
       mt.s[j] = past ? 0.f : sv;
       float z = static_cast<float>(1 << (BITS - 1));
@@ -454,36 +459,41 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
   };
 
   const f32x16 zero16 = {};
-  f32x16 acc[2], yacc[2];
+  f32x16 acc[IM * JN], yacc[IM * JN];  // tile (i, j) at i JN + j
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    acc[j] = zero16;
-    yacc[j] = zero16;
+  for (int t = 0; t < IM * JN; ++t) {
+    acc[t] = zero16;
+    yacc[t] = zero16;
   }
   // a block's sums into the running sums (with float zero points, plus
   // -scale * zf * the row's block sum, block f of the step on `stage`);
   // blocks of 128 or more codes start from zeroed sums, shorter ones from a
   // zero accumulator operand
   auto flush = [&](const Meta& mt, int stage, int f) {
-    float rr[16];
+    float rr[IM][16];
     if constexpr (ZK == 2) {
-      // the lane's rows wm 32 + 8 (q / 4) + 4 (lane / 32) + q % 4, by name
-      const float* rp = &s_rsum[stage][f][wm * 32 + 4 * (lane >> 5)];
-      const f32x4 v0 = *reinterpret_cast<const f32x4*>(rp), v1 = *reinterpret_cast<const f32x4*>(rp + 8);
-      const f32x4 v2 = *reinterpret_cast<const f32x4*>(rp + 16), v3 = *reinterpret_cast<const f32x4*>(rp + 24);
-      const float t[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
 #pragma unroll
-      for (int q = 0; q < 16; ++q) rr[q] = t[q];
+      for (int i = 0; i < IM; ++i) {
+        // row tile i's rows wm WR + 32 i + 8 (q / 4) + 4 (lane / 32) + q % 4, by name
+        const float* rp = &s_rsum[stage][f][wm * WR + 32 * i + 4 * (lane >> 5)];
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(rp), v1 = *reinterpret_cast<const f32x4*>(rp + 8);
+        const f32x4 v2 = *reinterpret_cast<const f32x4*>(rp + 16), v3 = *reinterpret_cast<const f32x4*>(rp + 24);
+        const float t[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w, v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+#pragma unroll
+        for (int q = 0; q < 16; ++q) rr[i][q] = t[q];
+      }
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int i = 0; i < IM; ++i)
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        float y = yacc[j][q];
-        if constexpr (ZK == 2) y = __builtin_fmaf(mt.nz[j], rr[q], y);
-        yacc[j][q] = __builtin_fmaf(mt.s[j], acc[j][q], y);
-        if constexpr (BKM == 8) acc[j][q] = 0.f;
-      }
+      for (int j = 0; j < JN; ++j)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          float y = yacc[i * JN + j][q];
+          if constexpr (ZK == 2) y = __builtin_fmaf(mt.nz[j], rr[i][q], y);
+          yacc[i * JN + j][q] = __builtin_fmaf(mt.s[j], acc[i * JN + j][q], y);
+          if constexpr (BKM == 8) acc[i * JN + j][q] = 0.f;
+        }
   };
   auto mfmas = [&](int stage, const Meta (&mt)[NB]) {
     const f16* Ah = lds + stage * STAGE;
@@ -492,19 +502,26 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
 #pragma unroll
     for (int kk = 0; kk < KS / 16; ++kk) {
       const int ko = kk * 16 + (lane >> 5) * 8;
-      const int ar = wm * 32 + (lane & 31);
-      const f16x8 fh = *reinterpret_cast<const f16x8*>(Ah + ar * LD + ko);
-      f16x8 fl;
-      if constexpr (LO) fl = *reinterpret_cast<const f16x8*>(Al + ar * LD + ko);
+      f16x8 fh[IM], fl[IM];
+#pragma unroll
+      for (int i = 0; i < IM; ++i) {
+        const int ar = wm * WR + 32 * i + (lane & 31);
+        fh[i] = *reinterpret_cast<const f16x8*>(Ah + ar * LD + ko);
+        if constexpr (LO) fl[i] = *reinterpret_cast<const f16x8*>(Al + ar * LD + ko);
+      }
       const Meta& m = mt[BKM == 8 ? 0 : kk / BKM];
       const bool first = BKM != 8 && kk % BKM == 0;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int c = wn * 64 + j * 32 + (lane & 31);
+      for (int j = 0; j < JN; ++j) {
+        const int c = wn * WC + j * 32 + (lane & 31);
         const uint32_t* w = BITS == 2 ? Bw + kk * CT + c : Bw + ((ko >> 3) * CT + c) * (BITS / 4);
         const f16x8 fb = dq(w, m, j);
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh, fb, first ? zero16 : acc[j], 0, 0, 0);
-        if constexpr (LO) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fl, fb, acc[j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < IM; ++i) {
+          f32x16& ac = acc[i * JN + j];
+          ac = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh[i], fb, first ? zero16 : ac, 0, 0, 0);
+          if constexpr (LO) ac = __builtin_amdgcn_mfma_f32_32x32x16_f16(fl[i], fb, ac, 0, 0, 0);
+        }
       }
       if constexpr (BKM != 8) {
         if ((kk + 1) % BKM == 0) flush(m, stage, kk / BKM);
@@ -554,19 +571,21 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
 
   // ---- epilogue: lane holds D[8 (q / 4) + 4 (lane / 32) + q % 4][lane % 32]
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int c = n0 + wn * 64 + j * 32 + (lane & 31);
+  for (int j = 0; j < JN; ++j) {
+    const int c = n0 + wn * WC + j * 32 + (lane & 31);
     if (c >= a.N) continue;
     const float b = (a.splits == 1 && a.bias) ? static_cast<float>(static_cast<const T*>(a.bias)[c]) : 0.f;
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int r = wm * 32 + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
-      const int m = m0 + r;
-      if (m >= a.M) continue;
-      const float v = LO ? yacc[j][q] * s_ru[r] : yacc[j][q];
-      if (a.splits == 1) static_cast<T*>(a.Y)[static_cast<int64_t>(m) * a.N + c] = static_cast<T>(v + b);
-      else a.part[(static_cast<int64_t>(sp) * a.M + m) * a.N + c] = v;
-    }
+    for (int i = 0; i < IM; ++i)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int r = wm * WR + 32 * i + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+        const int m = m0 + r;
+        if (m >= a.M) continue;
+        const float v = LO ? yacc[i * JN + j][q] * s_ru[r] : yacc[i * JN + j][q];
+        if (a.splits == 1) static_cast<T*>(a.Y)[static_cast<int64_t>(m) * a.N + c] = static_cast<T>(v + b);
+        else a.part[(static_cast<int64_t>(sp) * a.M + m) * a.N + c] = v;
+      }
   }
 }
 
