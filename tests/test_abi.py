@@ -178,7 +178,10 @@ def test_fuzz_reaches_every_kernel_family():
     (0, 512, 2560, 4096, 4, 64, nat.F32, nat.F32, "gemm_f32_mfma"),      # upstream qwen3 prefill zero-bias case
     (0, 48, 2561, 1021, 8, 32, nat.F32, nat.UNSPECIFIED, "gemm_f32_mfma"),  # upstream tail case (K % 4 != 0)
     (0, 128, 5120, 17408, 2, 128, nat.F16, nat.F16, "gemm_f32_mfma"),    # upstream bonsai2 case, float16 zero points
-    (0, 1, 2048, 2048, 2, 32, nat.F32, nat.UNSPECIFIED, "generic"),      # 2-bit codes, one row
+    (0, 1, 2048, 2048, 2, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),  # 2-bit codes, one row: the float32 GEMV
+    (0, 2, 5120, 17408, 2, 128, nat.F16, nat.F16, "gemv_q4_f32"),        # 2-bit float16 decode (bonsai2 geometry)
+    (0, 4, 5120, 17408, 2, 128, nat.F16, nat.F16, "gemv_q4_f32"),        # four rows of two chunks per lane: chunks of two rows
+    (0, 16, 8192, 512, 2, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),  # 2-bit, 16 rows of K 8192: chunks of two rows
     (0, 128, 5120, 17408, 2, 128, nat.F16, nat.UNSPECIFIED, "gemm_f32_mfma"),  # upstream bonsai2 2-bit prefill
     (0, 64, 2048, 2048, 2, 32, nat.F32, nat.U8, "gemm_f32_mfma"),        # 2-bit, float32
     (0, 64, 2048, 2048, 4, 32, nat.F16, nat.UNSPECIFIED, "gemv_q4_splitk"),  # 4-bit float16: the binary16 kernels

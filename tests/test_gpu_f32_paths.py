@@ -49,6 +49,13 @@ CASES = [
     (17, 1024, 96, 8, 128, None, True),
     (64, 4096, 256, 4, 32, None, False),      # float32 prefill, 16 chunks of four rows
     (130, 768, 72, 8, 32, "packed", False),
+    (1, 4096, 1000, 2, 32, None, True),         # 2-bit codes: one dword per 16 codes
+    (3, 2048, 300, 2, 64, "packed", False),
+    (4, 1024, 100, 2, 16, "float", True),
+    (16, 4096, 96, 2, 128, "packed", True),
+    (2, 8192, 64, 2, 32, None, False),          # two chunks per lane
+    (7, 8192, 130, 2, 64, "packed", True),      # two chunks per lane, seven rows: chunks of two rows
+    (5, 16384, 40, 2, 32, None, False),         # four chunks per lane: one row per workgroup
 ]
 
 
@@ -190,6 +197,8 @@ F16_CASES = [
     (17, 1024, 96, 8, 128, None, True),
     (130, 768, 72, 8, 32, "packed", False),
     (512, 256, 64, 8, 16, "float16", True),   # prefill rows, 16-code blocks
+    (2, 5120, 1000, 2, 128, "float16", False),  # 2-bit decode, the bonsai2 K and blocks
+    (8, 2048, 200, 2, 32, "packed", True),
 ]
 
 

@@ -62,12 +62,12 @@ __device__ __forceinline__ float ubyte(uint32_t x, int i) {
 // T: float (activations, scales, bias and outputs in float32) or f16.
 template <typename T, int ZPK, int CPL, int C, int MR, int W, int BITS = 4>
 __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
-  static_assert(BITS == 4 || BITS == 8, "4- or 8-bit codes");
+  static_assert(BITS == 2 || BITS == 4 || BITS == 8, "2-, 4- or 8-bit codes");
   constexpr uint32_t TS = sizeof(T);
   constexpr uint32_t CODES = 128 / BITS;         // codes per 16-byte chunk
   constexpr uint32_t H = CODES / 16;             // 16-code halves per chunk
   constexpr uint32_t CS = f32_chunk_stride<BITS>();
-  constexpr float ZMID = BITS == 4 ? 8.f : 128.f;  // implicit zero point 2^(bits - 1)
+  constexpr float ZMID = static_cast<float>(1 << (BITS - 1));  // implicit zero point 2^(bits - 1)
   extern __shared__ __align__(16) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -198,14 +198,24 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
         const float s = static_cast<float>(*reinterpret_cast<const T*>(meta + (i * kb + b) * TS));
         float z = ZMID;
         if constexpr (ZPK == ZP_PACKED) {
-          if constexpr (BITS == 4) z = static_cast<float>((zmeta[i * zrow + (b >> 1)] >> ((b & 1u) * 4u)) & 15u);
+          if constexpr (BITS == 2) z = static_cast<float>((zmeta[i * zrow + (b >> 2)] >> ((b & 3u) * 2u)) & 3u);
+          else if constexpr (BITS == 4) z = static_cast<float>((zmeta[i * zrow + (b >> 1)] >> ((b & 1u) * 4u)) & 15u);
           else z = static_cast<float>(zmeta[i * zrow + b]);
         } else if constexpr (ZPK == ZP_FLOAT) {
           const unsigned char* zp = zmeta + i * zrow + b * a.zesz;
           z = a.zesz == 4 ? *reinterpret_cast<const float*>(zp) : static_cast<float>(*reinterpret_cast<const f16*>(zp));
         }
         float cv[16];
-        if constexpr (BITS == 4) {
+        if constexpr (BITS == 2) {
+          // one dword: code 4 e + s in bits 8 e + 2 s .. + 1
+          const uint32_t x = wv[i][j][h];
+#pragma unroll
+          for (int sh = 0; sh < 4; ++sh) {
+            const uint32_t v = (x >> (2 * sh)) & 0x03030303u;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cv[4 * e + sh] = ubyte(v, e);
+          }
+        } else if constexpr (BITS == 4) {
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
             const uint32_t x = wv[i][j][2 * h + q];
@@ -275,8 +285,15 @@ inline int f32_cpl(const Launch& L) {
   return 0;
 }
 
-// Rows per workgroup: 1, 2 or 4 (more rows: chunks of four on the grid's y).
-inline int f32_mr(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
+// Rows per workgroup: 1, 2 or 4 (more rows: chunks on the grid's y), fewer
+// where a thread would hold more than 16 activation loads (2-bit rows of more
+// than 64 chunks).
+inline int f32_mr(const Launch& L) {
+  int mr = L.M <= 1 ? 1 : L.M <= 2 ? 2 : 4;
+  const int cpl = f32_cpl(L);
+  while (mr > 1 && mr * cpl * 8 / L.bits > 16) mr /= 2;
+  return mr;
+}
 
 // Bytes of one activation, scale, bias or output value: float32 or float16.
 inline int64_t f32_esz(const Launch& L) { return L.dtype == DT_F16 ? 2 : 4; }
@@ -289,18 +306,19 @@ inline uint32_t f32_meta_bytes(const Launch& L, uint32_t& zoff) {
   return (zoff + zb + 3u + 15u) & ~15u;
 }
 
-// fp32, or fp16 with 8-bit codes or float32 weights required (`exact`:
-// dequantised weights binary16 cannot hold); 4- or 8-bit, power-of-two
+// fp32, or fp16 with 2- or 8-bit codes or float32 weights required (`exact`:
+// dequantised weights binary16 cannot hold); 2-, 4- or 8-bit, power-of-two
 // block_size >= 16, K a multiple of 4, 16-byte aligned tensors, rows of at
 // most 256 chunks (whole 16-byte chunks), the wave's scale / zero-point block
 // within 4 KB and the staging within 160 KB of LDS; at most 65535 chunks of
 // four rows (the grid's y).
 inline bool f32_fits(const Launch& L) {
-  const bool t_ok = L.dtype == DT_F32 || (L.dtype == DT_F16 && (L.bits == 8 || L.exact_weights));
-  if (!t_ok || (L.bits != 4 && L.bits != 8) || L.bs_log2 < 4 || L.op != OP_MATMUL || L.K % 4 != 0) return false;
+  const bool t_ok = L.dtype == DT_F32 || (L.dtype == DT_F16 && (L.bits != 4 || L.exact_weights));
+  if (!t_ok || (L.bits != 2 && L.bits != 4 && L.bits != 8) || L.bs_log2 < 4 || L.op != OP_MATMUL || L.K % 4 != 0)
+    return false;
   if ((L.kb * L.block_size) % (128 / L.bits) != 0) return false;
-  if (L.M < 1 || (L.M + 3) / 4 > 65535) return false;
-  const int mr = f32_mr(L.M), cpl = f32_cpl(L);
+  const int mr = f32_mr(L), cpl = f32_cpl(L);
+  if (L.M < 1 || (L.M + mr - 1) / mr > 65535) return false;
   if (cpl == 0) return false;
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   if (!al(L.A) || !al(L.p[0].B) || !al(L.p[0].scales) || !al(L.p[0].zp)) return false;
@@ -316,7 +334,7 @@ inline bool f32_fits(const Launch& L) {
 }
 
 template <typename T, int ZPK, int CPL, int MR, int BITS>
-inline hipError_t launch_f32_3(const Launch& L, hipStream_t st) {
+inline hipError_t launch_f32_k(const Launch& L, hipStream_t st) {
   F32Args a{};
   const Proj& P = L.p[0];
   a.A = L.A;
@@ -348,9 +366,17 @@ inline hipError_t launch_f32_3(const Launch& L, hipStream_t st) {
   return hipGetLastError();
 }
 
+// the activation loads per thread f32_fits admits (2-bit: MR CPL <= 4; the
+// other shapes are not instantiated)
+template <typename T, int ZPK, int CPL, int MR, int BITS>
+inline hipError_t launch_f32_3(const Launch& L, hipStream_t st) {
+  if constexpr (MR * CPL * 8 / BITS > 16) return hipErrorInvalidValue;
+  else return launch_f32_k<T, ZPK, CPL, MR, BITS>(L, st);
+}
+
 template <typename T, int ZPK, int CPL, int BITS>
 inline hipError_t launch_f32_2(const Launch& L, hipStream_t st) {
-  switch (f32_mr(L.M)) {
+  switch (f32_mr(L)) {
     case 1: return launch_f32_3<T, ZPK, CPL, 1, BITS>(L, st);
     case 2: return launch_f32_3<T, ZPK, CPL, 2, BITS>(L, st);
     default: return launch_f32_3<T, ZPK, CPL, 4, BITS>(L, st);
@@ -368,7 +394,9 @@ inline hipError_t launch_f32_b(const Launch& L, hipStream_t st) {
 
 template <typename T, int ZPK>
 inline hipError_t launch_f32_t(const Launch& L, hipStream_t st) {
-  return L.bits == 8 ? launch_f32_b<T, ZPK, 8>(L, st) : launch_f32_b<T, ZPK, 4>(L, st);
+  if (L.bits == 8) return launch_f32_b<T, ZPK, 8>(L, st);
+  if (L.bits == 2) return launch_f32_b<T, ZPK, 2>(L, st);
+  return launch_f32_b<T, ZPK, 4>(L, st);
 }
 
 template <int ZPK>
