@@ -4,6 +4,8 @@ qwen3-qproj-decode-m1-q8g32 case's geometry, …/com.microsoft.MatMulNBits/
 build/webgpu/bench.json:224), and on the float32 matrix-core GEMM (more than
 16 rows, with a workspace), against the oracle at the float32 bar
 max|d| <= 1e-5 max|Y_ref|."""
+import zlib
+
 import numpy as np
 import pytest
 
@@ -292,3 +294,34 @@ def test_mfma_gemm_nonfinite_rows(gpu, dt, bits, bs, zp):
     ok, err, lim = O.tolerance_ok(Y, ref, dt)
     assert ok, (err, lim, np.argwhere(np.isfinite(Y) != np.isfinite(ref))[:5])
     assert not np.isfinite(ref[3]).any() and np.isnan(ref[11]).all() and np.isfinite(ref[0]).all()
+
+
+UPSTREAM_PREFILL = [
+    # name, M, K, N, bits, bs, zp, activations: the upstream prefill cases at their own sizes
+    # (…/com.microsoft.MatMulNBits/build/webgpu/bench.json; inputs drawn here, not the
+    # upstream generators)
+    ("qwen3-qproj-prefill-m512-q4g64-zero-bias", 512, 2560, 4096, 4, 64, "float", np.float32),
+    ("qwen3-qproj-prefill-m512-q8g32", 512, 2560, 4096, 8, 32, None, np.float32),
+    ("qwen3-prefill-m512-q8g32-unaligned-n2052", 512, 2560, 2052, 8, 32, None, np.float32),
+    ("matmul-nbits-q4-naive-fallback-tailK-m32-k2561-n4096", 32, 2561, 4096, 4, 32, None, np.float32),
+    ("rfdetr-fc2-m1300-q4g64", 1300, 1536, 384, 4, 64, None, np.float32),
+    ("bonsai2-ffn-gate-prefill-m128-q2g128-k5120-n17408-zero1-f16", 128, 5120, 17408, 2, 128, "float16", np.float16),
+]
+
+
+@pytest.mark.parametrize("name,M,K,N,bits,bs,zp,dt", UPSTREAM_PREFILL, ids=[c[0] for c in UPSTREAM_PREFILL])
+def test_upstream_prefill_cases_full_size(gpu, name, M, K, N, bits, bs, zp, dt):
+    """The upstream prefill geometries at full size on the float32-arithmetic
+    MFMA GEMM, against the oracle at the bar of the activations' type."""
+    rng = np.random.default_rng(zlib.crc32(name.encode()))
+    A, B, S, Z, b = case(rng, M, K, N, bits, bs, zp, False)
+    A = (A * 0.2).astype(dt)
+    S = S.astype(dt)
+    if zp == "float16":
+        Z = Z.astype(np.float16)
+    kind = None if zp is None else ("packed" if zp == "packed" else "float")
+    assert ops().select_kernel("MatMulNBits", M, K, N, bits, bs, torch.from_numpy(A).dtype, kind) == "gemm_f32_mfma"
+    Y = ops().matmul_nbits(dev(A), dev(B), dev(S), dev(Z), None, K=K, N=N, bits=bits, block_size=bs).cpu().numpy()
+    ref = O.matmul_nbits(A, B, S, Z, None, K=K, N=N, bits=bits, block_size=bs)
+    ok, err, lim = O.tolerance_ok(Y, ref, dt)
+    assert ok, (err, lim)
