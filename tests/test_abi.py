@@ -108,7 +108,7 @@ def test_qkv_requires_norm_scale():
     (1, 64, 2048, 512, 32, nat.F16, nat.U8, "gemv_q4_splitk"),          # Qkv, four row chunks
     (1, 65, 2048, 512, 32, nat.F16, nat.U8, "gemm_q4_fused"),           # Qkv prefill
     (1, 17, 4096, 4096, 16, nat.F16, nat.F16, "gemm_q4_fused"),
-    (1, 32, 96, 16, 32, nat.F32, nat.UNSPECIFIED, "generic"),           # float32 prefill
+    (1, 32, 96, 16, 32, nat.F32, nat.UNSPECIFIED, "f32_proj"),          # float32 Qkv: prologue + float32 MatMulNBits
     (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),       # the CPU-oracle workload, float32
     (0, 4, 4096, 14336, 64, nat.F32, nat.F32, "gemv_q4_f32"),
     (0, 5, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),         # float32 beyond four rows: chunks of four
@@ -118,7 +118,11 @@ def test_qkv_requires_norm_scale():
     (0, 64, 4096, 4096, 16, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),    # blocks of 16
     (0, 64, 4096, 4096, 32, nat.F32, nat.F32, "gemv_q4_f32"),            # float zero points, blocks of 32
     (0, 64, 4096, 4096, 64, nat.F32, nat.F32, "gemm_f32_mfma"),          # float zero points, blocks of 64
-    (1, 8, 256, 64, 32, nat.F32, nat.UNSPECIFIED, "generic"),         # float32 Qkv
+    (1, 8, 256, 64, 32, nat.F32, nat.UNSPECIFIED, "f32_proj"),        # float32 Qkv
+    (2, 1, 2048, 5632, 32, nat.F32, nat.UNSPECIFIED, "f32_proj"),     # upstream mlp-q4-decode-k2048-n5632 (float32)
+    (2, 64, 2048, 5632, 32, nat.F32, nat.UNSPECIFIED, "f32_proj"),    # upstream mlp-q4-prefill-m64-k2048-n5632
+    (1, 8, 4096, 4096, 32, nat.F32, nat.UNSPECIFIED, "f32_proj"),     # upstream qkv-q4-llama-spec8
+    (1, 4, 96, 64, 48, nat.F32, nat.UNSPECIFIED, "generic"),          # non-power-of-two blocks: the generic kernel
     (0, 1, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),
     (0, 4, 16384, 14336, 16, nat.F16, nat.UNSPECIFIED, "generic"),  # dot staging would exceed 160 KB of LDS
     (0, 1, 33, 8, 32, nat.F16, nat.UNSPECIFIED, "generic"),

@@ -120,7 +120,8 @@ QKV_CASES = [
     (8, 2048, 64, 32, 32, np.float16, False, "gemv_q4_splitk"),
     (32, 1024, 40, 24, 32, np.float16, False, "gemm_q4_fused"),
     (20, 512, 130, 3, 16, np.float16, True, "gemm_q4_fused"),
-    (5, 96, 16, 8, 32, np.float32, True, "generic"),
+    (5, 96, 16, 8, 32, np.float32, True, "f32_proj"),
+    (40, 1024, 64, 32, 64, np.float32, True, "f32_proj"),   # more than 16 rows: the MFMA GEMM per projection
 ]
 
 
@@ -158,8 +159,9 @@ MLP_CASES = [
     (24, 2048, 64, 32, np.float16, False, "gemm_q4_thin"),      # 17..64 rows: the thin GEMM
     (70, 1024, 64, 32, np.float16, False, "gemm_q4_fused"),
     (130, 1024, 40, 64, np.float16, True, "gemm_q4_fused"),
-    (4, 96, 24, 32, np.float32, False, "generic"),
-    (4, 96, 24, 32, np.float32, True, "generic"),
+    (4, 96, 24, 32, np.float32, False, "f32_proj"),
+    (4, 96, 24, 32, np.float32, True, "f32_proj"),
+    (48, 1024, 64, 64, np.float32, True, "f32_proj"),
 ]
 
 

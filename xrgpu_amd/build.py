@@ -47,6 +47,7 @@ UNITS = [
     ("xrmm_gemm_fused_zp.hip", ["-DXRMM_ZPK=2"], "fused_zp2.o"),
     ("xrmm_gemm_f32x.hip", [], "gemm_f32x.o"),
     ("xrmm_gemm_f32x_h.hip", [], "gemm_f32x_h.o"),
+    ("xrmm_f32_split.hip", [], "f32_split.o"),
     ("xrmm_moe.hip", [], "moe.o"),
     ("xrmm_quant.hip", [], "quant.o"),
     ("xrmm_int8a.hip", [], "int8a.o"),

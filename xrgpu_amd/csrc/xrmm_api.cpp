@@ -297,14 +297,17 @@ int mlp_launch(xrmm::Launch& L, const void* A, const void* skip, const void* nor
   return XRMM_OK;
 }
 
-// Bytes of the normalised-activation workspace a Qkv / Mlp launch would use
-// (0: its kernel reads none). The selection looks at the workspace pointer,
-// so it is asked with a placeholder one.
+// Bytes of the workspace a Qkv / Mlp launch would use (0: its kernel reads
+// none): the normalised binary16 rows of the float16 prefill GEMMs, or the
+// float32 path's x, gate / up rows and projection workspace. The selection
+// looks at the workspace pointer, so it is asked with a placeholder one.
 int64_t xs_need(xrmm::Launch L) {
-  if (L.M <= 0 || !xrmm::fused_prologue(L)) return 0;
+  if (L.M <= 0) return 0;
   static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
   L.xs = const_cast<uint8_t*>(dummy);
   const xrmm::Kernel k = xrmm::select_kernel(L);
+  if (k == xrmm::K_F32_SPLIT) return xrmm::f32split_xs_bytes(L);
+  if (!xrmm::fused_prologue(L)) return 0;
   return k == xrmm::K_GEMM_FUSED || k == xrmm::K_GEMM_BIG_FUSED || k == xrmm::K_GEMM_THIN ? xrmm::fused_xs_bytes(L) : 0;
 }
 

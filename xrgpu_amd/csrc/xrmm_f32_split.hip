@@ -1,0 +1,151 @@
+// Float32 MatMulNBitsQkv / MatMulNBitsMlp (T1 = float32, the dtype of every
+// upstream Qkv / Mlp bench case) as a prologue and one MatMulNBits per
+// projection on the float32-arithmetic kernels.
+//
+// The reference forms packedInput x = (A + skip) * inversesqrt(mean(r^2) +
+// eps) * gamma (or A + skip) in float32 (complex_kernel.glsl:81), then each
+// projection's float32 dot products (:83; Mlp: act(gate + gate_bias) *
+// (up + up_bias)). Here k_f32_prologue writes x (and the residual A + skip)
+// to the workspace once per row, each projection runs as a float32
+// MatMulNBits on x (the float32 GEMV up to 16 rows, the float32-arithmetic
+// MFMA GEMM beyond, both meeting the float32 bar), Qkv's straight into Q, K
+// and V, Mlp's into float32 gate / up rows that k_mlp_act combines.
+//
+// Workspace (Launch::xs): x [M][K] (when there is a prologue), gate and up
+// [M][N] (Mlp), then the MatMulNBits workspace of the projections (the MFMA
+// GEMM's prepared rows and split partials; the projections run one after
+// another on the stream and share it).
+#include "xrmm_device.h"
+
+namespace xrmm {
+
+namespace {
+
+int64_t al256(int64_t b) { return (b + 255) / 256 * 256; }
+
+// One workgroup per row: r = A + skip (float32), the residual, and x = r or
+// r * inversesqrt(sum(r^2) / K + eps) * gamma.
+__global__ __launch_bounds__(256) void k_f32_prologue(const float* __restrict__ A, const float* __restrict__ skip,
+                                                      const float* __restrict__ gamma, float* __restrict__ x,
+                                                      float* __restrict__ residual, int K, float eps) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const int64_t o = static_cast<int64_t>(m) * K;
+  float ss = 0.f;
+  for (int k = tid; k < K; k += 256) {
+    const float r = skip ? A[o + k] + skip[o + k] : A[o + k];
+    x[o + k] = r;
+    if (residual) residual[o + k] = r;
+    ss = __builtin_fmaf(r, r, ss);
+  }
+  if (!gamma) return;  // uniform
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  if (lane == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  ss = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = 1.f / __builtin_sqrtf(ss / static_cast<float>(K) + eps);
+  // each thread rescales the elements it wrote
+  for (int k = tid; k < K; k += 256) x[o + k] = x[o + k] * inv * gamma[k];
+}
+
+// Mlp: y = act(gate) * up (the biases are in gate and up already).
+__global__ __launch_bounds__(256) void k_mlp_act(const float* __restrict__ g, const float* __restrict__ u,
+                                                 float* __restrict__ y, int64_t n, int act) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) y[i] = activate(g[i], act) * u[i];
+}
+
+// Projection p of a float32 Qkv / Mlp as a MatMulNBits launch on `A` into `Y`.
+Launch projection(const Launch& L, int p, const void* A, void* Y, void* ws) {
+  Launch L2 = L;
+  L2.op = OP_MATMUL;
+  L2.nproj = 1;
+  L2.A = A;
+  L2.skip = nullptr;
+  L2.gamma = nullptr;
+  L2.residual = nullptr;
+  L2.p[0] = L.p[p];
+  L2.p[0].Y = Y;
+  L2.p[1] = Proj{};
+  L2.p[2] = Proj{};
+  if (!L.p[p].zp) L2.zp_kind = ZP_NONE;
+  L2.ws = ws;
+  L2.splits = 1;
+  L2.xs = nullptr;
+  return L2;
+}
+
+bool has_prologue(const Launch& L) { return L.skip || L.gamma || L.residual; }
+
+// x is reserved whether or not the call has a prologue: the workspace size is
+// asked without knowing whether the caller wants the residual
+int64_t x_bytes(const Launch& L) { return al256(L.M * L.K * 4); }
+int64_t gu_bytes(const Launch& L) { return L.op == OP_MLP ? 2 * al256(L.M * L.p[0].N * 4) : 0; }
+
+// The projections' MatMulNBits workspace: the largest MFMA GEMM need (sized
+// for float zero points, the kind that needs most), when more than 16 rows.
+int64_t proj_ws_bytes(const Launch& L) {
+  if (L.M <= 16) return 0;
+  static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
+  int64_t need = 0;
+  for (int p = 0; p < L.nproj; ++p) {
+    Launch L2 = projection(L, p, dummy, nullptr, const_cast<uint8_t*>(dummy));
+    L2.p[0].B = L.p[p].B ? L.p[p].B : dummy;
+    L2.p[0].scales = L.p[p].scales ? L.p[p].scales : dummy;
+    if (select_kernel(L2) != K_GEMM_F32X) continue;
+    L2.zp_kind = ZP_FLOAT;
+    const int64_t b = f32x_workspace_bytes(L2);
+    need = b > need ? b : need;
+  }
+  return need;
+}
+
+}  // namespace
+
+// Float32 Qkv / Mlp whose every projection runs on the float32 GEMV or the
+// float32-arithmetic MFMA GEMM (given the workspace), with K and the
+// projections' shapes inside their limits.
+bool f32split_fits(const Launch& L) {
+  if ((L.op != OP_QKV && L.op != OP_MLP) || L.dtype != DT_F32 || L.M < 1) return false;
+  const int64_t lim = int64_t(1) << 31;
+  if (L.M * L.K >= lim / 4 || L.M * L.p[0].N >= lim / 4) return false;
+  static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
+  for (int p = 0; p < L.nproj; ++p) {
+    // the projections read x from the workspace (256-byte aligned) or A
+    Launch L2 = projection(L, p, has_prologue(L) ? dummy : L.A, nullptr, L.M > 16 ? const_cast<uint8_t*>(dummy) : nullptr);
+    const Kernel k = select_kernel(L2);
+    if (k != K_GEMV_F32 && k != K_GEMM_F32X) return false;
+  }
+  return true;
+}
+
+int64_t f32split_xs_bytes(const Launch& L) { return x_bytes(L) + gu_bytes(L) + proj_ws_bytes(L); }
+
+hipError_t launch_f32_split(const Launch& L, hipStream_t st) {
+  uint8_t* w = static_cast<uint8_t*>(L.xs);
+  const void* x = L.A;
+  if (has_prologue(L)) {
+    float* xf = reinterpret_cast<float*>(w);
+    hipLaunchKernelGGL(k_f32_prologue, dim3(static_cast<uint32_t>(L.M)), dim3(256), 0, st, static_cast<const float*>(L.A),
+                       static_cast<const float*>(L.skip), static_cast<const float*>(L.gamma), xf,
+                       static_cast<float*>(L.residual), static_cast<int>(L.K), L.eps);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    x = xf;
+  }
+  float* g = reinterpret_cast<float*>(w + x_bytes(L));
+  float* u = reinterpret_cast<float*>(w + x_bytes(L) + gu_bytes(L) / 2);
+  void* pws = L.M > 16 ? w + x_bytes(L) + gu_bytes(L) : nullptr;
+  for (int p = 0; p < L.nproj; ++p) {
+    void* Y = L.op == OP_MLP ? static_cast<void*>(p == 0 ? g : u) : L.p[p].Y;
+    if (hipError_t e = launch(projection(L, p, x, Y, pws), st); e != hipSuccess) return e;
+  }
+  if (L.op == OP_MLP) {
+    const int64_t n = L.M * L.p[0].N;
+    hipLaunchKernelGGL(k_mlp_act, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, st, g, u,
+                       static_cast<float*>(L.p[0].Y), n, L.act);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace xrmm

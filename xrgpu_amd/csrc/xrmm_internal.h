@@ -75,7 +75,8 @@ class ExactWeightsScope {
 
 // Kernel families the dispatcher chooses between.
 enum Kernel { K_GENERIC = 0, K_GEMV_Q4 = 1, K_GEMM_Q4 = 2, K_GEMV_DOT = 3, K_GEMM_BIG = 4, K_GEMV_SK = 5, K_GEMV_MQ = 6,
-              K_GEMV_F32 = 7, K_GEMM_FUSED = 8, K_GEMM_BIG_FUSED = 9, K_GEMM_THIN = 10, K_GEMM_F32X = 11 };
+              K_GEMV_F32 = 7, K_GEMM_FUSED = 8, K_GEMM_BIG_FUSED = 9, K_GEMM_THIN = 10, K_GEMM_F32X = 11,
+              K_F32_SPLIT = 12 };
 
 // Whether a Qkv / Mlp launch has a prologue (skip or normScale) whose
 // normalised activations a prefill GEMM can take from L.xs.
@@ -91,6 +92,14 @@ bool f32x_fits(const Launch& L);
 int f32x_splits(const Launch& L);
 int64_t f32x_workspace_bytes(const Launch& L);
 hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st);
+
+// Float32 Qkv / Mlp as a prologue and one float32 MatMulNBits per projection
+// (xrmm_f32_split.hip): whether a geometry fits, the workspace it needs
+// (Launch::xs: x, Mlp's gate / up rows, the projections' workspace), and the
+// launch.
+bool f32split_fits(const Launch& L);
+int64_t f32split_xs_bytes(const Launch& L);
+hipError_t launch_f32_split(const Launch& L, hipStream_t st);
 
 // Choose a kernel family for the geometry (host only, no device calls).
 Kernel select_kernel(const Launch& L);

@@ -662,6 +662,9 @@ inline bool thin_takes(const Launch& L) {
 }
 
 Kernel select_kernel(const Launch& L) {
+  // float32 Qkv / Mlp with the caller's workspace: prologue + float32
+  // MatMulNBits per projection
+  if (L.op != OP_MATMUL && L.dtype == DT_F32 && L.xs != nullptr && f32split_fits(L)) return K_F32_SPLIT;
   if (L.exact_weights) {
     // the dot and four-row MFMA GEMVs and the float32-arithmetic GEMM keep
     // weights out of binary16; every other fast kernel stages binary16 weights
@@ -711,6 +714,7 @@ const char* kernel_name(Kernel k) {
     case K_GEMM_BIG_FUSED: return "gemm_q4_big_fused";
     case K_GEMM_THIN: return "gemm_q4_thin";
     case K_GEMM_F32X: return "gemm_f32_mfma";
+    case K_F32_SPLIT: return "f32_proj";
     default: return "generic";
   }
 }
@@ -779,6 +783,7 @@ static int effective_zpk(const Launch& L) {
 hipError_t launch(const Launch& L, hipStream_t st) {
   if (L.M == 0) return hipSuccess;
   Kernel k = select_kernel(L);
+  if (k == K_F32_SPLIT) return launch_f32_split(L, st);  // per projection (each with its own zero points)
   const int zpk = effective_zpk(L);
   if (zpk < 0) k = K_GENERIC;  // mixed presence of zero points
   if (k == K_GEMM_F32X) return launch_gemm_f32x(L, st);
