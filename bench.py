@@ -32,7 +32,8 @@ SEEDS = {"decode_up_m1": 1, "qkv_gqa_m4": 2, "mlp_swiglu_m16": 3, "prefill_m2048
          "bnb4_nf4_m1": 7, "gbq_embed_t2048": 8, "int8a_decode_m1": 1, "f32_k2048_m1": 0,
          "mlp_prefill_m64": 9, "prefill_m2048_prepacked": 4, "down_proj_m64": 10, "mlp_prefill_m2048": 13,
          "qkv_prefill_m2048": 14, "q8_f32_decode_m1": 15, "f32_prefill_m64": 16, "qmoe_prefill_t256": 17,
-         "q8_f16_decode_m1": 18, "f32_prefill_m512": 19, "q2_f16_prefill_m128": 20}
+         "q8_f16_decode_m1": 18, "f32_prefill_m512": 19, "q2_f16_prefill_m128": 20, "f32_qkv_decode_m1": 21,
+         "f32_mlp_prefill_m64": 22}
 # The CPU-oracle workload on the GPU: MatMulNBits float32, M=1, K=N=2048,
 # block_size 32, packed zero points (2,703,360 algorithmic bytes per call)
 F32 = dict(M=1, K=2048, N=2048, bs=32)
@@ -53,6 +54,12 @@ F32P512 = dict(M=512, K=2560, N=4096, bs=64, bits=4)
 Q2F16 = dict(M=128, K=5120, N=17408, bs=128, bits=2)
 # the MatMulNBits legs with float32 arithmetic (float32 activations, or
 # float16 with 2- or 8-bit codes)
+# float32 MatMulNBitsQkv decode and MatMulNBitsMlp prefill: the upstream
+# qkv-q4-llama-decode-k4096-nq4096-nkv4096 and mlp-q4-prefill-m64-k2048-n5632
+# cases (float32 activations, scales and outputs, block_size 32, normScale;
+# Mlp SiLU)
+F32QKV = dict(M=1, K=4096, Nq=4096, Nkv=4096, bs=32)
+F32MLP = dict(M=64, K=2048, N=5632, bs=32)
 WIDE_LEGS = {"q8_f32_decode_m1": Q8F32, "q8_f16_decode_m1": Q8F32, "f32_prefill_m64": F32P, "f32_prefill_m512": F32P512,
              "q2_f16_prefill_m128": Q2F16}
 # MatMulNBitsMlp prefill of the Llama-3-8B FFN: 2048 rows, K=4096, N=14336,
@@ -209,6 +216,20 @@ def make_replicas(torch, name, R, dev, seed):
             reps.append(dict(B=torch.randint(0, 256, (N, kb, bs * bits // 8), dtype=torch.uint8, device=dev, generator=g),
                              S=(torch.rand((N, kb), device=dev, generator=g) * 0.01 + 0.04).to(dt)))
         return dict(A=A, reps=reps, K=K, N=N, bs=bs, bits=bits)
+    if name in ("f32_qkv_decode_m1", "f32_mlp_prefill_m64"):
+        q = F32QKV if name == "f32_qkv_decode_m1" else F32MLP
+        K, bs = q["K"], q["bs"]
+        kb = K // bs
+        A = torch.randn((q["M"], K), device=dev, generator=g) * 0.2
+        gamma = torch.rand((K,), device=dev, generator=g) + 0.5
+        shapes = (("q", q["Nq"]), ("k", q["Nkv"]), ("v", q["Nkv"])) if "qkv" in name else (("g", q["N"]), ("u", q["N"]))
+        for _ in range(R):
+            r = {}
+            for p, n in shapes:
+                r[p + "B"] = _gen_weights(torch, g, n, kb, bs // 2, dev)
+                r[p + "S"] = _scales(torch, g, (n, kb), dev).float()
+            reps.append(r)
+        return dict(A=A, reps=reps, K=K, bs=bs, gamma=gamma, q=q)
     if name == "mlp_prefill_m2048":
         q = MLP2K
         K, N, bs = q["K"], q["N"], q["bs"]
@@ -310,6 +331,27 @@ def step_fn(ops, name, w):
         def f(i):
             r = reps[i % len(reps)]
             return ops.matmul_nbits(A, r["B"], r["S"], block_size=w["bs"], bits=w["bits"], out=Y, workspace=ws)
+        return f
+    if name in ("f32_qkv_decode_m1", "f32_mlp_prefill_m64"):
+        q = w["q"]
+        # the workspace (x, gate / up rows, the projections' GEMM workspace),
+        # allocated once outside the timed graph
+        if "qkv" in name:
+            ws = torch.empty(max(1, ops.fused_workspace_bytes("qkv", q["M"], q["K"], q["Nq"], q["Nkv"], 4, w["bs"],
+                                                              torch.float32)), dtype=torch.uint8, device=A.device)
+
+            def f(i):
+                r = reps[i % len(reps)]
+                return ops.matmul_nbits_qkv(A, r["qB"], r["qS"], r["kB"], r["kS"], r["vB"], r["vS"], norm_scale=w["gamma"],
+                                            block_size=w["bs"], want_residual=False, workspace=ws)
+        else:
+            ws = torch.empty(max(1, ops.fused_workspace_bytes("mlp", q["M"], q["K"], q["N"], 0, 4, w["bs"], torch.float32)),
+                             dtype=torch.uint8, device=A.device)
+
+            def f(i):
+                r = reps[i % len(reps)]
+                return ops.matmul_nbits_mlp(A, r["gB"], r["gS"], r["uB"], r["uS"], norm_scale=w["gamma"],
+                                            block_size=w["bs"], workspace=ws)
         return f
     if name == "mlp_prefill_m2048":
         # one workspace for the normalised rows, allocated once (the front end
@@ -670,6 +712,7 @@ def main():
     names = ["decode_up_m1", "prefill_m2048", "prefill_m2048_prepacked", "qkv_gqa_m4", "mlp_swiglu_m16",
              "mlp_prefill_m64", "down_proj_m64", "mlp_prefill_m2048", "qkv_prefill_m2048", "f32_k2048_m1",
              "q8_f32_decode_m1", "q8_f16_decode_m1", "f32_prefill_m64", "f32_prefill_m512", "q2_f16_prefill_m128",
+             "f32_qkv_decode_m1", "f32_mlp_prefill_m64",
              "qmoe_mixtral_t1", "qmoe_prefill_t256", "bnb4_nf4_m1", "gbq_embed_t2048", "int8a_decode_m1"]
     if args.only:
         names = [n for n in names if n in args.only.split(",")]
@@ -680,7 +723,8 @@ def main():
         R = {"prefill_m2048": 8, "prefill_m2048_prepacked": 8, "mlp_prefill_m2048": 8, "qkv_prefill_m2048": 24,
              "qmoe_mixtral_t1": 2, "qmoe_prefill_t256": 1, "gbq_embed_t2048": 8, "qkv_gqa_m4": 24,
              "f32_k2048_m1": 100, "mlp_prefill_m64": 24, "down_proj_m64": 12, "q8_f32_decode_m1": 24, "q8_f16_decode_m1": 24,
-             "f32_prefill_m64": 24, "f32_prefill_m512": 24, "q2_f16_prefill_m128": 12}.get(name, args.replicas)
+             "f32_prefill_m64": 24, "f32_prefill_m512": 24, "q2_f16_prefill_m128": 12, "f32_qkv_decode_m1": 12,
+             "f32_mlp_prefill_m64": 24}.get(name, args.replicas)
         w = make_replicas(torch, name, R, dev, seed=SEEDS[name])
         fn = step_fn(ops, name, w)
         steps = args.steps if "prefill_m2048" not in name and name != "qmoe_prefill_t256" else max(10, args.steps // 10)
@@ -838,6 +882,24 @@ def main():
                      "bytes_per_launch": nbytes, "replicas": r["replicas"],
                      "kernel": ops.select_kernel("MatMulNBits", q["M"], q["K"], q["N"], q["bits"], q["bs"],
                                                  torch.float16 if esz == 2 else torch.float32)}
+    for name, q in (("f32_qkv_decode_m1", F32QKV), ("f32_mlp_prefill_m64", F32MLP)):
+        if name not in results:
+            continue
+        r = results[name]
+        kb = q["K"] // q["bs"]
+        ncols = q["Nq"] + 2 * q["Nkv"] if "qkv" in name else 2 * q["N"]
+        nout = ncols if "qkv" in name else q["N"]
+        nbytes = ncols * (q["K"] // 2 + kb * 4) + q["M"] * (q["K"] + nout) * 4 + q["K"] * 4
+        fl = 2 * q["M"] * q["K"] * ncols
+        gbs = nbytes / (r["ms"] * 1e-3) / 1e9
+        what = ("MatMulNBitsQkv float32 M=1 K=4096 Nq=Nkv=4096 bs=32 normScale (upstream qkv-q4-llama-decode-k4096)"
+                if "qkv" in name else
+                "MatMulNBitsMlp float32 M=64 K=2048 N=5632 bs=32 normScale SiLU (upstream mlp-q4-prefill-m64-k2048-n5632)")
+        out[name] = {"workload": what, "us": round(r["ms"] * 1e3, 3), "gbs": round(gbs, 2),
+                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "tflops": round(fl / (r["ms"] * 1e-3) / 1e12, 2),
+                     "bytes_per_launch": nbytes, "replicas": r["replicas"],
+                     "kernel": ops.select_kernel("MatMulNBitsQkv" if "qkv" in name else "MatMulNBitsMlp", q["M"], q["K"],
+                                                 q["Nq"] if "qkv" in name else q["N"], 4, q["bs"], torch.float32)}
     if "f32_k2048_m1" in results:
         r, q = results["f32_k2048_m1"], F32
         nbytes = 2_703_360
