@@ -7,15 +7,17 @@
 // projection's float32 dot products (:83; Mlp: act(gate + gate_bias) *
 // (up + up_bias)). Here k_f32_prologue writes x (and the residual A + skip)
 // to the workspace once per row, each projection runs as a float32
-// MatMulNBits on x (the float32 GEMV up to 16 rows, the float32-arithmetic
-// MFMA GEMM beyond, both meeting the float32 bar), Qkv's straight into Q, K
-// and V, Mlp's into float32 gate / up rows that k_mlp_act combines.
+// MatMulNBits on x (the float32 GEMV up to 16 rows, all projections on one
+// grid; the float32-arithmetic MFMA GEMM beyond, one launch per projection;
+// both meet the float32 bar), Qkv's straight into Q, K and V, Mlp's into
+// float32 gate / up rows that k_mlp_act combines.
 //
 // Workspace (Launch::xs): x [M][K] (when there is a prologue), gate and up
 // [M][N] (Mlp), then the MatMulNBits workspace of the projections (the MFMA
 // GEMM's prepared rows and split partials; the projections run one after
 // another on the stream and share it).
-#include "xrmm_device.h"
+#include "xrmm_gemv.h"
+#include "xrmm_gemv_f32.h"
 
 namespace xrmm {
 
@@ -136,9 +138,29 @@ hipError_t launch_f32_split(const Launch& L, hipStream_t st) {
   float* g = reinterpret_cast<float*>(w + x_bytes(L));
   float* u = reinterpret_cast<float*>(w + x_bytes(L) + gu_bytes(L) / 2);
   void* pws = L.M > 16 ? w + x_bytes(L) + gu_bytes(L) : nullptr;
+  auto out_of = [&](int p) { return L.op == OP_MLP ? static_cast<void*>(p == 0 ? g : u) : L.p[p].Y; };
+  // every projection on one float32 GEMV grid when they all fit it
+  Launch Lg = projection(L, 0, x, out_of(0), nullptr);
+  Lg.nproj = L.nproj;
+  int with_zp = 0;
   for (int p = 0; p < L.nproj; ++p) {
-    void* Y = L.op == OP_MLP ? static_cast<void*>(p == 0 ? g : u) : L.p[p].Y;
-    if (hipError_t e = launch(projection(L, p, x, Y, pws), st); e != hipSuccess) return e;
+    Lg.p[p] = L.p[p];
+    Lg.p[p].Y = out_of(p);
+    with_zp += L.p[p].zp != nullptr;
+  }
+  // one zero-point kind on the grid: all projections carry zero points or none
+  Lg.zp_kind = with_zp ? L.zp_kind : ZP_NONE;
+  bool one = L.M <= 16 && (with_zp == 0 || with_zp == L.nproj) && f32_fits(Lg) && fits_i32(Lg);
+  for (int p = 0; p < L.nproj && one; ++p) one = select_kernel(projection(L, p, x, nullptr, nullptr)) == K_GEMV_F32;
+  if (one) {
+    hipError_t e;
+    if (Lg.zp_kind == ZP_NONE) e = launch_f32_for<ZP_NONE>(Lg, st);
+    else if (Lg.zp_kind == ZP_PACKED) e = launch_f32_for<ZP_PACKED>(Lg, st);
+    else e = launch_f32_for<ZP_FLOAT>(Lg, st);
+    if (e != hipSuccess) return e;
+  } else {
+    for (int p = 0; p < L.nproj; ++p)
+      if (hipError_t e = launch(projection(L, p, x, out_of(p), pws), st); e != hipSuccess) return e;
   }
   if (L.op == OP_MLP) {
     const int64_t n = L.M * L.p[0].N;

@@ -38,6 +38,14 @@ struct F32Args {
   uint32_t N, K, kb, rowb, zrow, M, bsl, zesz;
   uint32_t meta_bytes;  // per-wave LDS slice: C*kb*4 scales (+ zero points), 16-aligned
   uint32_t zoff;        // zero points' offset inside the slice
+  // further projections on the same grid (Qkv's K and V, Mlp's up; the same
+  // A, K, block size and zero-point kind): projection p owns the grid's
+  // columns [c1 or c2, ...), each projection's count rounded up to whole waves
+  uint32_t np, c1, c2;
+  const uint8_t *B1, *B2;
+  const void *S1, *S2, *Z1, *Z2, *bias1, *bias2;
+  void *Y1, *Y2;
+  uint32_t N1, N2;
 };
 
 // LDS of the staged activations: [MR][nchunk] chunks of 128 / BITS floats
@@ -71,14 +79,23 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t N = a.N, K = a.K, kb = a.kb, rowb = a.rowb, zrow = a.zrow;
+  // this wave's projection and its first column (wave-uniform)
+  const uint32_t gcol = (xcd_slot(blockIdx.x, gridDim.x) * W + wave) * C;
+  const uint32_t pj = a.np > 1 && gcol >= a.c1 ? (a.np > 2 && gcol >= a.c2 ? 2u : 1u) : 0u;
+  const uint8_t* PB = pj == 0 ? a.B : pj == 1 ? a.B1 : a.B2;
+  const void* PS = pj == 0 ? a.S : pj == 1 ? a.S1 : a.S2;
+  const void* PZ = pj == 0 ? a.Z : pj == 1 ? a.Z1 : a.Z2;
+  const void* Pbias = pj == 0 ? a.bias : pj == 1 ? a.bias1 : a.bias2;
+  void* PY = pj == 0 ? a.Y : pj == 1 ? a.Y1 : a.Y2;
+  const uint32_t N = pj == 0 ? a.N : pj == 1 ? a.N1 : a.N2;
+  const uint32_t K = a.K, kb = a.kb, rowb = a.rowb, zrow = a.zrow;
   const uint32_t nchunk = rowb >> 4;
   // this workgroup's chunk of up to MR rows (the grid's second dimension)
   const uint32_t m0 = blockIdx.y * MR;
   const int M = static_cast<int>(a.M - m0 < MR ? a.M - m0 : MR);
   const T* A = static_cast<const T*>(a.A) + static_cast<size_t>(m0) * K;
-  T* Yo = static_cast<T*>(a.Y) + static_cast<size_t>(m0) * N;
-  const uint32_t col0 = (xcd_slot(blockIdx.x, gridDim.x) * W + wave) * C;
+  T* Yo = static_cast<T*>(PY) + static_cast<size_t>(m0) * N;
+  const uint32_t col0 = gcol - (pj == 0 ? 0u : pj == 1 ? a.c1 : a.c2);
   auto clampc = [&](uint32_t c) { return c < N ? c : N - 1; };
   const uint32_t act_floats = MR * nchunk * CS;
   float* xs = reinterpret_cast<float*>(smem);        // [MR][nchunk][CS]
@@ -97,14 +114,14 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
     // a dword straddling the range's end reads as zero, so the range ends on
     // the dword boundary past the last float16 scale (the scales are 16-byte
     // aligned, so that dword lies in the page of the last scale)
-    const rsrc_t rS = mk_rsrc(a.S, (N * kb * TS + 3u) & ~3u);
+    const rsrc_t rS = mk_rsrc(PS, (N * kb * TS + 3u) & ~3u);
 #pragma unroll
     for (int q = 0; q < MP; ++q) {
       const uint32_t o = lane * 16u + 1024u * q;
       sv[q] = bld16_nt(rS, o < sbytes ? c0 * kb * TS + o : kOOB, 0);
     }
     if constexpr (ZPK != ZP_NONE) {
-      const rsrc_t rZ = mk_rsrc(a.Z, (N * zrow + 15u) & ~15u);
+      const rsrc_t rZ = mk_rsrc(PZ, (N * zrow + 15u) & ~15u);
 #pragma unroll
       for (int q = 0; q < MP; ++q) {
         const uint32_t o = lane * 16u + 1024u * q;
@@ -140,7 +157,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- weights: every chunk of the wave's C columns
-  const rsrc_t rB = mk_rsrc(a.B, N * rowb);
+  const rsrc_t rB = mk_rsrc(PB, N * rowb);
   u32x4 wv[C][CPL];
 #pragma unroll
   for (int i = 0; i < C; ++i)
@@ -268,7 +285,7 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
   }
   const uint32_t mycol = col0 + static_cast<uint32_t>(lane);
   if (lane < C && mycol < N) {
-    const float b = a.bias ? static_cast<float>(static_cast<const T*>(a.bias)[mycol]) : 0.f;
+    const float b = Pbias ? static_cast<float>(static_cast<const T*>(Pbias)[mycol]) : 0.f;
 #pragma unroll
     for (int m = 0; m < MR; ++m)
       if (m < M) Yo[static_cast<uint32_t>(m) * N + mycol] = static_cast<T>(out[m] + b);
@@ -321,8 +338,11 @@ inline bool f32_fits(const Launch& L) {
   if (L.M < 1 || (L.M + mr - 1) / mr > 65535) return false;
   if (cpl == 0) return false;
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-  if (!al(L.A) || !al(L.p[0].B) || !al(L.p[0].scales) || !al(L.p[0].zp)) return false;
-  if (L.zp_kind == ZP_FLOAT && L.p[0].zp == nullptr) return false;
+  if (!al(L.A) || L.nproj < 1 || L.nproj > 3) return false;
+  for (int i = 0; i < L.nproj; ++i) {  // further projections: Qkv / Mlp on one grid
+    if (!al(L.p[i].B) || !al(L.p[i].scales) || !al(L.p[i].zp)) return false;
+    if (L.zp_kind != ZP_NONE && L.p[i].zp == nullptr) return false;
+  }
   uint32_t zoff = 0;
   const uint32_t meta = f32_meta_bytes(L, zoff);
   if (kF32C * L.kb * f32_esz(L) > 4096 || meta - zoff > 4096 + 16) return false;
@@ -352,6 +372,22 @@ inline hipError_t launch_f32_k(const Launch& L, hipStream_t st) {
   a.M = static_cast<uint32_t>(L.M);
   a.bsl = static_cast<uint32_t>(L.bs_log2);
   a.meta_bytes = f32_meta_bytes(L, a.zoff);
+  // the projections' columns on the grid, each rounded up to whole waves
+  auto wcols = [](int64_t n) { return static_cast<uint32_t>((n + kF32C - 1) / kF32C * kF32C); };
+  uint32_t cols = wcols(P.N);
+  a.np = static_cast<uint32_t>(L.nproj);
+  if (L.nproj > 1) {
+    a.c1 = cols;
+    a.B1 = L.p[1].B, a.S1 = L.p[1].scales, a.Z1 = L.p[1].zp, a.bias1 = L.p[1].bias, a.Y1 = L.p[1].Y;
+    a.N1 = static_cast<uint32_t>(L.p[1].N);
+    cols += wcols(L.p[1].N);
+  }
+  if (L.nproj > 2) {
+    a.c2 = cols;
+    a.B2 = L.p[2].B, a.S2 = L.p[2].scales, a.Z2 = L.p[2].zp, a.bias2 = L.p[2].bias, a.Y2 = L.p[2].Y;
+    a.N2 = static_cast<uint32_t>(L.p[2].N);
+    cols += wcols(L.p[2].N);
+  }
   const uint32_t nchunk = a.rowb / 16u;
   const size_t lds = f32_act_bytes<MR, BITS>(nchunk) + size_t(kF32W) * a.meta_bytes;
   auto kern = k_gemv_f32<T, ZPK, CPL, kF32C, MR, kF32W, BITS>;
@@ -360,7 +396,7 @@ inline hipError_t launch_f32_k(const Launch& L, hipStream_t st) {
     const hipError_t attr = raise_lds_cap(reinterpret_cast<const void*>(kern), 160 * 1024, done);
     if (attr != hipSuccess) return attr;
   }
-  const uint32_t waves = static_cast<uint32_t>((P.N + kF32C - 1) / kF32C);
+  const uint32_t waves = cols / kF32C;
   const uint32_t chunks = static_cast<uint32_t>((L.M + MR - 1) / MR);
   hipLaunchKernelGGL(kern, dim3((waves + kF32W - 1) / kF32W, chunks), dim3(kF32W * 64), lds, st, a);
   return hipGetLastError();
