@@ -7,8 +7,9 @@
 // projection's float32 dot products (:83; Mlp: act(gate + gate_bias) *
 // (up + up_bias)). Here k_f32_prologue writes x (and the residual A + skip)
 // to the workspace once per row, each projection runs as a float32
-// MatMulNBits on x (the float32 GEMV up to 16 rows, all projections on one
-// grid; the float32-arithmetic MFMA GEMM beyond, one launch per projection;
+// MatMulNBits on x (up to 16 rows: the float32 GEMV with all projections on
+// one grid and the prologue done on its staged rows; beyond: k_f32_prologue
+// into the workspace, then the float32-arithmetic MFMA GEMM per projection;
 // both meet the float32 bar), Qkv's straight into Q, K and V, Mlp's into
 // float32 gate / up rows that k_mlp_act combines.
 //
@@ -126,22 +127,22 @@ int64_t f32split_xs_bytes(const Launch& L) { return x_bytes(L) + gu_bytes(L) + p
 
 hipError_t launch_f32_split(const Launch& L, hipStream_t st) {
   uint8_t* w = static_cast<uint8_t*>(L.xs);
-  const void* x = L.A;
-  if (has_prologue(L)) {
-    float* xf = reinterpret_cast<float*>(w);
-    hipLaunchKernelGGL(k_f32_prologue, dim3(static_cast<uint32_t>(L.M)), dim3(256), 0, st, static_cast<const float*>(L.A),
-                       static_cast<const float*>(L.skip), static_cast<const float*>(L.gamma), xf,
-                       static_cast<float*>(L.residual), static_cast<int>(L.K), L.eps);
-    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    x = xf;
-  }
   float* g = reinterpret_cast<float*>(w + x_bytes(L));
   float* u = reinterpret_cast<float*>(w + x_bytes(L) + gu_bytes(L) / 2);
-  void* pws = L.M > 16 ? w + x_bytes(L) + gu_bytes(L) : nullptr;
   auto out_of = [&](int p) { return L.op == OP_MLP ? static_cast<void*>(p == 0 ? g : u) : L.p[p].Y; };
-  // every projection on one float32 GEMV grid when they all fit it
-  Launch Lg = projection(L, 0, x, out_of(0), nullptr);
+  // up to 16 rows: every projection on one float32 GEMV grid, when they all
+  // fit it; up to 4 rows (one row chunk of the grid) the prologue runs on
+  // the GEMV's staged rows, beyond that once per row in k_f32_prologue (each
+  // row chunk's workgroups would otherwise all redo it)
+  const bool fuse = L.M <= 4;
+  Launch Lg = projection(L, 0, fuse || !has_prologue(L) ? L.A : w, out_of(0), nullptr);
   Lg.nproj = L.nproj;
+  if (fuse) {
+    Lg.skip = L.skip;
+    Lg.gamma = L.gamma;
+    Lg.residual = L.residual;
+    Lg.eps = L.eps;
+  }
   int with_zp = 0;
   for (int p = 0; p < L.nproj; ++p) {
     Lg.p[p] = L.p[p];
@@ -151,14 +152,32 @@ hipError_t launch_f32_split(const Launch& L, hipStream_t st) {
   // one zero-point kind on the grid: all projections carry zero points or none
   Lg.zp_kind = with_zp ? L.zp_kind : ZP_NONE;
   bool one = L.M <= 16 && (with_zp == 0 || with_zp == L.nproj) && f32_fits(Lg) && fits_i32(Lg);
-  for (int p = 0; p < L.nproj && one; ++p) one = select_kernel(projection(L, p, x, nullptr, nullptr)) == K_GEMV_F32;
+  for (int p = 0; p < L.nproj && one; ++p) one = select_kernel(projection(L, p, Lg.A, nullptr, nullptr)) == K_GEMV_F32;
   if (one) {
+    if (!fuse && has_prologue(L)) {
+      hipLaunchKernelGGL(k_f32_prologue, dim3(static_cast<uint32_t>(L.M)), dim3(256), 0, st,
+                         static_cast<const float*>(L.A), static_cast<const float*>(L.skip),
+                         static_cast<const float*>(L.gamma), static_cast<float*>(static_cast<void*>(w)),
+                         static_cast<float*>(L.residual), static_cast<int>(L.K), L.eps);
+      if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    }
     hipError_t e;
     if (Lg.zp_kind == ZP_NONE) e = launch_f32_for<ZP_NONE>(Lg, st);
     else if (Lg.zp_kind == ZP_PACKED) e = launch_f32_for<ZP_PACKED>(Lg, st);
     else e = launch_f32_for<ZP_FLOAT>(Lg, st);
     if (e != hipSuccess) return e;
   } else {
+    const void* x = L.A;
+    if (has_prologue(L)) {
+      float* xf = reinterpret_cast<float*>(w);
+      hipLaunchKernelGGL(k_f32_prologue, dim3(static_cast<uint32_t>(L.M)), dim3(256), 0, st,
+                         static_cast<const float*>(L.A), static_cast<const float*>(L.skip),
+                         static_cast<const float*>(L.gamma), xf, static_cast<float*>(L.residual), static_cast<int>(L.K),
+                         L.eps);
+      if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+      x = xf;
+    }
+    void* pws = L.M > 16 ? w + x_bytes(L) + gu_bytes(L) : nullptr;
     for (int p = 0; p < L.nproj; ++p)
       if (hipError_t e = launch(projection(L, p, x, out_of(p), pws), st); e != hipSuccess) return e;
   }

@@ -46,6 +46,12 @@ struct F32Args {
   const void *S1, *S2, *Z1, *Z2, *bias1, *bias2;
   void *Y1, *Y2;
   uint32_t N1, N2;
+  // Qkv / Mlp prologue on the staged rows (null: none): r = A + skip, the
+  // residual r, x = r * inversesqrt(sum(r^2) / K + eps) * gamma
+  const void* skip;
+  const void* gamma;
+  void* residual;
+  float eps;
 };
 
 // LDS of the staged activations: [MR][nchunk] chunks of 128 / BITS floats
@@ -181,6 +187,72 @@ __global__ __launch_bounds__(W * 64) void k_gemv_f32(F32Args a) {
     if (p < MR * ppr) *reinterpret_cast<u32x4*>(xs + (p / (CODES / 4)) * CS + (p % (CODES / 4)) * 4u) = av[it];
   }
   __syncthreads();
+  if (a.skip || a.gamma || a.residual) {  // uniform: the Qkv / Mlp prologue (float32 calls)
+    // each thread reworks the pieces it staged: r = x + skip (the residual,
+    // written by the workgroups of the grid's first column), its rows' sums
+    // of r^2, then x = r * inv * gamma
+    auto ld4 = [](const T* q) {
+      if constexpr (TS == 4) {
+        return *reinterpret_cast<const f32x4*>(q);
+      } else {
+        const u32x2 h = *reinterpret_cast<const u32x2*>(q);
+        const f16x2 h0 = as_h2(h[0]), h1 = as_h2(h[1]);
+        return f32x4{static_cast<float>(h0[0]), static_cast<float>(h0[1]), static_cast<float>(h1[0]), static_cast<float>(h1[1])};
+      }
+    };
+    float ss[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) ss[m] = 0.f;
+#pragma unroll
+    for (int it = 0; it < PPT; ++it) {
+      const uint32_t p = static_cast<uint32_t>(tid) + it * W * 64u;
+      const uint32_t m = p / ppr, k = (p % ppr) * 4u;
+      if (p >= MR * ppr || static_cast<int>(m) >= M || k >= K) continue;
+      f32x4* px = reinterpret_cast<f32x4*>(xs + (p / (CODES / 4)) * CS + (p % (CODES / 4)) * 4u);
+      f32x4 v = *px;
+      const size_t o = static_cast<size_t>(m0 + m) * K + k;
+      if (a.skip) v += ld4(static_cast<const T*>(a.skip) + o);
+      if (a.residual && blockIdx.x == 0) {
+        T* r = static_cast<T*>(a.residual) + o;
+        r[0] = static_cast<T>(v.x), r[1] = static_cast<T>(v.y), r[2] = static_cast<T>(v.z), r[3] = static_cast<T>(v.w);
+      }
+      *px = v;
+      const float q = __builtin_fmaf(v.x, v.x, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.z, v.z, v.w * v.w)));
+#pragma unroll
+      for (int mm = 0; mm < MR; ++mm) ss[mm] += static_cast<int>(m) == mm ? q : 0.f;
+    }
+    if (a.gamma) {
+      __shared__ float s_ss[W][MR];
+#pragma unroll
+      for (int mm = 0; mm < MR; ++mm) {
+        const float t = wave_sum(ss[mm]);
+        if (lane == 0) s_ss[wave][mm] = t;
+      }
+      __syncthreads();
+      float inv[MR];
+#pragma unroll
+      for (int mm = 0; mm < MR; ++mm) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) t += s_ss[w][mm];
+        inv[mm] = 1.f / __builtin_sqrtf(t / static_cast<float>(K) + a.eps);
+      }
+#pragma unroll
+      for (int it = 0; it < PPT; ++it) {
+        const uint32_t p = static_cast<uint32_t>(tid) + it * W * 64u;
+        const uint32_t m = p / ppr, k = (p % ppr) * 4u;
+        if (p >= MR * ppr || static_cast<int>(m) >= M || k >= K) continue;
+        f32x4* px = reinterpret_cast<f32x4*>(xs + (p / (CODES / 4)) * CS + (p % (CODES / 4)) * 4u);
+        float im = inv[0];
+#pragma unroll
+        for (int mm = 1; mm < MR; ++mm) im = static_cast<int>(m) == mm ? inv[mm] : im;
+        const f32x4 gv = ld4(static_cast<const T*>(a.gamma) + k);
+        const f32x4 v = *px;
+        *px = f32x4{v.x * im * gv.x, v.y * im * gv.y, v.z * im * gv.z, v.w * im * gv.w};
+      }
+    }
+    __syncthreads();
+  }
   // sums per 16 codes: thread t sums half h = t, t + 64 W, ...
   for (uint32_t h = static_cast<uint32_t>(tid); h < MR * nchunk * H; h += W * 64u) {
     const float* x = xs + (h / H) * CS + (h % H) * 16u;
@@ -343,6 +415,7 @@ inline bool f32_fits(const Launch& L) {
     if (!al(L.p[i].B) || !al(L.p[i].scales) || !al(L.p[i].zp)) return false;
     if (L.zp_kind != ZP_NONE && L.p[i].zp == nullptr) return false;
   }
+  if (!al(L.skip) || !al(L.gamma) || !al(L.residual)) return false;  // the staged prologue's 16-byte pieces
   uint32_t zoff = 0;
   const uint32_t meta = f32_meta_bytes(L, zoff);
   if (kF32C * L.kb * f32_esz(L) > 4096 || meta - zoff > 4096 + 16) return false;
@@ -350,7 +423,7 @@ inline bool f32_fits(const Launch& L) {
   if (mr * f32_cpl(L) * 8 / L.bits > 16) return false;  // activation loads per thread (registers)
   const int64_t codes = 128 / L.bits;
   const int64_t lds = int64_t(mr) * nchunk * (codes + 4) * 4 + int64_t(mr) * nchunk * (codes / 16) * 4 + int64_t(kF32W) * meta;
-  return lds <= 160 * 1024;
+  return lds <= 159 * 1024;
 }
 
 template <typename T, int ZPK, int CPL, int MR, int BITS>
@@ -372,6 +445,10 @@ inline hipError_t launch_f32_k(const Launch& L, hipStream_t st) {
   a.M = static_cast<uint32_t>(L.M);
   a.bsl = static_cast<uint32_t>(L.bs_log2);
   a.meta_bytes = f32_meta_bytes(L, a.zoff);
+  a.skip = L.skip;
+  a.gamma = L.gamma;
+  a.residual = L.residual;
+  a.eps = L.eps;
   // the projections' columns on the grid, each rounded up to whole waves
   auto wcols = [](int64_t n) { return static_cast<uint32_t>((n + kF32C - 1) / kF32C * kF32C); };
   uint32_t cols = wcols(P.N);
@@ -393,7 +470,8 @@ inline hipError_t launch_f32_k(const Launch& L, hipStream_t st) {
   auto kern = k_gemv_f32<T, ZPK, CPL, kF32C, MR, kF32W, BITS>;
   if (lds > 64 * 1024) {
     static std::atomic<int> done[kMaxDevices];  // per instantiation and device
-    const hipError_t attr = raise_lds_cap(reinterpret_cast<const void*>(kern), 160 * 1024, done);
+    // 1 KB of the 160 KB stays for the kernel's static LDS (the prologue's sums)
+    const hipError_t attr = raise_lds_cap(reinterpret_cast<const void*>(kern), 159 * 1024, done);
     if (attr != hipSuccess) return attr;
   }
   const uint32_t waves = cols / kF32C;
