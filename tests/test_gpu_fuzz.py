@@ -121,9 +121,8 @@ QKV = _qkv_cases()
 
 
 @pytest.mark.parametrize("M,K,Nq,Nkv,bs,zp,skip", QKV, ids=ids(QKV))
-def test_qkv_random(gpu, M, K, Nq, Nkv, bs, zp, skip):
+def test_qkv_random(gpu, M, K, Nq, Nkv, bs, zp, skip, dt=np.float16):
     rng = np.random.default_rng([SEED, 1, M, K, Nq, Nkv, bs])
-    dt = np.float16
     A = rng.standard_normal((M, K)).astype(dt)
     sk = rng.standard_normal((M, K)).astype(dt) if skip else None
     g = rng.uniform(0.5, 1.5, K).astype(dt)
@@ -155,9 +154,8 @@ MLP = _mlp_cases()
 
 
 @pytest.mark.parametrize("M,K,N,bs,skip,norm,biases,act,res", MLP, ids=ids(MLP))
-def test_mlp_random(gpu, M, K, N, bs, skip, norm, biases, act, res):
+def test_mlp_random(gpu, M, K, N, bs, skip, norm, biases, act, res, dt=np.float16):
     rng = np.random.default_rng([SEED, 2, M, K, N, bs])
-    dt = np.float16
     A = rng.standard_normal((M, K)).astype(dt)
     sk = rng.standard_normal((M, K)).astype(dt) if skip else None
     g = rng.uniform(0.5, 1.5, K).astype(dt) if norm else None
@@ -215,6 +213,55 @@ MLP2 = _mlp_prefill_cases()
 @pytest.mark.parametrize("M,K,N,bs,skip,norm,biases,act,res", MLP2, ids=ids(MLP2))
 def test_mlp_prefill_random(gpu, M, K, N, bs, skip, norm, biases, act, res):
     test_mlp_random(gpu, M, K, N, bs, skip, norm, biases, act, res)
+
+
+def _f32_fused_rows(rng):
+    """Up to four rows (the prologue inside the float32 GEMV), up to 16 (a
+    prologue launch, then one GEMV grid), more (one MFMA GEMM grid for every
+    projection)."""
+    return int(rng.choice([1, 3, 4, 5, 9, 16, 17, 33, 64, 100, 130]))
+
+
+def _f32_qkv_cases(n=10):
+    """Float32 Qkv: K tails and whole blocks, every zero-point kind."""
+    rng = np.random.default_rng(SEED + 17)
+    out = []
+    for _ in range(n):
+        bs = int(rng.choice([16, 32, 64, 128]))
+        K = int(rng.choice([2048, 4096])) if rng.random() < 0.4 else int(bs * rng.integers(1, max(2, 1024 // bs + 1)))
+        out.append((_f32_fused_rows(rng), K, int(rng.integers(1, 400)), int(rng.integers(1, 200)), bs,
+                    str(rng.choice(["none", "packed", "float_int", "float"])), bool(rng.integers(0, 2))))
+    return out
+
+
+# plus more than 16 rows with each zero-point kind on the one-grid MFMA GEMM
+F32QKV = _f32_qkv_cases() + [(65, 2048, 256, 64, 32, "packed", True), (200, 1024, 300, 100, 64, "float", True),
+                             (48, 4096, 128, 128, 128, "float_int", False)]
+
+
+@pytest.mark.parametrize("M,K,Nq,Nkv,bs,zp,skip", F32QKV, ids=ids(F32QKV))
+def test_f32_qkv_random(gpu, M, K, Nq, Nkv, bs, zp, skip):
+    test_qkv_random(gpu, M, K, Nq, Nkv, bs, zp, skip, dt=np.float32)
+
+
+def _f32_mlp_cases(n=10):
+    rng = np.random.default_rng(SEED + 18)
+    out = []
+    for _ in range(n):
+        bs = int(rng.choice([16, 32, 64, 128]))
+        K = int(rng.choice([2048, 4096])) if rng.random() < 0.4 else int(bs * rng.integers(1, max(2, 1024 // bs + 1)))
+        out.append((_f32_fused_rows(rng), K, int(rng.integers(1, 600)), bs, bool(rng.integers(0, 2)),
+                    bool(rng.integers(0, 2)), bool(rng.integers(0, 2)), str(rng.choice(["silu", "gelu", "relu", "tanh"])),
+                    bool(rng.integers(0, 2))))
+    return out
+
+
+F32MLP = _f32_mlp_cases()
+
+
+@pytest.mark.parametrize("M,K,N,bs,skip,norm,biases,act,res", F32MLP, ids=ids(F32MLP))
+def test_f32_mlp_random(gpu, M, K, N, bs, skip, norm, biases, act, res):
+    test_mlp_random(gpu, M, K, N, bs, skip, norm, biases, act, res, dt=np.float32)
 
 
 def _f32_cases(n=10):

@@ -86,8 +86,26 @@ bool has_prologue(const Launch& L) { return L.skip || L.gamma || L.residual; }
 int64_t x_bytes(const Launch& L) { return al256(L.M * L.K * 4); }
 int64_t gu_bytes(const Launch& L) { return L.op == OP_MLP ? 2 * al256(L.M * L.p[0].N * 4) : 0; }
 
-// The projections' MatMulNBits workspace: the largest MFMA GEMM need (sized
-// for float zero points, the kind that needs most), when more than 16 rows.
+// All projections as one MatMulNBits launch on `A` (outputs `Y[p]`): one
+// float32 GEMV grid, or one MFMA GEMM grid (given `ws`); the zero-point kind
+// applies only when every projection carries zero points.
+Launch projections(const Launch& L, const void* A, void* const* Y, void* ws, bool& uniform_zp) {
+  Launch Lg = projection(L, 0, A, Y[0], ws);
+  Lg.nproj = L.nproj;
+  int with_zp = 0;
+  for (int p = 0; p < L.nproj; ++p) {
+    Lg.p[p] = L.p[p];
+    Lg.p[p].Y = Y[p];
+    with_zp += L.p[p].zp != nullptr;
+  }
+  Lg.zp_kind = with_zp ? L.zp_kind : ZP_NONE;
+  uniform_zp = with_zp == 0 || with_zp == L.nproj;
+  return Lg;
+}
+
+// The projections' MatMulNBits workspace: the largest MFMA GEMM need, one
+// projection or all on one grid (sized for float zero points, the kind that
+// needs most), when more than 16 rows.
 int64_t proj_ws_bytes(const Launch& L) {
   if (L.M <= 16) return 0;
   static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
@@ -101,7 +119,12 @@ int64_t proj_ws_bytes(const Launch& L) {
     const int64_t b = f32x_workspace_bytes(L2);
     need = b > need ? b : need;
   }
-  return need;
+  void* const ys[3] = {nullptr, nullptr, nullptr};
+  bool uz = true;
+  Launch Lm = projections(L, dummy, ys, const_cast<uint8_t*>(dummy), uz);
+  Lm.zp_kind = ZP_FLOAT;
+  const int64_t b = f32x_workspace_bytes(Lm);
+  return b > need ? b : need;
 }
 
 }  // namespace
@@ -178,8 +201,19 @@ hipError_t launch_f32_split(const Launch& L, hipStream_t st) {
       x = xf;
     }
     void* pws = L.M > 16 ? w + x_bytes(L) + gu_bytes(L) : nullptr;
-    for (int p = 0; p < L.nproj; ++p)
-      if (hipError_t e = launch(projection(L, p, x, out_of(p), pws), st); e != hipSuccess) return e;
+    // all projections on one MFMA GEMM grid (one prepass of x) when each
+    // takes the MFMA GEMM, else one launch per projection
+    void* const ys[3] = {out_of(0), L.nproj > 1 ? out_of(1) : nullptr, L.nproj > 2 ? out_of(2) : nullptr};
+    bool uz = true;
+    const Launch Lm = projections(L, x, ys, pws, uz);
+    bool grid = pws != nullptr && uz && f32x_fits(Lm);
+    for (int p = 0; p < L.nproj && grid; ++p) grid = select_kernel(projection(L, p, x, nullptr, pws)) == K_GEMM_F32X;
+    if (grid) {
+      if (hipError_t e = launch_gemm_f32x(Lm, st); e != hipSuccess) return e;
+    } else {
+      for (int p = 0; p < L.nproj; ++p)
+        if (hipError_t e = launch(projection(L, p, x, out_of(p), pws), st); e != hipSuccess) return e;
+    }
   }
   if (L.op == OP_MLP) {
     const int64_t n = L.M * L.p[0].N;

@@ -40,22 +40,36 @@
 namespace xrmm {
 namespace fx {
 
-struct Args {
-  const void* A;     // float16 activations [M][K] (read directly)
-  const f16* Ahi;    // float32 activations, prepared: [M][Kd] binary16 terms (Kd: K padded to whole K steps)
-  const f16* Alo;
+// One projection of the grid (Qkv and Mlp put theirs side by side: the same
+// A, K, codes and zero-point kind).
+struct Proj1 {
   const uint8_t* B;
-  const void* S;     // scales [N][kb], the activations' type
+  const void* S;      // scales [N][kb], the activations' type
   const uint8_t* Z;   // packed zero points or null
   const void* Zf;     // float zero points [N][kb] (the activations' type) or null
   const void* bias;
   void* Y;
+  int N;
+  int cb;  // first column among all projections' (the partials' layout)
+  int ct;  // first column tile on the grid
+};
+
+struct Args {
+  const void* A;     // float16 activations [M][K] (read directly)
+  const f16* Ahi;    // float32 activations, prepared: [M][Kd] binary16 terms (Kd: K padded to whole K steps)
+  const f16* Alo;
+  Proj1 pr[3];
+  int np;              // projections
+  int NT;              // columns of all projections
   const int32_t* ex;   // float32 activations: the row exponents
   const float* rsum;   // float zero points: block sums of the (scaled) rows, [kb][M]
   const int32_t* bad;  // float zero points: rows holding +-Inf or NaN
-  float* part;         // [splits][M][N] with split K
-  int M, K, N, kb, bs, Kd, rowb, zrow, bits, splits;
+  float* part;         // [splits][M][NT] with split K
+  int M, K, kb, bs, Kd, rowb, zrow, bits, splits;
 };
+
+// projection p of the grid (wave-uniform selects, no indexing of the argument)
+__device__ __forceinline__ Proj1 pick(const Args& a, int p) { return p == 0 ? a.pr[0] : p == 1 ? a.pr[1] : a.pr[2]; }
 
 hipError_t launch_gemm_f16(const Args& a, hipStream_t st);  // xrmm_gemm_f32x_h.hip
 
@@ -281,7 +295,11 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
   const int wm = wave / WNW, wn = wave % WNW;
   // workgroup b: split b % splits of tile b / splits (column tiles fastest)
   const int sp = static_cast<int>(blockIdx.x) % a.splits, tb = static_cast<int>(blockIdx.x) / a.splits;
-  const int m0 = (tb / nct) * RT, n0 = (tb % nct) * CT;
+  // column tile ct of all projections' tiles: this workgroup's projection
+  const int ct = tb % nct;
+  const int pj = a.np > 1 && ct >= a.pr[1].ct ? (a.np > 2 && ct >= a.pr[2].ct ? 2 : 1) : 0;
+  const Proj1 P = pick(a, pj);
+  const int m0 = (tb / nct) * RT, n0 = (ct - P.ct) * CT;
   if constexpr (LO) {
     if (tid < RT) {
       const int m = m0 + tid;
@@ -298,8 +316,8 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
   const rsrc_t rAl = mk_rsrc(LO ? a.Alo : a.Ahi, LO ? static_cast<uint32_t>(a.M) * static_cast<uint32_t>(a.Kd) * 2u : 0u);
   const int bcol = tid >> 1, bh = tid & 1;
   const int bn = n0 + bcol;
-  const rsrc_t rB = mk_rsrc(a.B, static_cast<uint32_t>(a.N) * static_cast<uint32_t>(a.rowb));
-  const uint32_t boff = bn < a.N ? static_cast<uint32_t>(bn) * static_cast<uint32_t>(a.rowb) : OOB;
+  const rsrc_t rB = mk_rsrc(P.B, static_cast<uint32_t>(P.N) * static_cast<uint32_t>(a.rowb));
+  const uint32_t boff = bn < P.N ? static_cast<uint32_t>(bn) * static_cast<uint32_t>(a.rowb) : OOB;
   // K steps [kstep0, kstep0 + ksteps) of this split; splits hold whole blocks
   const int kall = a.Kd / KS;
   const int bsteps = BKM == 8 ? a.bs / KS : 1;
@@ -387,7 +405,7 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
 #pragma unroll
   for (int j = 0; j < JN; ++j) {
     const int c = n0 + wn * WC + j * 32 + (lane & 31);
-    col[j] = c < a.N ? c : a.N - 1;
+    col[j] = c < P.N ? c : P.N - 1;
   }
   // Per block and column: the scale, the dequantisation constants
   // -(base + z), z the (integer) zero point, exact in binary16 (the bases are
@@ -407,14 +425,14 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
     Meta mt;
 #pragma unroll
     for (int j = 0; j < JN; ++j) {
-      const float sv = static_cast<float>(static_cast<const T*>(a.S)[static_cast<int64_t>(col[j]) * a.kb + blk]);
+      const float sv = static_cast<float>(static_cast<const T*>(P.S)[static_cast<int64_t>(col[j]) * a.kb + blk]);
       mt.s[j] = past ? 0.f : sv;
       float z = static_cast<float>(1 << (BITS - 1));
       if constexpr (ZK == 1) {
-        const uint32_t zb = a.Z[static_cast<int64_t>(col[j]) * a.zrow + (blk * BITS) / 8];
+        const uint32_t zb = P.Z[static_cast<int64_t>(col[j]) * a.zrow + (blk * BITS) / 8];
         z = static_cast<float>((zb >> ((blk * BITS) % 8)) & ((1u << BITS) - 1u));
       } else if constexpr (ZK == 2) {
-        const float zv = static_cast<float>(static_cast<const T*>(a.Zf)[static_cast<int64_t>(col[j]) * a.kb + blk]);
+        const float zv = static_cast<float>(static_cast<const T*>(P.Zf)[static_cast<int64_t>(col[j]) * a.kb + blk]);
         z = fminf(fmaxf(__builtin_rintf(zv), -1024.f), 1024.f);  // NaN -> -1024, its fraction NaN
         mt.nz[j] = past ? 0.f : -(mt.s[j] * (zv - z));
       }
@@ -573,8 +591,8 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
 #pragma unroll
   for (int j = 0; j < JN; ++j) {
     const int c = n0 + wn * WC + j * 32 + (lane & 31);
-    if (c >= a.N) continue;
-    const float b = (a.splits == 1 && a.bias) ? static_cast<float>(static_cast<const T*>(a.bias)[c]) : 0.f;
+    if (c >= P.N) continue;
+    const float b = (a.splits == 1 && P.bias) ? static_cast<float>(static_cast<const T*>(P.bias)[c]) : 0.f;
 #pragma unroll
     for (int i = 0; i < IM; ++i)
 #pragma unroll
@@ -583,22 +601,27 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
         const int m = m0 + r;
         if (m >= a.M) continue;
         const float v = LO ? yacc[i * JN + j][q] * s_ru[r] : yacc[i * JN + j][q];
-        if (a.splits == 1) static_cast<T*>(a.Y)[static_cast<int64_t>(m) * a.N + c] = static_cast<T>(v + b);
-        else a.part[(static_cast<int64_t>(sp) * a.M + m) * a.N + c] = v;
+        if (a.splits == 1) static_cast<T*>(P.Y)[static_cast<int64_t>(m) * P.N + c] = static_cast<T>(v + b);
+        else a.part[(static_cast<int64_t>(sp) * a.M + m) * a.NT + P.cb + c] = v;
       }
   }
 }
 
-// Y = the splits' partials added in split order, then the bias, rounded once.
+// Y = the splits' partials added in split order, then the bias, rounded once
+// (element i of [M][NT]: the projection of its column).
 template <typename T>
 __global__ __launch_bounds__(256) void k_fx_combine(Args a) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t MN = static_cast<int64_t>(a.M) * a.N;
+  const int64_t MN = static_cast<int64_t>(a.M) * a.NT;
   if (i >= MN) return;
+  const int m = static_cast<int>(i / a.NT), gc = static_cast<int>(i % a.NT);
+  const int pj = a.np > 1 && gc >= a.pr[1].cb ? (a.np > 2 && gc >= a.pr[2].cb ? 2 : 1) : 0;
+  const Proj1 P = pick(a, pj);
+  const int c = gc - P.cb;
   float y = a.part[i];
   for (int s = 1; s < a.splits; ++s) y += a.part[s * MN + i];
-  if (a.bias) y += static_cast<float>(static_cast<const T*>(a.bias)[i % a.N]);
-  static_cast<T*>(a.Y)[i] = static_cast<T>(y);
+  if (P.bias) y += static_cast<float>(static_cast<const T*>(P.bias)[c]);
+  static_cast<T*>(P.Y)[static_cast<int64_t>(m) * P.N + c] = static_cast<T>(y);
 }
 
 // Float zero points: rows holding +-Inf or NaN recomputed in the reference's
@@ -609,11 +632,14 @@ __global__ __launch_bounds__(256) void k_fx_fix(Args a) {
   const int m = blockIdx.x;
   if (!a.bad[m]) return;
   const T* row = static_cast<const T*>(a.A) + static_cast<int64_t>(m) * a.K;
-  const T* S = static_cast<const T*>(a.S);
-  const T* Zf = static_cast<const T*>(a.Zf);
   const int blob = a.bs * BITS / 8;
-  for (int n = threadIdx.x; n < a.N; n += 256) {
-    const uint8_t* Bn = a.B + static_cast<int64_t>(n) * a.rowb;
+  for (int g = threadIdx.x; g < a.NT; g += 256) {
+    const int pj = a.np > 1 && g >= a.pr[1].cb ? (a.np > 2 && g >= a.pr[2].cb ? 2 : 1) : 0;
+    const Proj1 P = pick(a, pj);
+    const int n = g - P.cb;
+    const T* S = static_cast<const T*>(P.S);
+    const T* Zf = static_cast<const T*>(P.Zf);
+    const uint8_t* Bn = P.B + static_cast<int64_t>(n) * a.rowb;
     float acc = 0.f;
     for (int k = 0; k < a.K; ++k) {
       const int b = k / a.bs, e = k - b * a.bs;
@@ -622,8 +648,8 @@ __global__ __launch_bounds__(256) void k_fx_fix(Args a) {
       const float w = (static_cast<float>(c) - static_cast<float>(Zf[i])) * static_cast<float>(S[i]);
       acc += static_cast<float>(row[k]) * w;
     }
-    if (a.bias) acc += static_cast<float>(static_cast<const T*>(a.bias)[n]);
-    static_cast<T*>(a.Y)[static_cast<int64_t>(m) * a.N + n] = static_cast<T>(acc);
+    if (P.bias) acc += static_cast<float>(static_cast<const T*>(P.bias)[n]);
+    static_cast<T*>(P.Y)[static_cast<int64_t>(m) * P.N + n] = static_cast<T>(acc);
   }
 }
 
@@ -654,19 +680,19 @@ hipError_t launch_b(const Args& a, int nct, int64_t grid, hipStream_t st) {
 
 template <typename T, int BITS>
 hipError_t launch_z(const Args& a, int nct, int64_t grid, hipStream_t st) {
-  if (a.Zf) {
+  if (a.pr[0].Zf) {
     if (hipError_t e = launch_b<T, BITS, 2>(a, nct, grid, st); e != hipSuccess) return e;
     if (a.splits > 1) {
-      const int64_t MN = static_cast<int64_t>(a.M) * a.N;
+      const int64_t MN = static_cast<int64_t>(a.M) * a.NT;
       hipLaunchKernelGGL(k_fx_combine<T>, dim3(static_cast<uint32_t>((MN + 255) / 256)), dim3(256), 0, st, a);
     }
     hipLaunchKernelGGL((k_fx_fix<T, BITS>), dim3(static_cast<uint32_t>(a.M)), dim3(256), 0, st, a);
     return hipGetLastError();
   }
-  hipError_t e = a.Z ? launch_b<T, BITS, 1>(a, nct, grid, st) : launch_b<T, BITS, 0>(a, nct, grid, st);
+  hipError_t e = a.pr[0].Z ? launch_b<T, BITS, 1>(a, nct, grid, st) : launch_b<T, BITS, 0>(a, nct, grid, st);
   if (e != hipSuccess) return e;
   if (a.splits > 1) {
-    const int64_t MN = static_cast<int64_t>(a.M) * a.N;
+    const int64_t MN = static_cast<int64_t>(a.M) * a.NT;
     hipLaunchKernelGGL(k_fx_combine<T>, dim3(static_cast<uint32_t>((MN + 255) / 256)), dim3(256), 0, st, a);
   }
   return hipGetLastError();
@@ -676,7 +702,8 @@ hipError_t launch_z(const Args& a, int nct, int64_t grid, hipStream_t st) {
 // non-finite rows with float zero points) for activations of type T.
 template <typename T>
 hipError_t launch_gemm(const Args& a, hipStream_t st) {
-  const int nct = (a.N + CT - 1) / CT;
+  int nct = 0;
+  for (int p = 0; p < a.np; ++p) nct += (a.pr[p].N + CT - 1) / CT;
   const int64_t grid = static_cast<int64_t>((a.M + RT - 1) / RT) * nct * a.splits;
   if (a.bits == 8) return launch_z<T, 8>(a, nct, grid, st);
   if (a.bits == 2) return launch_z<T, 2>(a, nct, grid, st);

@@ -29,12 +29,25 @@ int64_t fx_rs_bytes(const Launch& L) {
 }
 int64_t fx_prep_bytes(const Launch& L) { return fx_hl_bytes(L) + fx_rs_bytes(L); }
 
+// columns and column tiles of all projections (Qkv / Mlp put theirs side by
+// side on one grid)
+int64_t fx_cols(const Launch& L) {
+  int64_t n = 0;
+  for (int p = 0; p < L.nproj; ++p) n += L.p[p].N;
+  return n;
+}
+int64_t fx_ctiles(const Launch& L) {
+  int64_t t = 0;
+  for (int p = 0; p < L.nproj; ++p) t += (L.p[p].N + fx::CT - 1) / fx::CT;
+  return t;
+}
+
 }  // namespace
 
 // K splits: enough for about 256 workgroups (one per CU) when the tiles are
 // fewer, eight at most, each split at least 8 K steps of 64.
 int f32x_splits(const Launch& L) {
-  const int64_t tiles = ((L.M + fx::RT - 1) / fx::RT) * ((L.p[0].N + fx::CT - 1) / fx::CT);
+  const int64_t tiles = ((L.M + fx::RT - 1) / fx::RT) * fx_ctiles(L);
   const int64_t ksteps = fx_kd(L) / fx::KS;
   int64_t s = (256 + tiles - 1) / tiles;
   if (s > 8) s = 8;
@@ -44,7 +57,7 @@ int f32x_splits(const Launch& L) {
 
 int64_t f32x_workspace_bytes(const Launch& L) {
   const int s = f32x_splits(L);
-  return kFxKeep + fx_prep_bytes(L) + (s > 1 ? al256(int64_t(s) * L.M * L.p[0].N * 4) : 0);
+  return kFxKeep + fx_prep_bytes(L) + (s > 1 ? al256(int64_t(s) * L.M * fx_cols(L) * 4) : 0);
 }
 
 // MatMulNBits with more than 16 rows: float32 activations with 2-, 4- or
@@ -52,9 +65,12 @@ int64_t f32x_workspace_bytes(const Launch& L) {
 // exact weights; K a multiple of 8, A 16-byte aligned); blocks of 32 or more
 // codes (powers of two), packed, float
 // (of the activations' type, blocks of 64 or more) or no zero points,
-// 16-byte aligned B, 32-bit offsets. The caller supplies the workspace.
+// 16-byte aligned B, 32-bit offsets; up to three projections of one A (the
+// same zero-point kind, present on all or none). The caller supplies the
+// workspace.
 bool f32x_fits(const Launch& L) {
   if (L.op != OP_MATMUL || L.M <= 16 || (L.bits != 2 && L.bits != 4 && L.bits != 8)) return false;
+  if (L.nproj < 1 || L.nproj > 3) return false;
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   if (L.dtype == DT_F16) {
     if (L.bits == 4 && !L.exact_weights) return false;  // the binary16 GEMMs
@@ -63,25 +79,38 @@ bool f32x_fits(const Launch& L) {
     return false;
   }
   if (L.block_size < 32 || L.bs_log2 < 5) return false;
-  if (L.zp_kind == ZP_FLOAT && (L.zp_dtype != L.dtype || L.p[0].zp == nullptr || L.block_size < 64)) return false;
-  if (!al(L.p[0].B)) return false;
+  if (L.zp_kind == ZP_FLOAT && (L.zp_dtype != L.dtype || L.block_size < 64)) return false;
   const int64_t lim = int64_t(1) << 31, rowb = fx_kd(L) * L.bits / 8;  // rows as read (past the last: zeros)
-  return L.M * fx_kd(L) * 4 < lim && L.M * L.K * 4 < lim && L.p[0].N * rowb < lim && L.kb * L.M * 4 < lim &&
-         int64_t(f32x_splits(L)) * L.M * L.p[0].N < lim && L.p[0].N * L.kb < lim && L.M < lim / fx::RT;
+  for (int p = 0; p < L.nproj; ++p) {
+    if (!al(L.p[p].B) || (L.zp_kind != ZP_NONE && L.p[p].zp == nullptr)) return false;
+    if (L.p[p].N * rowb >= lim || L.p[p].N * L.kb >= lim) return false;
+  }
+  return L.M * fx_kd(L) * 4 < lim && L.M * L.K * 4 < lim && L.kb * L.M * 4 < lim &&
+         int64_t(f32x_splits(L)) * L.M * fx_cols(L) < lim && L.M < lim / fx::RT;
 }
 
 hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st) {
   fx::Args a{};
   a.A = L.A;
-  a.B = L.p[0].B;
-  a.S = L.p[0].scales;
-  a.Z = L.zp_kind == ZP_PACKED ? static_cast<const uint8_t*>(L.p[0].zp) : nullptr;
-  a.Zf = L.zp_kind == ZP_FLOAT ? L.p[0].zp : nullptr;
-  a.bias = L.p[0].bias;
-  a.Y = L.p[0].Y;
+  a.np = L.nproj;
+  int cb = 0, ct = 0;
+  for (int p = 0; p < L.nproj; ++p) {
+    fx::Proj1& q = a.pr[p];
+    q.B = L.p[p].B;
+    q.S = L.p[p].scales;
+    q.Z = L.zp_kind == ZP_PACKED ? static_cast<const uint8_t*>(L.p[p].zp) : nullptr;
+    q.Zf = L.zp_kind == ZP_FLOAT ? L.p[p].zp : nullptr;
+    q.bias = L.p[p].bias;
+    q.Y = L.p[p].Y;
+    q.N = static_cast<int>(L.p[p].N);
+    q.cb = cb;
+    q.ct = ct;
+    cb += q.N;
+    ct += (q.N + fx::CT - 1) / fx::CT;
+  }
+  a.NT = cb;
   a.M = static_cast<int>(L.M);
   a.K = static_cast<int>(L.K);
-  a.N = static_cast<int>(L.p[0].N);
   a.kb = static_cast<int>(L.kb);
   a.bs = static_cast<int>(L.block_size);
   a.Kd = static_cast<int>(fx_kd(L));
