@@ -83,6 +83,16 @@ bool has_prologue(const Launch& L) { return L.skip || L.gamma || L.residual; }
 
 // x is reserved whether or not the call has a prologue: the workspace size is
 // asked without knowing whether the caller wants the residual
+// Rows from which the projections share one MFMA GEMM grid (below: one
+// float32 GEMV grid). From 5 rows the GEMV's float32 FMAs cost more than the
+// GEMM's weight decode: Mlp K = 2048, N = 5632 at 16 rows 38.7 -> 26.2 us,
+// Qkv K = 4096, N = 3 x 4096 at 8 rows 54.2 -> 49.6 us, at 16 rows 99.8 ->
+// 51.5 us (5 rows: Mlp 23.7 -> 24.4, Qkv 53.3 -> 49.8 us).
+#ifndef XRMM_F32_SPLIT_GEMM_ROWS
+#define XRMM_F32_SPLIT_GEMM_ROWS 5
+#endif
+constexpr int64_t kGridRows = XRMM_F32_SPLIT_GEMM_ROWS;
+
 int64_t x_bytes(const Launch& L) { return al256(L.M * L.K * 4); }
 int64_t gu_bytes(const Launch& L) { return L.op == OP_MLP ? 2 * al256(L.M * L.p[0].N * 4) : 0; }
 
@@ -105,9 +115,9 @@ Launch projections(const Launch& L, const void* A, void* const* Y, void* ws, boo
 
 // The projections' MatMulNBits workspace: the largest MFMA GEMM need, one
 // projection or all on one grid (sized for float zero points, the kind that
-// needs most), when more than 16 rows.
+// needs most), from kGridRows rows on.
 int64_t proj_ws_bytes(const Launch& L) {
-  if (L.M <= 16) return 0;
+  if (L.M < kGridRows) return 0;
   static const uint8_t dummy[16] __attribute__((aligned(16))) = {0};
   int64_t need = 0;
   for (int p = 0; p < L.nproj; ++p) {
@@ -153,8 +163,8 @@ hipError_t launch_f32_split(const Launch& L, hipStream_t st) {
   float* g = reinterpret_cast<float*>(w + x_bytes(L));
   float* u = reinterpret_cast<float*>(w + x_bytes(L) + gu_bytes(L) / 2);
   auto out_of = [&](int p) { return L.op == OP_MLP ? static_cast<void*>(p == 0 ? g : u) : L.p[p].Y; };
-  // up to 16 rows: every projection on one float32 GEMV grid, when they all
-  // fit it; up to 4 rows (one row chunk of the grid) the prologue runs on
+  // below kGridRows rows: every projection on one float32 GEMV grid, when
+  // they all fit it; up to 4 rows (one row chunk of the grid) the prologue runs on
   // the GEMV's staged rows, beyond that once per row in k_f32_prologue (each
   // row chunk's workgroups would otherwise all redo it)
   const bool fuse = L.M <= 4;
@@ -174,7 +184,7 @@ hipError_t launch_f32_split(const Launch& L, hipStream_t st) {
   }
   // one zero-point kind on the grid: all projections carry zero points or none
   Lg.zp_kind = with_zp ? L.zp_kind : ZP_NONE;
-  bool one = L.M <= 16 && (with_zp == 0 || with_zp == L.nproj) && f32_fits(Lg) && fits_i32(Lg);
+  bool one = L.M < kGridRows && L.M <= 16 && (with_zp == 0 || with_zp == L.nproj) && f32_fits(Lg) && fits_i32(Lg);
   for (int p = 0; p < L.nproj && one; ++p) one = select_kernel(projection(L, p, Lg.A, nullptr, nullptr)) == K_GEMV_F32;
   if (one) {
     if (!fuse && has_prologue(L)) {
@@ -200,14 +210,13 @@ hipError_t launch_f32_split(const Launch& L, hipStream_t st) {
       if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
       x = xf;
     }
-    void* pws = L.M > 16 ? w + x_bytes(L) + gu_bytes(L) : nullptr;
+    void* pws = L.M >= kGridRows ? w + x_bytes(L) + gu_bytes(L) : nullptr;
     // all projections on one MFMA GEMM grid (one prepass of x) when each
     // takes the MFMA GEMM, else one launch per projection
     void* const ys[3] = {out_of(0), L.nproj > 1 ? out_of(1) : nullptr, L.nproj > 2 ? out_of(2) : nullptr};
     bool uz = true;
     const Launch Lm = projections(L, x, ys, pws, uz);
-    bool grid = pws != nullptr && uz && f32x_fits(Lm);
-    for (int p = 0; p < L.nproj && grid; ++p) grid = select_kernel(projection(L, p, x, nullptr, pws)) == K_GEMM_F32X;
+    const bool grid = pws != nullptr && uz && f32x_fits(Lm, kGridRows);
     if (grid) {
       if (hipError_t e = launch_gemm_f32x(Lm, st); e != hipSuccess) return e;
     } else {

@@ -60,7 +60,7 @@ int64_t f32x_workspace_bytes(const Launch& L) {
   return kFxKeep + fx_prep_bytes(L) + (s > 1 ? al256(int64_t(s) * L.M * fx_cols(L) * 4) : 0);
 }
 
-// MatMulNBits with more than 16 rows: float32 activations with 2-, 4- or
+// MatMulNBits with at least `min_rows` rows (17 for one MatMulNBits): float32 activations with 2-, 4- or
 // 8-bit codes (any K), float16 activations with 2- or 8-bit codes (4-bit with
 // exact weights; K a multiple of 8, A 16-byte aligned); blocks of 32 or more
 // codes (powers of two), packed, float
@@ -68,8 +68,8 @@ int64_t f32x_workspace_bytes(const Launch& L) {
 // 16-byte aligned B, 32-bit offsets; up to three projections of one A (the
 // same zero-point kind, present on all or none). The caller supplies the
 // workspace.
-bool f32x_fits(const Launch& L) {
-  if (L.op != OP_MATMUL || L.M <= 16 || (L.bits != 2 && L.bits != 4 && L.bits != 8)) return false;
+bool f32x_fits(const Launch& L, int64_t min_rows) {
+  if (L.op != OP_MATMUL || L.M < min_rows || L.M < 1 || (L.bits != 2 && L.bits != 4 && L.bits != 8)) return false;
   if (L.nproj < 1 || L.nproj > 3) return false;
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   if (L.dtype == DT_F16) {

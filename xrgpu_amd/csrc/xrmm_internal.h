@@ -88,7 +88,7 @@ inline int64_t fused_xs_bytes(const Launch& L) { return (L.M * L.K * 2 + 255) / 
 // (xrmm_gemm_f32x.hip): whether a geometry fits, its K splits, the workspace
 // it needs (prepared float32 rows and split partials; the launch takes it
 // from Launch::ws), and the launch.
-bool f32x_fits(const Launch& L);
+bool f32x_fits(const Launch& L, int64_t min_rows = 17);
 int f32x_splits(const Launch& L);
 int64_t f32x_workspace_bytes(const Launch& L);
 hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st);
