@@ -94,7 +94,8 @@ int xrmm_matmul_nbits(const void* A, const void* B, const void* scales, const vo
  * xrmm_matmul_nbits within the float16 bar.
  * The workspace also carries the float32-arithmetic MFMA GEMM that runs
  * more than 16 rows of float32 activations, or of float16 activations with
- * 2- or 8-bit codes ("gemm_f32_mfma"; without a workspace those calls take
+ * 2- or 8-bit codes (from 12 rows for weight matrices of 2^24 codes or more,
+ * from 5 rows for 2^25 or more; "gemm_f32_mfma"; without a workspace those calls take
  * the float32-arithmetic GEMV): its prepared rows (binary16 hi / lo terms of
  * float32 activations, block sums for float zero points) and split partials;
  * same results as xrmm_matmul_nbits within the float32 bar (float32

@@ -113,7 +113,11 @@ def test_qkv_requires_norm_scale():
     (0, 4, 4096, 14336, 64, nat.F32, nat.F32, "gemv_q4_f32"),
     (0, 5, 2048, 2048, 32, nat.F32, nat.U8, "gemv_q4_f32"),         # float32 beyond four rows: chunks of four
     (0, 64, 4096, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemm_f32_mfma"),  # float32, more than 16 rows: MFMA
-    (0, 16, 4096, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),
+    (0, 16, 4096, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemm_f32_mfma"),  # 2^24 codes: MFMA from 12 rows
+    (0, 11, 4096, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),
+    (0, 5, 4096, 14336, 32, nat.F32, nat.UNSPECIFIED, "gemm_f32_mfma"),  # 2^25 codes or more: from 5 rows
+    (0, 4, 4096, 14336, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),
+    (0, 16, 2048, 5632, 32, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),    # fewer codes: the GEMV up to 16 rows
     (0, 64, 4000, 4096, 32, nat.F32, nat.UNSPECIFIED, "gemm_f32_mfma"),  # padded K not a multiple of 64
     (0, 64, 4096, 4096, 16, nat.F32, nat.UNSPECIFIED, "gemv_q4_f32"),    # blocks of 16
     (0, 64, 4096, 4096, 32, nat.F32, nat.F32, "gemv_q4_f32"),            # float zero points, blocks of 32

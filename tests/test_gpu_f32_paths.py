@@ -122,6 +122,9 @@ MFMA_CASES = [
     (48, 2561, 1021, 8, 32, None, False),      # upstream tail case: K % 4 != 0, half a last K step
     (32, 2561, 4096, 4, 32, "packed", True),
     (17, 99, 33, 4, 64, None, True),           # one short K step
+    (5, 4096, 8192, 4, 32, "packed", True),    # 2^25 codes: the GEMM from 5 rows
+    (12, 4096, 4096, 8, 64, "float", False),   # 2^24 codes: from 12 rows
+    (16, 4096, 14336, 2, 64, None, True),
 ]
 
 
@@ -239,6 +242,8 @@ F16_MFMA_CASES = [
     (200, 1000, 257, 8, 256, None, False),       # partial last block (K % 8 == 0)
     (128, 5120, 1040, 2, 128, "float16", False),  # upstream bonsai2: float16 zero points
     (64, 2048, 300, 8, 64, "float16", True),
+    (12, 4096, 4096, 8, 32, None, False),        # 2^24 codes: from 12 rows
+    (9, 4096, 8192, 2, 64, "float16", True),     # 2^25 codes: from 5 rows
 ]
 
 

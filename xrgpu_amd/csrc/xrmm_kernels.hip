@@ -661,6 +661,21 @@ inline bool thin_takes(const Launch& L) {
   return false;
 }
 
+// Rows from which MatMulNBits takes the float32-arithmetic MFMA GEMM: 17, or
+// fewer for large weight matrices, where the float32 GEMV's FMAs per row
+// cost more than the GEMM's fixed prepass and decode. Measured with 4-bit
+// codes and float32 activations: K = N = 4096 at 12 rows 25.4 -> 20.4 us, at
+// 16 rows 32.0 -> 20.8; K = 4096, N = 14336 at 5 rows 54.4 -> 43.2, at 16
+// rows 110.9 -> 44.8; K = 2048, N = 5632 stays on the GEMV (16.5 against
+// 20.1 us at 16 rows); float16 activations at K = N = 4096, 12 rows: 8-bit
+// 22.3 -> 15.5, 2-bit 17.2 -> 13.1 us. Float16 4-bit (exact weights) keeps
+// 17: its dot GEMVs stay in binary16 arithmetic.
+inline int64_t f32x_min_rows(const Launch& L) {
+  if (L.dtype == DT_F16 && L.bits == 4) return 17;
+  const int64_t w = L.K * L.p[0].N;
+  return w >= (int64_t(1) << 25) ? 5 : w >= (int64_t(1) << 24) ? 12 : 17;
+}
+
 Kernel select_kernel(const Launch& L) {
   // float32 Qkv / Mlp with the caller's workspace: prologue + float32
   // MatMulNBits per projection
@@ -668,7 +683,7 @@ Kernel select_kernel(const Launch& L) {
   if (L.exact_weights) {
     // the dot and four-row MFMA GEMVs and the float32-arithmetic GEMM keep
     // weights out of binary16; every other fast kernel stages binary16 weights
-    if (L.ws != nullptr && f32x_fits(L)) return K_GEMM_F32X;
+    if (L.ws != nullptr && f32x_fits(L, f32x_min_rows(L))) return K_GEMM_F32X;
     if (q4_fast_ok(L) && fits_i32(L) && mq_takes(L)) return K_GEMV_MQ;
     if (q4_fast_ok(L) && fits_i32(L) && (L.op == OP_MATMUL || (L.op == OP_QKV && L.gamma)) && L.M >= 1 &&
         L.M < split_k_min_rows(L.op) && dot_fits(L))
@@ -677,9 +692,10 @@ Kernel select_kernel(const Launch& L) {
     if (f32_fits(L) && fits_i32(L)) return K_GEMV_F32;
     return K_GENERIC;
   }
-  // more than 16 rows of float32 activations, or of float16 activations with
-  // 2- or 8-bit codes, and a caller workspace: the float32-arithmetic GEMM
-  if (L.ws != nullptr && f32x_fits(L)) return K_GEMM_F32X;
+  // more than 16 rows (fewer for large weight matrices) of float32
+  // activations, or of float16 activations with 2- or 8-bit codes, and a
+  // caller workspace: the float32-arithmetic GEMM
+  if (L.ws != nullptr && f32x_fits(L, f32x_min_rows(L))) return K_GEMM_F32X;
   // float32 activations (the contract's T1 = float32) and float16 with 8-bit
   // codes, any row count: the float32-arithmetic GEMV
   if (f32_fits(L) && fits_i32(L)) return K_GEMV_F32;

@@ -121,8 +121,9 @@ def matmul_nbits(A, B, scales, zero_points=None, bias=None, *, K=None, N=None, b
 
     Geometries with few output tiles split K across workgroups on a workspace
     (``matmul_nbits_workspace_bytes``), and float32 activations with more than
-    16 rows run the float32 matrix-core GEMM, whose row exponents (and split
-    partials) live there too. Eager calls use one zero-filled
+    16 rows (from 5 or 12 rows for weight matrices of 2^25 or 2^24 codes) run
+    the float32 matrix-core GEMM, whose row exponents (and split partials)
+    live there too. Eager calls use one zero-filled
     workspace per (device, stream) kept by this module. A caller may pass its
     own ``workspace`` (uint8, 256-byte aligned, its first 4096 bytes zero
     before first use; every call leaves them zero); calls that may overlap
@@ -143,7 +144,7 @@ def matmul_nbits(A, B, scales, zero_points=None, bias=None, *, K=None, N=None, b
         out = torch.empty(tuple(A.shape[:-1]) + (N,), dtype=A.dtype, device=A.device)
     lib = nat.lib()
     s = _stream(stream, dev)
-    need = lib.xrmm_matmul_nbits_workspace_bytes(M, K, N, bits, block_size, _t1(A)) if M > 16 else 0
+    need = lib.xrmm_matmul_nbits_workspace_bytes(M, K, N, bits, block_size, _t1(A)) if M > 4 else 0
     if need > 0 and workspace is not None:
         if workspace.dtype != torch.uint8 or workspace.numel() < need or workspace.get_device() != dev:
             raise nat.XrmmInvalid(f"workspace must be uint8 with at least {need} bytes on A's device")
