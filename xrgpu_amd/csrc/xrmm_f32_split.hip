@@ -168,6 +168,7 @@ hipError_t launch_f32_split(const Launch& L, hipStream_t st) {
   // the GEMV's staged rows, beyond that once per row in k_f32_prologue (each
   // row chunk's workgroups would otherwise all redo it)
   const bool fuse = L.M <= 4;
+  bool act_done = false;
   Launch Lg = projection(L, 0, fuse || !has_prologue(L) ? L.A : w, out_of(0), nullptr);
   Lg.nproj = L.nproj;
   if (fuse) {
@@ -217,14 +218,19 @@ hipError_t launch_f32_split(const Launch& L, hipStream_t st) {
     bool uz = true;
     const Launch Lm = projections(L, x, ys, pws, uz);
     const bool grid = pws != nullptr && uz && f32x_fits(Lm, kGridRows);
+    // Mlp with split K and no float zero points (whose non-finite rows are
+    // recomputed after the combine): the combine forms act(gate) * up
+    act_done = grid && L.op == OP_MLP && Lm.zp_kind != ZP_FLOAT && f32x_splits(Lm) > 1;
     if (grid) {
-      if (hipError_t e = launch_gemm_f32x(Lm, st); e != hipSuccess) return e;
+      if (hipError_t e = launch_gemm_f32x(Lm, st, act_done ? static_cast<float*>(L.p[0].Y) : nullptr, L.act);
+          e != hipSuccess)
+        return e;
     } else {
       for (int p = 0; p < L.nproj; ++p)
         if (hipError_t e = launch(projection(L, p, x, out_of(p), pws), st); e != hipSuccess) return e;
     }
   }
-  if (L.op == OP_MLP) {
+  if (L.op == OP_MLP && !act_done) {
     const int64_t n = L.M * L.p[0].N;
     hipLaunchKernelGGL(k_mlp_act, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, st, g, u,
                        static_cast<float*>(L.p[0].Y), n, L.act);

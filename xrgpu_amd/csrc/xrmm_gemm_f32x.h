@@ -65,6 +65,8 @@ struct Args {
   const float* rsum;   // float zero points: block sums of the (scaled) rows, [kb][M]
   const int32_t* bad;  // float zero points: rows holding +-Inf or NaN
   float* part;         // [splits][M][NT] with split K
+  float* Yact;         // Mlp (two projections of one N): act(gate) * up [M][N] from the combine, or null
+  int act;             // its activation
   int M, K, kb, bs, Kd, rowb, zrow, bits, splits;
 };
 
@@ -608,11 +610,27 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
 }
 
 // Y = the splits' partials added in split order, then the bias, rounded once
-// (element i of [M][NT]: the projection of its column).
+// (element i of [M][NT]: the projection of its column). With Yact (Mlp: gate
+// and up of one N side by side), element i of [M][N] is act(gate) * up of
+// the two sums, as float32 gate / up rows would give it.
 template <typename T>
 __global__ __launch_bounds__(256) void k_fx_combine(Args a) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t MN = static_cast<int64_t>(a.M) * a.NT;
+  if (a.Yact) {
+    const int N = a.pr[0].N;
+    if (i >= static_cast<int64_t>(a.M) * N) return;
+    const int64_t m = i / N, c = i % N, ig = m * a.NT + c, iu = ig + N;
+    float g = a.part[ig], u = a.part[iu];
+    for (int s = 1; s < a.splits; ++s) {
+      g += a.part[s * MN + ig];
+      u += a.part[s * MN + iu];
+    }
+    if (a.pr[0].bias) g += static_cast<float>(static_cast<const T*>(a.pr[0].bias)[c]);
+    if (a.pr[1].bias) u += static_cast<float>(static_cast<const T*>(a.pr[1].bias)[c]);
+    a.Yact[i] = activate(g, a.act) * u;
+    return;
+  }
   if (i >= MN) return;
   const int m = static_cast<int>(i / a.NT), gc = static_cast<int>(i % a.NT);
   const int pj = a.np > 1 && gc >= a.pr[1].cb ? (a.np > 2 && gc >= a.pr[2].cb ? 2 : 1) : 0;
@@ -692,7 +710,7 @@ hipError_t launch_z(const Args& a, int nct, int64_t grid, hipStream_t st) {
   hipError_t e = a.pr[0].Z ? launch_b<T, BITS, 1>(a, nct, grid, st) : launch_b<T, BITS, 0>(a, nct, grid, st);
   if (e != hipSuccess) return e;
   if (a.splits > 1) {
-    const int64_t MN = static_cast<int64_t>(a.M) * a.NT;
+    const int64_t MN = static_cast<int64_t>(a.M) * (a.Yact ? a.pr[0].N : a.NT);
     hipLaunchKernelGGL(k_fx_combine<T>, dim3(static_cast<uint32_t>((MN + 255) / 256)), dim3(256), 0, st, a);
   }
   return hipGetLastError();

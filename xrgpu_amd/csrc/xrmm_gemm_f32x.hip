@@ -89,8 +89,12 @@ bool f32x_fits(const Launch& L, int64_t min_rows) {
          int64_t(f32x_splits(L)) * L.M * fx_cols(L) < lim && L.M < lim / fx::RT;
 }
 
-hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st) {
+hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st, float* act_out, int act) {
+  if (act_out && (L.nproj != 2 || L.p[0].N != L.p[1].N || L.zp_kind == ZP_FLOAT || f32x_splits(L) < 2))
+    return hipErrorInvalidValue;
   fx::Args a{};
+  a.Yact = act_out;
+  a.act = act;
   a.A = L.A;
   a.np = L.nproj;
   int cb = 0, ct = 0;

@@ -91,7 +91,9 @@ inline int64_t fused_xs_bytes(const Launch& L) { return (L.M * L.K * 2 + 255) / 
 bool f32x_fits(const Launch& L, int64_t min_rows = 17);
 int f32x_splits(const Launch& L);
 int64_t f32x_workspace_bytes(const Launch& L);
-hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st);
+// act_out: Mlp's two projections (one N, no float zero points, split K)
+// finished as act(gate) * up [M][N] float32 by the combine
+hipError_t launch_gemm_f32x(const Launch& L, hipStream_t st, float* act_out = nullptr, int act = 0);
 
 // Float32 Qkv / Mlp as a prologue and one float32 MatMulNBits per projection
 // (xrmm_f32_split.hip): whether a geometry fits, the workspace it needs
