@@ -27,19 +27,43 @@ namespace {
 int64_t al256(int64_t b) { return (b + 255) / 256 * 256; }
 
 // One workgroup per row: r = A + skip (float32), the residual, and x = r or
-// r * inversesqrt(sum(r^2) / K + eps) * gamma.
+// r * inversesqrt(sum(r^2) / K + eps) * gamma. Rows of up to 256 * kProHeld
+// elements stay in registers: every load of the row (and of gamma) is issued
+// before the first use, and x is written once.
+constexpr int kProHeld = 16;
+
 __global__ __launch_bounds__(256) void k_f32_prologue(const float* __restrict__ A, const float* __restrict__ skip,
                                                       const float* __restrict__ gamma, float* __restrict__ x,
                                                       float* __restrict__ residual, int K, float eps) {
   __shared__ float red[4];
   const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
   const int64_t o = static_cast<int64_t>(m) * K;
+  const bool held = K <= 256 * kProHeld;
   float ss = 0.f;
-  for (int k = tid; k < K; k += 256) {
-    const float r = skip ? A[o + k] + skip[o + k] : A[o + k];
-    x[o + k] = r;
-    if (residual) residual[o + k] = r;
-    ss = __builtin_fmaf(r, r, ss);
+  float rv[kProHeld], gv[kProHeld];
+  if (held) {
+#pragma unroll
+    for (int j = 0; j < kProHeld; ++j) {
+      const int k = tid + 256 * j;
+      rv[j] = k < K ? (skip ? A[o + k] + skip[o + k] : A[o + k]) : 0.f;
+      gv[j] = k < K && gamma ? gamma[k] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < kProHeld; ++j) {
+      const int k = tid + 256 * j;
+      if (k < K) {
+        if (!gamma) x[o + k] = rv[j];
+        if (residual) residual[o + k] = rv[j];
+        ss = __builtin_fmaf(rv[j], rv[j], ss);
+      }
+    }
+  } else {
+    for (int k = tid; k < K; k += 256) {
+      const float r = skip ? A[o + k] + skip[o + k] : A[o + k];
+      x[o + k] = r;
+      if (residual) residual[o + k] = r;
+      ss = __builtin_fmaf(r, r, ss);
+    }
   }
   if (!gamma) return;  // uniform
 #pragma unroll
@@ -48,6 +72,14 @@ __global__ __launch_bounds__(256) void k_f32_prologue(const float* __restrict__ 
   __syncthreads();
   ss = (red[0] + red[1]) + (red[2] + red[3]);
   const float inv = 1.f / __builtin_sqrtf(ss / static_cast<float>(K) + eps);
+  if (held) {
+#pragma unroll
+    for (int j = 0; j < kProHeld; ++j) {
+      const int k = tid + 256 * j;
+      if (k < K) x[o + k] = rv[j] * inv * gv[j];
+    }
+    return;
+  }
   // each thread rescales the elements it wrote
   for (int k = tid; k < K; k += 256) x[o + k] = x[o + k] * inv * gamma[k];
 }
