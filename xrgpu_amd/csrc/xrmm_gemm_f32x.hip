@@ -44,12 +44,16 @@ int64_t fx_ctiles(const Launch& L) {
 
 }  // namespace
 
-// K splits: enough for about 256 workgroups (one per CU) when the tiles are
-// fewer, eight at most, each split at least 8 K steps of 64.
+// K splits when the tiles are fewer than 256 (one per CU), eight at most,
+// each split at least 8 K steps of 64: float32 activations as many as keep
+// the grid within 256 workgroups (a second round of a few workgroups costs
+// a whole K pass: K = 4096, N = 14336 at 8 rows 44.0 us with 5 splits, 30.9
+// with 4), float16 activations at least 256 workgroups (K = 5120,
+// N = 17408 at 128 rows: 57.6 us with 2 splits, 61.9 with 1).
 int f32x_splits(const Launch& L) {
   const int64_t tiles = ((L.M + fx::RT - 1) / fx::RT) * fx_ctiles(L);
   const int64_t ksteps = fx_kd(L) / fx::KS;
-  int64_t s = (256 + tiles - 1) / tiles;
+  int64_t s = L.dtype == DT_F32 ? (tiles < 256 ? 256 / tiles : 1) : (256 + tiles - 1) / tiles;
   if (s > 8) s = 8;
   if (s > ksteps / 8) s = ksteps / 8;
   return s < 1 ? 1 : static_cast<int>(s);

@@ -665,8 +665,8 @@ inline bool thin_takes(const Launch& L) {
 // fewer for large weight matrices, where the float32 GEMV's FMAs per row
 // cost more than the GEMM's fixed prepass and decode. Measured with 4-bit
 // codes and float32 activations: K = N = 4096 at 12 rows 25.4 -> 20.4 us, at
-// 16 rows 32.0 -> 20.8; K = 4096, N = 14336 at 5 rows 54.4 -> 43.2, at 16
-// rows 110.9 -> 44.8; K = 2048, N = 5632 stays on the GEMV (16.5 against
+// 16 rows 32.0 -> 20.8; K = 4096, N = 14336 at 5 rows 54.4 -> 29.8, at 16
+// rows 110.9 -> 30.1; K = 2048, N = 5632 stays on the GEMV (16.5 against
 // 20.1 us at 16 rows); float16 activations at K = N = 4096, 12 rows: 8-bit
 // 22.3 -> 15.5, 2-bit 17.2 -> 13.1 us. Float16 4-bit (exact weights) keeps
 // 17: its dot GEMVs stay in binary16 arithmetic.
