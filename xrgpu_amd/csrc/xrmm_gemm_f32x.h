@@ -609,6 +609,10 @@ __global__ __launch_bounds__(NT, 1) void k_gemm_fx(Args a, int nct) {
   }
 }
 
+// Every split's partial is loaded before the first add (a loop of dependent
+// load-then-add pays the memory latency once per split).
+constexpr int kMaxSplits = 8;
+
 // Y = the splits' partials added in split order, then the bias, rounded once
 // (element i of [M][NT]: the projection of its column). With Yact (Mlp: gate
 // and up of one N side by side), element i of [M][N] is act(gate) * up of
@@ -621,11 +625,19 @@ __global__ __launch_bounds__(256) void k_fx_combine(Args a) {
     const int N = a.pr[0].N;
     if (i >= static_cast<int64_t>(a.M) * N) return;
     const int64_t m = i / N, c = i % N, ig = m * a.NT + c, iu = ig + N;
-    float g = a.part[ig], u = a.part[iu];
-    for (int s = 1; s < a.splits; ++s) {
-      g += a.part[s * MN + ig];
-      u += a.part[s * MN + iu];
+    float gv[kMaxSplits], uv[kMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) {
+      gv[s] = s < a.splits ? a.part[s * MN + ig] : 0.f;
+      uv[s] = s < a.splits ? a.part[s * MN + iu] : 0.f;
     }
+    float g = gv[0], u = uv[0];
+#pragma unroll
+    for (int s = 1; s < kMaxSplits; ++s)
+      if (s < a.splits) {
+        g += gv[s];
+        u += uv[s];
+      }
     if (a.pr[0].bias) g += static_cast<float>(static_cast<const T*>(a.pr[0].bias)[c]);
     if (a.pr[1].bias) u += static_cast<float>(static_cast<const T*>(a.pr[1].bias)[c]);
     a.Yact[i] = activate(g, a.act) * u;
@@ -636,8 +648,13 @@ __global__ __launch_bounds__(256) void k_fx_combine(Args a) {
   const int pj = a.np > 1 && gc >= a.pr[1].cb ? (a.np > 2 && gc >= a.pr[2].cb ? 2 : 1) : 0;
   const Proj1 P = pick(a, pj);
   const int c = gc - P.cb;
-  float y = a.part[i];
-  for (int s = 1; s < a.splits; ++s) y += a.part[s * MN + i];
+  float v[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) v[s] = s < a.splits ? a.part[s * MN + i] : 0.f;
+  float y = v[0];
+#pragma unroll
+  for (int s = 1; s < kMaxSplits; ++s)
+    if (s < a.splits) y += v[s];
   if (P.bias) y += static_cast<float>(static_cast<const T*>(P.bias)[c]);
   static_cast<T*>(P.Y)[static_cast<int64_t>(m) * P.N + c] = static_cast<T>(y);
 }
